@@ -1,0 +1,249 @@
+"""Benchmark of the spiking decode hot path on one MI355X.
+
+Headline (the `value`): paged popcount decode attention, config 4 of the
+baseline -- batch 256, context lengths uniform in [4096, 32768], Hq=14 /
+Hkv=2, head_dim 64, T=4, block_size 16, shuffled physical blocks, spike density
+0.2 -- as achieved HBM GB/s over ALGORITHMIC bytes (each unique K/V byte once,
+plus q, output, block-table entries and lengths).  A "step" is one call of
+paged_spike_attn_decode over the whole batch (decode kernel + partition
+combine), inputs resident in HBM.
+
+Also reported: the density sweep {0.05, 0.2, 0.5} (runtime must be flat),
+config 3 (batch 64, ctx U[128,192], 24 layers -> attention time per decode
+step), config 2 (fused LIF + pack + cache write, 4096 tokens), and the CPU
+oracle timed on a bounded sample of config 4 on the host cores.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip-extras]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+T, HQ, HKV, D, BS = 4, 14, 2, 64, 16
+
+
+def make_attn_inputs(n_seqs, lo, hi, density, seed, dev, layers=1):
+    """Synthetic paged cache: Bernoulli(density) bits, shuffled blocks."""
+    from spikeinfer_amd.kernels import pack_spikes
+
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (n_seqs,), generator=g, dtype=torch.int32)
+    blocks_per = (lens + BS - 1) // BS
+    max_blocks = int(math.ceil(hi / BS))
+    total_blocks = int(blocks_per.sum()) + 1  # + pad block
+    perm = torch.randperm(total_blocks - 1, generator=g)
+    tables = torch.full((n_seqs, max_blocks), total_blocks - 1, dtype=torch.int32)
+    cur = 0
+    for i, nb in enumerate(blocks_per.tolist()):
+        tables[i, :nb] = perm[cur:cur + nb].int()
+        cur += nb
+    slots = total_blocks * BS
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    caches = []
+    chunk = 1 << 20
+    for _ in range(layers):
+        kv = []
+        for _ in range(2):
+            c = torch.empty((T, HKV, slots, 2), dtype=torch.int32, device=dev)
+            flat = c.view(-1, 2)
+            for s0 in range(0, flat.shape[0], chunk):
+                n = min(chunk, flat.shape[0] - s0)
+                bits = torch.rand((n, D), generator=gd, device=dev) < density
+                flat[s0:s0 + n] = pack_spikes(bits)
+            kv.append(c)
+        caches.append(kv)
+    q = pack_spikes(torch.rand((T, n_seqs, HQ, D), generator=gd, device=dev) < density)
+    return dict(q=q, caches=caches, tables=tables.to(dev), lens=lens.to(dev),
+                lens_cpu=lens, max_blocks=max_blocks)
+
+
+def attn_bytes(lens_cpu, out_elem_bytes):
+    n = lens_cpu.numel()
+    ctx = int(lens_cpu.sum())
+    kv = ctx * T * HKV * 2 * 8
+    q = n * T * HQ * 8
+    out = n * T * HQ * D * out_elem_bytes
+    table = int(((lens_cpu + BS - 1) // BS).sum()) * 4
+    return kv + q + out + table + 4 * n
+
+
+def time_calls(fn, steps, warmup, stream):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per call
+
+
+def bench_attention(inp, steps, warmup, dev, out_dtype=torch.float32):
+    from spikeinfer_amd.kernels import decode_attn_workspace_bytes, paged_spike_attn_decode
+
+    n = inp["lens"].numel()
+    out = torch.empty((T, n, HQ, D), device=dev, dtype=out_dtype)
+    ws = torch.empty(decode_attn_workspace_bytes(T, n, HQ, HKV, D, BS, inp["max_blocks"]) or 1,
+                     dtype=torch.uint8, device=dev)
+    layers = inp["caches"]
+
+    def step():
+        for k, v in layers:
+            paged_spike_attn_decode(inp["q"], k, v, inp["tables"], inp["lens"], D, BS, HQ, HKV,
+                                    out=out, workspace=ws)
+
+    ms = time_calls(step, steps, warmup, torch.cuda.current_stream(dev))
+    return ms, out
+
+
+def cpu_baseline(inp, dev, budget_s=15.0):
+    """C oracle (OpenMP) on a bounded sample of the same config-4 batch."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    threads = min(16, os.cpu_count() or 1)
+    orc.threads(threads)
+    k, v = inp["caches"][0]
+    kc, vc = k.cpu().numpy(), v.cpu().numpy()
+    q = inp["q"].cpu().numpy()
+    tables = inp["tables"].cpu().numpy()
+    lens = inp["lens_cpu"].numpy()
+    done_bytes, elapsed, n_done = 0, 0.0, 0
+    while n_done < len(lens) and elapsed < budget_s:
+        sl = slice(n_done, n_done + 4)
+        t0 = time.perf_counter()
+        orc.decode_attn(q[:, sl], kc, vc, tables[sl], lens[sl], D, BS, HQ, HKV)
+        elapsed += time.perf_counter() - t0
+        done_bytes += attn_bytes(torch.from_numpy(lens[sl]), 4)
+        n_done += lens[sl].size
+    return {
+        "value": round(done_bytes / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"first {n_done} of {len(lens)} config-4 sequences (ctx U[4096,32768], "
+                  f"p=0.2), C oracle float64 softmax, {elapsed:.1f} s",
+    }
+
+
+def bench_lif(steps, warmup, dev):
+    """Config 2: fused LIF + pack + cache write for q/k/v, dense gate mask."""
+    from spikeinfer_amd.kernels import lif_multistep, lif_pack_write
+
+    g = torch.Generator(device=dev).manual_seed(2000)
+    n_tok = 4096
+    xq = torch.randn((T, n_tok, HQ, D), generator=g, device=dev).bfloat16()
+    xk = torch.randn((T, n_tok, HKV, D), generator=g, device=dev).bfloat16()
+    xv = torch.randn((T, n_tok, HKV, D), generator=g, device=dev).bfloat16()
+    xg = torch.randn((T, n_tok, 4864), generator=g, device=dev).bfloat16()
+    beta = torch.full((D,), 0.9, device=dev)
+    th = torch.full((D,), 1.0, device=dev)
+    bg = torch.full((4864,), 0.9, device=dev)
+    tg = torch.full((4864,), 1.0, device=dev)
+    S = 16 * 257 * 2  # >= 257 blocks of 16, 4096 distinct random slots
+    slots = torch.randperm(S, device=dev)[:n_tok]
+    qbuf = torch.empty((T, n_tok, HQ, 2), dtype=torch.int32, device=dev)
+    kc = torch.zeros((T, HKV, S, 2), dtype=torch.int32, device=dev)
+    vc = torch.zeros_like(kc)
+
+    def qkv():
+        lif_pack_write(xq, beta, th, qbuf)
+        lif_pack_write(xk, beta, th, kc, slot_mapping=slots)
+        lif_pack_write(xv, beta, th, vc, slot_mapping=slots)
+
+    def gate():
+        lif_multistep(xg, bg, tg)
+
+    stream = torch.cuda.current_stream(dev)
+    ms_qkv = time_calls(qkv, steps, warmup, stream)
+    ms_gate = time_calls(gate, steps, warmup, stream)
+    bytes_qkv = T * n_tok * (HQ + 2 * HKV) * D * 2 + T * n_tok * (HQ + 2 * HKV) * 8 + 2 * 8 * n_tok
+    bytes_gate = T * n_tok * 4864 * 2 * 2
+    return {
+        "qkv_ms": round(ms_qkv, 4), "qkv_gbs": round(bytes_qkv / ms_qkv / 1e6, 1),
+        "gate_ms": round(ms_gate, 4), "gate_gbs": round(bytes_gate / ms_gate / 1e6, 1),
+        "total_gbs": round((bytes_qkv + bytes_gate) / (ms_qkv + ms_gate) / 1e6, 1),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--skip-extras", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every (sequence, kv head, t) unit is independent; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    print("config 4: generating inputs", file=sys.stderr, flush=True)
+    inp = make_attn_inputs(256, 4096, 32768, 0.2, 4000, dev)
+    ms, _ = bench_attention(inp, args.steps, args.warmup, dev)
+    nbytes = attn_bytes(inp["lens_cpu"], 4)
+    gbs = nbytes / ms / 1e6
+    extras = {}
+    if not args.skip_extras:
+        for p in (0.05, 0.5):
+            print(f"config 4 density {p}", file=sys.stderr, flush=True)
+            alt = make_attn_inputs(256, 4096, 32768, p, 4000, dev)
+            ms_p, _ = bench_attention(alt, args.steps, args.warmup, dev)
+            extras[f"density_{p}_gbs"] = round(nbytes / ms_p / 1e6, 1)
+            del alt
+        print("config 3", file=sys.stderr, flush=True)
+        c3 = make_attn_inputs(64, 128, 192, 0.2, 3000, dev, layers=24)
+        ms3, _ = bench_attention(c3, args.steps, args.warmup, dev, torch.bfloat16)
+        extras["config3_attn_us_per_step_24_layers"] = round(ms3 * 1000, 1)
+        extras["config3_attn_gbs"] = round(attn_bytes(c3["lens_cpu"], 2) * 24 / ms3 / 1e6, 1)
+        del c3
+        print("config 2", file=sys.stderr, flush=True)
+        extras["config2_lif"] = bench_lif(args.steps, args.warmup, dev)
+    print("cpu baseline", file=sys.stderr, flush=True)
+    cpu = cpu_baseline(inp, dev, args.cpu_budget)
+
+    line = {
+        "metric": "popcount decode attn achieved HBM GB/s (config 4: batch 256, ctx U[4096,32768])",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32-popcount+f32",
+        "data": "synthetic: Bernoulli(0.2) spike bits, shuffled block tables, seeded",
+        "config": {"workload": "config4_paged_popcount_decode_attn", "batch": 256,
+                   "ctx": "U[4096,32768]", "Hq": HQ, "Hkv": HKV, "head_dim": D, "T": T,
+                   "block_size": BS, "density": 0.2, "out_dtype": "f32",
+                   "algorithmic_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "extras": extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

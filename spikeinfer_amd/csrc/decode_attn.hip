@@ -1,0 +1,361 @@
+// Paged popcount decode attention for gfx950.
+//
+// Reference semantics: spikeinfer/kernels/spike_attention.py:67-150 (Triton
+// kernel) and :247-282 (SDPA oracle).  For every (sequence n, query head h,
+// timestep t) the output is softmax_j(popc(q & k_j) * scale) @ bits(v_j) over
+// the sequence's first seq_len positions, walked through its block table.
+//
+// MI355X design (this file: the general path, every head_dim <= 128 and GQA
+// ratio <= 16):
+//   * one workgroup per (partition of the context, t, kv head, sequence);
+//     it serves all n_rep query heads of the kv head, so each K/V byte is read
+//     from HBM once, not n_rep times;
+//   * scores are integers, so the softmax uses the fixed offset c_q =
+//     popc(q) (an upper bound of every count): weight(d) = exp(-d*scale) with
+//     d = popc(q & ~k) = c_q - count in [0, head_dim].  No running max, no
+//     rescaling, and partition partial sums combine by plain addition;
+//   * the 1 + head_dim weights live in an LDS table, so a score costs two
+//     bitwise ops and two v_bcnt per word plus one LDS read;
+//   * value side: lane = channel, v bit selects the weight, fixed summation
+//     order (bit-reproducible run to run).
+#include "common.hpp"
+
+namespace spk {
+
+constexpr int kAttnThreads = 256;   // 4 waves
+constexpr int kMaxRep = 16;
+
+struct AttnParams {
+  const uint32_t *q;
+  int64_t qs0, qs1, qs2;
+  const uint32_t *k;
+  int64_t ks0, ks1, ks2;
+  const uint32_t *v;
+  int64_t vs0, vs1, vs2;
+  int64_t num_slots;
+  const int32_t *bt;
+  int64_t bts0, bts1;
+  const int32_t *lens;
+  void *out;
+  int out_dtype;
+  int64_t os0, os1, os2, os3;
+  int T, N, Hq, Hkv, head_dim, bs_log2, nrep;
+  float scale;
+  int part_len;      // tokens per partition (multiple of 256 and of block size)
+  int num_parts;     // partitions per sequence at most
+  float *ws;         // [num_parts][T][N][Hq][head_dim + 1] partial sums
+};
+
+// Partition length: long contexts are split so the grid has enough
+// workgroups and no single workgroup walks a 32k-token context alone.
+inline int choose_part_len(int64_t units, int64_t ctx_max) {
+  int part = 4096;
+  // Small decode batches: shorten partitions (down to 512) until the grid
+  // holds about four workgroups per CU.
+  while (part > 512 && units * ((ctx_max + part - 1) / part) < 1024) part >>= 1;
+  return part;
+}
+
+template <int W>
+__device__ __forceinline__ int popc_andn(const uint32_t (&q)[W], const uint32_t (&k)[W]) {
+  int d = 0;
+#pragma unroll
+  for (int w = 0; w < W; ++w) d += __popc(q[w] & ~k[w]);
+  return d;
+}
+
+template <int W, int REP>
+__global__ __launch_bounds__(kAttnThreads) void decode_attn_general(AttnParams p) {
+  constexpr int CPL = (W + 1) / 2;  // channels per lane (64 lanes)
+  const int part = blockIdx.x;
+  const int t = blockIdx.y / p.Hkv;
+  const int kvh = blockIdx.y % p.Hkv;
+  const int n = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  const int len = p.lens[n];
+  const int nparts_seq = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
+  if (part >= nparts_seq) return;
+  const int start = part * p.part_len;
+  const int end = min(len, start + p.part_len);
+
+  __shared__ float wtab[129];
+  __shared__ float P[REP][kAttnThreads];
+  __shared__ uint32_t Vs[kAttnThreads][W];
+  __shared__ float red_l[4][REP];
+  __shared__ float red_acc[4][REP][CPL * 64];
+
+  const int hd = p.head_dim;
+  for (int d = tid; d <= hd; d += kAttnThreads) wtab[d] = expf(-static_cast<float>(d) * p.scale);
+
+  // Query words of the n_rep heads sharing this kv head (uniform per block).
+  uint32_t qw[REP][W];
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      qw[h][w] = 0;
+      if (h < p.nrep)
+        qw[h][w] = p.q[t * p.qs0 + n * p.qs1 + (kvh * p.nrep + h) * p.qs2 + w];
+    }
+  }
+
+  float acc[REP][CPL];
+  float lsum[REP];
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    lsum[h] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) acc[h][c] = 0.f;
+  }
+
+  const uint32_t *kbase = p.k + t * p.ks0 + kvh * p.ks1;
+  const uint32_t *vbase = p.v + t * p.vs0 + kvh * p.vs1;
+  const int bs_mask = (1 << p.bs_log2) - 1;
+  __syncthreads();
+
+  for (int c0 = start; c0 < end; c0 += kAttnThreads) {
+    // Phase 1: one token per thread -> n_rep weights and the v words in LDS.
+    const int j = c0 + tid;
+    uint32_t kw[W], vw[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) kw[w] = vw[w] = 0;
+    bool valid = j < end;
+    if (valid) {
+      const int phys = p.bt[n * p.bts0 + (j >> p.bs_log2) * p.bts1];
+      const int64_t slot = (static_cast<int64_t>(phys) << p.bs_log2) | (j & bs_mask);
+      valid = slot >= 0 && slot < p.num_slots;
+      if (valid) {
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          kw[w] = kbase[slot * p.ks2 + w];
+          vw[w] = vbase[slot * p.vs2 + w];
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+      const float pv = valid ? wtab[popc_andn<W>(qw[h], kw)] : 0.f;
+      P[h][tid] = pv;
+      lsum[h] += pv;
+    }
+#pragma unroll
+    for (int w = 0; w < W; ++w) Vs[tid][w] = valid ? vw[w] : 0u;
+    __syncthreads();
+
+    // Phase 2: each wave owns 64 of the chunk's tokens; lane = channel.
+    const int i0 = wave * 64;
+    const int i1 = min(i0 + 64, end - c0);
+    for (int i = i0; i < i1; ++i) {
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int ch = lane + 64 * c;
+        const uint32_t word = (ch >> 5) < W ? Vs[i][(ch >> 5) < W ? (ch >> 5) : 0] : 0u;
+        const bool bit = (word >> (ch & 31)) & 1u;
+#pragma unroll
+        for (int h = 0; h < REP; ++h) acc[h][c] += bit ? P[h][i] : 0.f;
+      }
+    }
+    __syncthreads();
+  }
+
+  // Reduce the four waves' partial sums in a fixed order.
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    float l = lsum[h];
+    for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+    if (lane == 0) red_l[wave][h] = l;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) red_acc[wave][h][lane + 64 * c] = acc[h][c];
+  }
+  __syncthreads();
+
+  const bool single = nparts_seq == 1;
+  for (int idx = tid; idx < p.nrep * hd; idx += kAttnThreads) {
+    const int h = idx / hd;
+    const int ch = idx % hd;
+    const float a = ((red_acc[0][h][ch] + red_acc[1][h][ch]) + red_acc[2][h][ch]) + red_acc[3][h][ch];
+    const float l = ((red_l[0][h] + red_l[1][h]) + red_l[2][h]) + red_l[3][h];
+    const int hq = kvh * p.nrep + h;
+    if (single) {
+      const float o = len <= 0 ? 0.f : a / l;
+      store_f32_as(p.out, t * p.os0 + n * p.os1 + hq * p.os2 + ch * p.os3, p.out_dtype, o);
+    } else {
+      float *dst = p.ws + ((((int64_t)part * p.T + t) * p.N + n) * p.Hq + hq) * (hd + 1);
+      dst[ch] = a;
+      if (ch == 0) dst[hd] = l;
+    }
+  }
+}
+
+// Sums the partitions of every split sequence (fixed order) and normalises.
+__global__ __launch_bounds__(128) void decode_attn_combine(AttnParams p) {
+  const int row = blockIdx.x;  // (t, n, hq)
+  const int hq = row % p.Hq;
+  const int n = (row / p.Hq) % p.N;
+  const int t = row / (p.Hq * p.N);
+  const int len = p.lens[n];
+  const int nparts = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
+  if (nparts <= 1) return;
+  const int hd = p.head_dim;
+  const int64_t stride_part = (int64_t)p.T * p.N * p.Hq * (hd + 1);
+  const float *src = p.ws + (((int64_t)t * p.N + n) * p.Hq + hq) * (hd + 1);
+  for (int ch = threadIdx.x; ch < hd; ch += blockDim.x) {
+    float a = 0.f, l = 0.f;
+    for (int q = 0; q < nparts; ++q) {
+      a += src[q * stride_part + ch];
+      l += src[q * stride_part + hd];
+    }
+    store_f32_as(p.out, t * p.os0 + n * p.os1 + hq * p.os2 + ch * p.os3, p.out_dtype, a / l);
+  }
+}
+
+// Integer scores popc(q & k) for every valid position (score-path check).
+template <int W>
+__global__ __launch_bounds__(256) void decode_scores_kernel(AttnParams p, int32_t *scores,
+                                                            int max_len) {
+  const int t = blockIdx.y / p.Hkv;
+  const int kvh = blockIdx.y % p.Hkv;
+  const int n = blockIdx.z;
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  const int len = p.lens[n];
+  if (j >= len || j >= max_len) return;
+  const int phys = p.bt[n * p.bts0 + (j >> p.bs_log2) * p.bts1];
+  const int64_t slot = (static_cast<int64_t>(phys) << p.bs_log2) | (j & ((1 << p.bs_log2) - 1));
+  if (slot < 0 || slot >= p.num_slots) return;
+  uint32_t kw[W];
+  for (int w = 0; w < W; ++w) kw[w] = p.k[t * p.ks0 + kvh * p.ks1 + slot * p.ks2 + w];
+  for (int h = 0; h < p.nrep; ++h) {
+    const int hq = kvh * p.nrep + h;
+    int c = 0;
+    for (int w = 0; w < W; ++w) c += __popc(p.q[t * p.qs0 + n * p.qs1 + hq * p.qs2 + w] & kw[w]);
+    scores[(((int64_t)t * p.N + n) * p.Hq + hq) * max_len + j] = c;
+  }
+}
+
+// Launch of the general path; REP is the smallest instantiated bound >= nrep.
+template <int W>
+static void launch_general(const AttnParams &p, dim3 grid, hipStream_t s) {
+  if (p.nrep <= 1) decode_attn_general<W, 1><<<grid, kAttnThreads, 0, s>>>(p);
+  else if (p.nrep <= 2) decode_attn_general<W, 2><<<grid, kAttnThreads, 0, s>>>(p);
+  else if (p.nrep <= 4) decode_attn_general<W, 4><<<grid, kAttnThreads, 0, s>>>(p);
+  else if (p.nrep <= 8) decode_attn_general<W, 8><<<grid, kAttnThreads, 0, s>>>(p);
+  else decode_attn_general<W, 16><<<grid, kAttnThreads, 0, s>>>(p);
+}
+
+}  // namespace spk
+
+using namespace spk;
+
+static int check_common(int T, int N, int Hq, int Hkv, int head_dim, int block_size) {
+  if (T <= 0 || N < 0 || Hq <= 0 || Hkv <= 0)
+    return fail(SPK_EINVAL, "bad sizes T=%d N=%d Hq=%d Hkv=%d", T, N, Hq, Hkv);
+  if (Hq % Hkv != 0) return fail(SPK_EINVAL, "Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
+  if (Hq / Hkv > kMaxRep)
+    return fail(SPK_EUNSUPPORTED, "GQA ratio %d exceeds %d", Hq / Hkv, kMaxRep);
+  if (head_dim <= 0 || head_dim > 128)
+    return fail(SPK_EUNSUPPORTED, "head_dim=%d (supported: 1..128)", head_dim);
+  if (!is_pow2(block_size))
+    return fail(SPK_EINVAL, "block_size=%d is not a power of two", block_size);
+  return SPK_OK;
+}
+
+extern "C" size_t spk_decode_attn_workspace_bytes(int T, int N, int Hq, int Hkv, int head_dim,
+                                                  int block_size, int max_blocks) {
+  if (T <= 0 || N <= 0 || Hkv <= 0 || max_blocks <= 0 || block_size <= 0) return 0;
+  const int64_t ctx_max = (int64_t)max_blocks * block_size;
+  const int part = choose_part_len((int64_t)N * T * Hkv, ctx_max);
+  const int64_t nparts = (ctx_max + part - 1) / part;
+  if (nparts <= 1) return 0;
+  return (size_t)nparts * T * N * Hq * (head_dim + 1) * sizeof(float);
+}
+
+extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], const int32_t *k_cache,
+                               const int64_t k_strides[4], const int32_t *v_cache,
+                               const int64_t v_strides[4], int64_t num_slots,
+                               const int32_t *block_tables, int64_t bt_stride0, int64_t bt_stride1,
+                               const int32_t *seq_lens, void *out, int out_dtype,
+                               const int64_t out_strides[4], int T, int N, int Hq, int Hkv,
+                               int head_dim, int block_size, int max_blocks, float scale,
+                               void *workspace, size_t workspace_bytes, void *stream) {
+  int rc = check_common(T, N, Hq, Hkv, head_dim, block_size);
+  if (rc) return rc;
+  if (!valid_float_dtype(out_dtype)) return fail(SPK_EINVAL, "out dtype %d not a float type", out_dtype);
+  if (q_strides[3] != 1 || k_strides[3] != 1 || v_strides[3] != 1)
+    return fail(SPK_EINVAL, "packed word axis must be contiguous");
+  if (!(scale > 0.f) || scale * head_dim > 80.f)
+    return fail(SPK_EINVAL, "scale=%g outside (0, 80/head_dim]", (double)scale);
+  if (max_blocks <= 0) return fail(SPK_EINVAL, "max_blocks=%d", max_blocks);
+  if (N == 0) return SPK_OK;
+  const size_t need = spk_decode_attn_workspace_bytes(T, N, Hq, Hkv, head_dim, block_size, max_blocks);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(SPK_EINVAL, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+
+  AttnParams p{};
+  p.q = reinterpret_cast<const uint32_t *>(q);
+  p.qs0 = q_strides[0]; p.qs1 = q_strides[1]; p.qs2 = q_strides[2];
+  p.k = reinterpret_cast<const uint32_t *>(k_cache);
+  p.ks0 = k_strides[0]; p.ks1 = k_strides[1]; p.ks2 = k_strides[2];
+  p.v = reinterpret_cast<const uint32_t *>(v_cache);
+  p.vs0 = v_strides[0]; p.vs1 = v_strides[1]; p.vs2 = v_strides[2];
+  p.num_slots = num_slots;
+  p.bt = block_tables; p.bts0 = bt_stride0; p.bts1 = bt_stride1;
+  p.lens = seq_lens;
+  p.out = out; p.out_dtype = out_dtype;
+  p.os0 = out_strides[0]; p.os1 = out_strides[1]; p.os2 = out_strides[2]; p.os3 = out_strides[3];
+  p.T = T; p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.head_dim = head_dim;
+  p.bs_log2 = ilog2(block_size); p.nrep = Hq / Hkv; p.scale = scale;
+  const int64_t ctx_max = (int64_t)max_blocks * block_size;
+  p.part_len = choose_part_len((int64_t)N * T * Hkv, ctx_max);
+  p.num_parts = (int)((ctx_max + p.part_len - 1) / p.part_len);
+  p.ws = static_cast<float *>(workspace);
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 grid(p.num_parts, T * Hkv, N);
+  const int W = (head_dim + 31) / 32;
+  switch (W) {
+    case 1: launch_general<1>(p, grid, s); break;
+    case 2: launch_general<2>(p, grid, s); break;
+    case 3: launch_general<3>(p, grid, s); break;
+    default: launch_general<4>(p, grid, s); break;
+  }
+  if ((rc = check_launch("decode_attn"))) return rc;
+  if (p.num_parts > 1) {
+    decode_attn_combine<<<dim3(T * N * Hq), 128, 0, s>>>(p);
+    if ((rc = check_launch("decode_attn_combine"))) return rc;
+  }
+  return SPK_OK;
+}
+
+extern "C" int spk_decode_scores(const int32_t *q, const int64_t q_strides[4],
+                                 const int32_t *k_cache, const int64_t k_strides[4],
+                                 int64_t num_slots, const int32_t *block_tables,
+                                 int64_t bt_stride0, int64_t bt_stride1, const int32_t *seq_lens,
+                                 int32_t *scores, int max_len, int T, int N, int Hq, int Hkv,
+                                 int head_dim, int block_size, void *stream) {
+  int rc = check_common(T, N, Hq, Hkv, head_dim, block_size);
+  if (rc) return rc;
+  if (q_strides[3] != 1 || k_strides[3] != 1) return fail(SPK_EINVAL, "packed word axis must be contiguous");
+  if (max_len <= 0 || N == 0) return SPK_OK;
+  AttnParams p{};
+  p.q = reinterpret_cast<const uint32_t *>(q);
+  p.qs0 = q_strides[0]; p.qs1 = q_strides[1]; p.qs2 = q_strides[2];
+  p.k = reinterpret_cast<const uint32_t *>(k_cache);
+  p.ks0 = k_strides[0]; p.ks1 = k_strides[1]; p.ks2 = k_strides[2];
+  p.num_slots = num_slots;
+  p.bt = block_tables; p.bts0 = bt_stride0; p.bts1 = bt_stride1;
+  p.lens = seq_lens;
+  p.T = T; p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.head_dim = head_dim;
+  p.bs_log2 = ilog2(block_size); p.nrep = Hq / Hkv;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 grid((max_len + 255) / 256, T * Hkv, N);
+  switch ((head_dim + 31) / 32) {
+    case 1: decode_scores_kernel<1><<<grid, 256, 0, s>>>(p, scores, max_len); break;
+    case 2: decode_scores_kernel<2><<<grid, 256, 0, s>>>(p, scores, max_len); break;
+    case 3: decode_scores_kernel<3><<<grid, 256, 0, s>>>(p, scores, max_len); break;
+    default: decode_scores_kernel<4><<<grid, 256, 0, s>>>(p, scores, max_len); break;
+  }
+  return check_launch("decode_scores");
+}

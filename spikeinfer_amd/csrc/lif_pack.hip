@@ -1,0 +1,219 @@
+// LIF neuron, bit-packing and the fused LIF -> pack -> paged-cache scatter.
+//
+// Reference semantics: spikeinfer/kernels/lif_triton.py:13-28, 96-105 (the
+// recurrence, evaluated in fp32 with separate multiply and add roundings:
+// `enable_fp_fusion=False` at :222-227) and spikeinfer/kernels/packing.py:16-23
+// (bit i of int32 word w is channel 32*w + i).
+//
+// This file is compiled with -ffp-contract=off: `beta*u + x` must round twice,
+// exactly as PyTorch eager does, or a membrane that lands within an ulp of the
+// threshold flips its spike.
+#include "common.hpp"
+
+namespace spk {
+
+struct LifParams {
+  const void *x;
+  int x_dtype;
+  const void *beta;
+  const void *th;
+  int param_dtype;
+  int T;
+};
+
+// One LIF step on the fp32 membrane; returns the spike.  The delayed reset
+// uses the membrane of the previous step (lif_triton.py:98-101).
+__device__ __forceinline__ bool lif_step(float &u, float cur, float beta, float th) {
+  const float r = (u - th > 0.f) ? 1.f : 0.f;
+  u = (beta * u + cur) - r * th;
+  return u - th > 0.f;
+}
+
+__device__ __forceinline__ float clamp01(float b) { return fminf(fmaxf(b, 0.f), 1.f); }
+
+// ---- dense LIF: [T, M, N] -> spikes [T, M, N] -----------------------------
+__global__ __launch_bounds__(256) void lif_dense_kernel(LifParams p, int64_t xs0, int64_t xs1,
+                                                        int64_t xs2, const float *mem0,
+                                                        void *spikes, int spike_dtype,
+                                                        float *u_out, int64_t M, int N) {
+  const int64_t total = M * N;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = e / N;
+    const int c = static_cast<int>(e - m * N);
+    const float beta = clamp01(load_as_f32(p.beta, c, p.param_dtype));
+    const float th = load_as_f32(p.th, c, p.param_dtype);
+    float u = mem0 ? mem0[e] : 0.f;
+    const int64_t xoff = m * xs1 + c * xs2;
+    for (int t = 0; t < p.T; ++t) {
+      const bool s = lif_step(u, load_as_f32(p.x, t * xs0 + xoff, p.x_dtype), beta, th);
+      store_spike(spikes, t * total + e, spike_dtype, s);
+    }
+    if (u_out) u_out[e] = u;
+  }
+}
+
+// ---- fused LIF + pack + scatter --------------------------------------------
+// One wave per (token, head) row; lane = channel (CPL chunks of 64 channels).
+// Per timestep the wave's 64 spikes become one 64-bit word by __ballot, and
+// lanes 0..W-1 store the int32 words straight to the packed buffer or to the
+// cache slot the token maps to.
+template <int CPL>
+__global__ __launch_bounds__(256) void lif_pack_kernel(LifParams p, int64_t xs0, int64_t xs1,
+                                                       int64_t xs2, int64_t xs3, uint32_t *packed,
+                                                       int64_t ps0, int64_t ps1, int64_t ps2,
+                                                       const int64_t *slots, int64_t num_slots,
+                                                       void *spikes, int spike_dtype,
+                                                       int64_t n_tok, int H, int D) {
+  const int lane = threadIdx.x & 63;
+  const int W = (D + 31) >> 5;
+  const int64_t rows = n_tok * H;
+  const int64_t waves_total = (int64_t)gridDim.x * (blockDim.x >> 6);
+  float beta[CPL], th[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = lane + 64 * c;
+    beta[c] = ch < D ? clamp01(load_as_f32(p.beta, ch, p.param_dtype)) : 0.f;
+    th[c] = ch < D ? load_as_f32(p.th, ch, p.param_dtype) : 1.f;
+  }
+  for (int64_t row = blockIdx.x * (int64_t)(blockDim.x >> 6) + (threadIdx.x >> 6); row < rows;
+       row += waves_total) {
+    const int64_t tok = row / H;
+    const int h = static_cast<int>(row - tok * H);
+    int64_t dst = 0;
+    bool write = true;
+    if (slots) {
+      const int64_t slot = slots[tok];
+      write = slot >= 0 && slot < num_slots;
+      dst = h * ps1 + slot * ps2;
+    } else {
+      dst = tok * ps1 + h * ps2;
+    }
+    float u[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) u[c] = 0.f;
+    for (int t = 0; t < p.T; ++t) {
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int ch = lane + 64 * c;
+        bool s = false;
+        if (ch < D) {
+          const float cur = load_as_f32(p.x, t * xs0 + tok * xs1 + h * xs2 + ch * xs3, p.x_dtype);
+          s = lif_step(u[c], cur, beta[c], th[c]);
+          if (spikes)
+            store_spike(spikes, ((t * n_tok + tok) * H + h) * (int64_t)D + ch, spike_dtype, s);
+        }
+        const uint64_t mask = __ballot(s);
+        // Lanes 0 and 1 store the two int32 words of this 64-channel chunk.
+        const int w = 2 * c + lane;
+        if (write && lane < 2 && w < W)
+          packed[t * ps0 + dst + w] = static_cast<uint32_t>(mask >> (32 * lane));
+      }
+    }
+  }
+}
+
+// ---- pack / unpack ---------------------------------------------------------
+// One wave per row; each 64-channel chunk is one __ballot.
+__global__ __launch_bounds__(256) void pack_kernel(const void *x, int x_dtype, int64_t row_stride,
+                                                   uint32_t *out, int64_t rows, int C) {
+  const int lane = threadIdx.x & 63;
+  const int W = (C + 31) >> 5;
+  const int64_t waves_total = (int64_t)gridDim.x * (blockDim.x >> 6);
+  for (int64_t row = blockIdx.x * (int64_t)(blockDim.x >> 6) + (threadIdx.x >> 6); row < rows;
+       row += waves_total) {
+    for (int c0 = 0; c0 < C; c0 += 64) {
+      const int ch = c0 + lane;
+      const bool s = ch < C && load_nonzero(x, row * row_stride + ch, x_dtype);
+      const uint64_t mask = __ballot(s);
+      const int w = (c0 >> 5) + lane;
+      if (lane < 2 && w < W) out[row * W + w] = static_cast<uint32_t>(mask >> (32 * lane));
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void unpack_kernel(const uint32_t *words, int64_t rows, int C,
+                                                     void *out, int out_dtype) {
+  const int W = (C + 31) >> 5;
+  const int64_t total = rows * C;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / C;
+    const int c = static_cast<int>(e - r * C);
+    const bool s = (words[r * W + (c >> 5)] >> (c & 31)) & 1u;
+    store_spike(out, e, out_dtype, s);
+  }
+}
+
+inline unsigned grid_for(int64_t items, int per_block) {
+  int64_t g = (items + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > 65536) g = 65536;  // grid-stride loops cover the rest
+  return static_cast<unsigned>(g);
+}
+
+}  // namespace spk
+
+using namespace spk;
+
+extern "C" int spk_lif_multistep(const void *x, int x_dtype, const int64_t x_strides[3],
+                                 const void *beta, const void *threshold, int param_dtype,
+                                 const float *mem0, void *spikes, int spike_dtype, float *u_out,
+                                 int T, int64_t M, int N, void *stream) {
+  if (T <= 0 || M < 0 || N <= 0) return fail(SPK_EINVAL, "bad sizes T=%d M=%lld N=%d", T, (long long)M, N);
+  if (!valid_float_dtype(x_dtype) || !valid_float_dtype(param_dtype) || !valid_any_dtype(spike_dtype))
+    return fail(SPK_EINVAL, "unsupported dtype (x %d, params %d, spikes %d)", x_dtype, param_dtype, spike_dtype);
+  if (M == 0) return SPK_OK;
+  LifParams p{x, x_dtype, beta, threshold, param_dtype, T};
+  lif_dense_kernel<<<grid_for(M * N, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      p, x_strides[0], x_strides[1], x_strides[2], mem0, spikes, spike_dtype, u_out, M, N);
+  return check_launch("lif_multistep");
+}
+
+extern "C" int spk_lif_pack_write(const void *x, int x_dtype, const int64_t x_strides[4],
+                                  const void *beta, const void *threshold, int param_dtype,
+                                  int32_t *packed, const int64_t packed_strides[3],
+                                  const int64_t *slot_mapping, int64_t num_slots, void *spikes,
+                                  int spike_dtype, int T, int64_t n_tok, int H, int D,
+                                  void *stream) {
+  if (T <= 0 || n_tok < 0 || H <= 0 || D <= 0)
+    return fail(SPK_EINVAL, "bad sizes T=%d n_tok=%lld H=%d D=%d", T, (long long)n_tok, H, D);
+  if (D > 128) return fail(SPK_EUNSUPPORTED, "fused LIF-pack supports D <= 128, got %d", D);
+  if (!valid_float_dtype(x_dtype) || !valid_float_dtype(param_dtype) ||
+      (spikes && !valid_any_dtype(spike_dtype)))
+    return fail(SPK_EINVAL, "unsupported dtype (x %d, params %d, spikes %d)", x_dtype, param_dtype, spike_dtype);
+  if (n_tok == 0) return SPK_OK;
+  LifParams p{x, x_dtype, beta, threshold, param_dtype, T};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = grid_for(n_tok * H, 4);
+  uint32_t *pk = reinterpret_cast<uint32_t *>(packed);
+  if (D <= 64)
+    lif_pack_kernel<1><<<grid, 256, 0, s>>>(p, x_strides[0], x_strides[1], x_strides[2], x_strides[3], pk,
+                                            packed_strides[0], packed_strides[1], packed_strides[2],
+                                            slot_mapping, num_slots, spikes, spike_dtype, n_tok, H, D);
+  else
+    lif_pack_kernel<2><<<grid, 256, 0, s>>>(p, x_strides[0], x_strides[1], x_strides[2], x_strides[3], pk,
+                                            packed_strides[0], packed_strides[1], packed_strides[2],
+                                            slot_mapping, num_slots, spikes, spike_dtype, n_tok, H, D);
+  return check_launch("lif_pack_write");
+}
+
+extern "C" int spk_pack(const void *x, int x_dtype, int64_t x_row_stride, int32_t *out, int64_t rows,
+                        int C, void *stream) {
+  if (rows < 0 || C <= 0) return fail(SPK_EINVAL, "bad sizes rows=%lld C=%d", (long long)rows, C);
+  if (!valid_any_dtype(x_dtype)) return fail(SPK_EINVAL, "unsupported dtype %d", x_dtype);
+  if (rows == 0) return SPK_OK;
+  pack_kernel<<<grid_for(rows, 4), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      x, x_dtype, x_row_stride, reinterpret_cast<uint32_t *>(out), rows, C);
+  return check_launch("pack");
+}
+
+extern "C" int spk_unpack(const int32_t *words, int64_t rows, int C, void *out, int out_dtype,
+                          void *stream) {
+  if (rows < 0 || C <= 0) return fail(SPK_EINVAL, "bad sizes rows=%lld C=%d", (long long)rows, C);
+  if (!valid_any_dtype(out_dtype)) return fail(SPK_EINVAL, "unsupported dtype %d", out_dtype);
+  if (rows == 0) return SPK_OK;
+  unpack_kernel<<<grid_for(rows * C, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      reinterpret_cast<const uint32_t *>(words), rows, C, out, out_dtype);
+  return check_launch("unpack");
+}

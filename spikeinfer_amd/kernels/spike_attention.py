@@ -1,0 +1,171 @@
+"""Paged popcount decode attention on gfx950 (drop-in for
+spikeinfer/kernels/spike_attention.py:153-244).
+
+The HIP kernel serves all ``num_q_heads // num_kv_heads`` query heads of a KV
+head from one read of the KV blocks, scores with ``v_bcnt``, and uses the fixed
+softmax offset ``popcount(q)`` (an upper bound of every integer score), so long
+contexts split into partitions whose partial sums simply add.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+from .packing import packed_width, unpack_spikes
+
+
+def _as_int32(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.int32 else t.to(torch.int32)
+
+
+def _check_packed(name: str, t: torch.Tensor) -> None:
+    if t.dtype != torch.int32:
+        raise ValueError(f"{name} must be int32 packed words, got {t.dtype}")
+    if t.ndim != 4 or t.stride(-1) != 1:
+        raise ValueError(f"{name} must be 4-D with a contiguous word axis")
+
+
+def decode_attn_workspace_bytes(
+    T: int, n_seqs: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+    block_size: int, max_blocks: int,
+) -> int:
+    """Scratch bytes :func:`paged_spike_attn_decode` needs for this shape."""
+    return int(
+        _lib.load().spk_decode_attn_workspace_bytes(
+            T, n_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks
+        )
+    )
+
+
+def paged_spike_attn_decode(
+    q_packed: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    head_dim: int,
+    block_size: int,
+    num_q_heads: int,
+    num_kv_heads: int,
+    out: torch.Tensor | None = None,
+    dtype: torch.dtype = torch.float32,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One decode step of attention against the paged spike cache.
+
+    Same contract as the reference (spike_attention.py:153-189): ``q_packed``
+    ``int32 [T, N, H_q, W]``, caches ``int32 [T, H_kv, num_slots, W]``,
+    ``block_tables int32 [N, max_blocks]``, ``seq_lens int32 [N]`` including
+    the token being decoded; ``out`` optional ``[T, N, H_q, head_dim]`` (needed
+    for graph capture).  ``workspace`` optionally supplies the partition
+    scratch (``uint8``, at least :func:`decode_attn_workspace_bytes`); by
+    default it comes from torch's caching allocator, which is capture-safe.
+    """
+    T, n_seqs, n_heads, words = q_packed.shape
+    if words != packed_width(head_dim):
+        raise ValueError(f"q has {words} words, expected {packed_width(head_dim)}")
+    if n_heads != num_q_heads:
+        raise ValueError(f"q has {n_heads} heads, expected {num_q_heads}")
+    dev = _lib.require_gpu(q_packed, k_cache, v_cache, block_tables, seq_lens, out)
+    _check_packed("q_packed", q_packed)
+    _check_packed("k_cache", k_cache)
+    _check_packed("v_cache", v_cache)
+    if k_cache.shape != v_cache.shape:
+        raise ValueError(f"k/v cache shapes differ: {tuple(k_cache.shape)} vs {tuple(v_cache.shape)}")
+    if k_cache.shape[1] != num_kv_heads or k_cache.shape[0] != T or k_cache.shape[3] != words:
+        raise ValueError(
+            f"cache shape {tuple(k_cache.shape)} does not match T={T}, H_kv={num_kv_heads}, W={words}"
+        )
+    block_tables = _as_int32(block_tables)
+    seq_lens = _as_int32(seq_lens).contiguous()
+    if block_tables.ndim != 2 or block_tables.shape[0] < n_seqs or seq_lens.numel() < n_seqs:
+        raise ValueError("block_tables must be [N, max_blocks] and seq_lens [N]")
+
+    if out is None:
+        out = torch.empty((T, n_seqs, n_heads, head_dim), device=dev, dtype=dtype)
+    elif tuple(out.shape) != (T, n_seqs, n_heads, head_dim):
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected {(T, n_seqs, n_heads, head_dim)}")
+    if n_seqs == 0:
+        return out
+
+    max_blocks = block_tables.shape[1]
+    need = decode_attn_workspace_bytes(
+        T, n_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks
+    )
+    if need:
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        elif workspace.numel() * workspace.element_size() < need:
+            raise ValueError(f"workspace holds {workspace.nbytes} bytes, need {need}")
+    ws_ptr = workspace.data_ptr() if (need and workspace is not None) else None
+
+    _lib.check(
+        _lib.load().spk_decode_attn(
+            q_packed.data_ptr(), _lib.strides(q_packed),
+            k_cache.data_ptr(), _lib.strides(k_cache),
+            v_cache.data_ptr(), _lib.strides(v_cache), k_cache.shape[2],
+            block_tables.data_ptr(), block_tables.stride(0), block_tables.stride(1),
+            seq_lens.data_ptr(), out.data_ptr(), _lib.dtype_code(out.dtype), _lib.strides(out),
+            T, n_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks,
+            1.0 / math.sqrt(head_dim), ws_ptr, need, _lib.stream_of(dev),
+        ),
+        "paged_spike_attn_decode",
+    )
+    return out
+
+
+def paged_spike_attn_scores(
+    q_packed: torch.Tensor,
+    k_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    head_dim: int,
+    block_size: int,
+    num_q_heads: int,
+    num_kv_heads: int,
+    max_len: int,
+) -> torch.Tensor:
+    """Integer scores ``popcount(q & k)`` as ``int32 [T, N, H_q, max_len]``
+    (positions at or past ``seq_len`` hold -1), through the same block-table
+    walk as the decode kernel.  Exposed to check the score path bit-exactly.
+    """
+    T, n_seqs, n_heads, words = q_packed.shape
+    if words != packed_width(head_dim) or n_heads != num_q_heads:
+        raise ValueError("q_packed does not match head_dim / num_q_heads")
+    dev = _lib.require_gpu(q_packed, k_cache, block_tables, seq_lens)
+    _check_packed("q_packed", q_packed)
+    _check_packed("k_cache", k_cache)
+    block_tables = _as_int32(block_tables)
+    seq_lens = _as_int32(seq_lens).contiguous()
+    scores = torch.full((T, n_seqs, n_heads, max_len), -1, dtype=torch.int32, device=dev)
+    _lib.check(
+        _lib.load().spk_decode_scores(
+            q_packed.data_ptr(), _lib.strides(q_packed), k_cache.data_ptr(), _lib.strides(k_cache),
+            k_cache.shape[2], block_tables.data_ptr(), block_tables.stride(0),
+            block_tables.stride(1), seq_lens.data_ptr(), scores.data_ptr(), max_len,
+            T, n_seqs, num_q_heads, num_kv_heads, head_dim, block_size, _lib.stream_of(dev),
+        ),
+        "paged_spike_attn_scores",
+    )
+    return scores
+
+
+def gather_kv_unpacked(
+    cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_len: int,
+    head_dim: int,
+    block_size: int,
+    dtype: torch.dtype,
+) -> torch.Tensor:
+    """One sequence's cached spikes as dense ``[T, H_kv, S, D]`` (prefill
+    reader, spike_attention.py:224-244): slot gather, then the HIP unpack."""
+    n_blocks = (seq_len + block_size - 1) // block_size
+    slots = (
+        block_table[:n_blocks, None].to(torch.int64) * block_size
+        + torch.arange(block_size, device=cache.device)[None, :]
+    ).reshape(-1)[:seq_len]
+    words = cache.index_select(2, slots)
+    return unpack_spikes(words, head_dim, dtype)

@@ -1,0 +1,185 @@
+"""HIP paged popcount decode attention vs the CPU oracle (restates
+tests/test_spike_attention.py and tests/test_cpu_backend.py of the reference).
+
+Tolerances: fp32 output max-abs 1e-3 (the stated bar) and, tighter, the
+reference test's own relative bound 1e-5 (tests/test_spike_attention.py:28);
+bf16 output within one bf16 rounding of the fp32 result; scores bit-exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from cases import attn_case, oracle_attn
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+ABS_TOL = 1e-3
+REL_TOL = 1e-5
+
+
+def _to_dev(case, dev):
+    return dict(
+        q_packed=torch.from_numpy(case["q"]).to(dev),
+        k_cache=torch.from_numpy(case["k"]).to(dev),
+        v_cache=torch.from_numpy(case["v"]).to(dev),
+        block_tables=torch.from_numpy(case["tables"]).to(dev),
+        seq_lens=torch.from_numpy(case["lens"]).to(dev),
+        head_dim=case["head_dim"], block_size=case["block_size"],
+        num_q_heads=case["num_q_heads"], num_kv_heads=case["num_kv_heads"],
+    )
+
+
+def _check(got, want, ctx=""):
+    got = got.float().cpu().numpy().astype(np.float64)
+    assert np.isfinite(got).all(), f"non-finite output {ctx}"
+    err = np.abs(got - want).max()
+    assert err <= ABS_TOL, f"max-abs {err:.2e} > {ABS_TOL} {ctx}"
+    rel = err / max(np.abs(want).max(), 1e-6)
+    assert rel < REL_TOL, f"relative {rel:.2e} > {REL_TOL} {ctx}"
+
+
+def _run(case, gpu, **kw):
+    from spikeinfer_amd.kernels import paged_spike_attn_decode
+
+    print(f"attn case lens={case['lens'].tolist()[:8]} bs={case['block_size']} "
+          f"H={case['num_q_heads']}/{case['num_kv_heads']} D={case['head_dim']}", flush=True)
+    out = paged_spike_attn_decode(**_to_dev(case, gpu), **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("block_size", [16, 32, 64])
+@pytest.mark.parametrize("seq_lens", [[1], [7], [32], [33], [128], [1, 5, 40, 97], [64] * 8])
+def test_matches_oracle(block_size, seq_lens, gpu):
+    case = attn_case(seq_lens, block_size=block_size, seed=block_size)
+    _check(_run(case, gpu), oracle_attn(case), f"bs={block_size} lens={seq_lens}")
+
+
+@pytest.mark.parametrize("T", [1, 2, 4, 8])
+def test_across_timesteps(T, gpu):
+    case = attn_case([5, 61], block_size=32, T=T, seed=T)
+    _check(_run(case, gpu), oracle_attn(case), f"T={T}")
+
+
+@pytest.mark.parametrize("q_heads,kv_heads", [(14, 2), (4, 4), (8, 1), (16, 8), (16, 1), (6, 2)])
+def test_grouped_query_attention(q_heads, kv_heads, gpu):
+    case = attn_case([48, 19], block_size=32, q_heads=q_heads, kv_heads=kv_heads, seed=q_heads)
+    _check(_run(case, gpu), oracle_attn(case), f"GQA {q_heads}/{kv_heads}")
+
+
+@pytest.mark.parametrize("head_dim", [32, 64, 96, 128, 40])
+def test_head_dims(head_dim, gpu):
+    case = attn_case([10, 33, 50], head_dim=head_dim, q_heads=4, kv_heads=2, seed=head_dim)
+    _check(_run(case, gpu), oracle_attn(case), f"head_dim={head_dim}")
+
+
+def test_all_zero_query_is_mean_of_values(gpu):
+    case = attn_case([40, 17], block_size=32, seed=3)
+    case["q"][:] = 0
+    _check(_run(case, gpu), oracle_attn(case), "zero query")
+
+
+def test_only_the_sequence_own_blocks_are_read(gpu):
+    case = attn_case([50], block_size=32, seed=5, extra_blocks=14)
+    before = _run(case, gpu).clone()
+    owned = set(case["tables"][0, :2].tolist())
+    for b in range(case["k"].shape[2] // 32):
+        if b not in owned:
+            case["k"][:, :, b * 32:(b + 1) * 32] = -1
+            case["v"][:, :, b * 32:(b + 1) * 32] = -1
+    assert torch.equal(before, _run(case, gpu)), "attention read outside the sequence's blocks"
+
+
+def test_padding_tail_of_the_last_block_is_ignored(gpu):
+    case = attn_case([33], block_size=32, seed=7)
+    before = _run(case, gpu).clone()
+    last = case["tables"][0, 1]
+    case["k"][:, :, last * 32 + 1:(last + 1) * 32] = -1
+    case["v"][:, :, last * 32 + 1:(last + 1) * 32] = -1
+    assert torch.equal(before, _run(case, gpu)), "attention read past seq_len"
+
+
+@pytest.mark.parametrize("lens", [[5000, 9000, 17, 8192], [20000]])
+def test_long_context_split_partitions(lens, gpu):
+    """Contexts longer than one partition take the split + combine path."""
+    case = attn_case(lens, block_size=16, T=2, density=0.2, q_density=0.2, seed=11)
+    _check(_run(case, gpu), oracle_attn(case), f"long lens={lens}")
+
+
+def test_bf16_output_within_bf16_rounding(gpu):
+    case = attn_case([1, 5, 40, 97, 300], block_size=16, seed=13)
+    got = _run(case, gpu, dtype=torch.bfloat16)
+    assert got.dtype == torch.bfloat16
+    want = torch.from_numpy(oracle_attn(case)).float()
+    # one bf16 rounding of the exact value: |err| <= 2^-8 * |x| (half-ulp, rel)
+    err = (got.float().cpu() - want).abs()
+    assert (err <= want.abs() * 2.0 ** -8 + 1e-6).all()
+
+
+def test_fp16_output(gpu):
+    case = attn_case([3, 70], block_size=16, seed=17)
+    got = _run(case, gpu, dtype=torch.float16).float().cpu().numpy()
+    np.testing.assert_allclose(got, oracle_attn(case), atol=1e-3)
+
+
+def test_preallocated_strided_out(gpu):
+    """out may be a strided view (the reference passes out[:, :n_dec])."""
+    case = attn_case([9, 30], seed=19)
+    big = torch.full((4, 5, 14, 64), 7.0, device=gpu)
+    _run(case, gpu, out=big[:, 1:3])
+    got = big[:, 1:3]
+    _check(got, oracle_attn(case), "strided out")
+    assert torch.all(big[:, 0] == 7) and torch.all(big[:, 3:] == 7)
+
+
+def test_permuted_query_view(gpu):
+    case = attn_case([12, 44, 3], seed=23)
+    d = _to_dev(case, gpu)
+    q = d["q_packed"]  # [T, N, H, W] -> stored as [T, H, N, W], viewed back
+    d["q_packed"] = q.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    assert not d["q_packed"].is_contiguous()
+    from spikeinfer_amd.kernels import paged_spike_attn_decode
+
+    _check(paged_spike_attn_decode(**d), oracle_attn(case), "permuted q")
+
+
+def test_deterministic_run_to_run(gpu):
+    case = attn_case([4000, 123, 77], density=0.3, seed=29)
+    a = _run(case, gpu).clone()
+    b = _run(case, gpu)
+    assert torch.equal(a, b)
+
+
+def test_pad_rows_seq_len_one_on_pad_block(gpu):
+    """Graph padding rows: table = pad block, seq_len = 1 (model_runner.py:234-240)."""
+    case = attn_case([20, 1, 1], seed=31)
+    pad = case["k"].shape[2] // 16 - 1
+    case["tables"][1:] = pad
+    _check(_run(case, gpu), oracle_attn(case), "pad rows")
+
+
+def test_scores_bit_exact(gpu):
+    from spikeinfer_amd.kernels import paged_spike_attn_scores
+
+    case = attn_case([1, 5, 40, 97], block_size=16, seed=37)
+    d = _to_dev(case, gpu)
+    d.pop("v_cache")
+    got = paged_spike_attn_scores(**d, max_len=97).cpu().numpy()
+    want = orc.decode_scores(case["q"], case["k"], case["tables"], case["lens"], 64, 16, 14, 2, 97)
+    assert np.array_equal(got, want)
+
+
+def test_rejects_bad_arguments(gpu):
+    from spikeinfer_amd.kernels import paged_spike_attn_decode
+
+    case = attn_case([8])
+    d = _to_dev(case, gpu)
+    with pytest.raises(ValueError, match="words"):
+        paged_spike_attn_decode(**{**d, "head_dim": 128})
+    with pytest.raises(ValueError, match="heads"):
+        paged_spike_attn_decode(**{**d, "num_q_heads": 7})
+    with pytest.raises(ValueError, match="power of two"):
+        paged_spike_attn_decode(**{**d, "block_size": 24})

@@ -1,0 +1,86 @@
+"""The C-ABI library loads, exports every symbol the header declares, and
+rejects bad arguments on the host -- no kernel is launched (CPU only)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from spikeinfer_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "spikeinfer_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(spk_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert _declared() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.spk_abi_version() == _lib.ABI_VERSION
+
+
+def _i64(*v):
+    return (ctypes.c_int64 * len(v))(*v)
+
+
+def test_host_side_validation_without_a_gpu():
+    lib = _lib.load()
+    s4 = _i64(0, 0, 0, 1)
+    rc = lib.spk_decode_attn(None, s4, None, s4, None, s4, 0, None, 0, 0, None, None, 0, s4,
+                             4, 1, 5, 2, 64, 16, 8, 0.125, None, 0, None)
+    assert rc == _lib.SPK_EINVAL and b"multiple" in lib.spk_last_error()
+    rc = lib.spk_decode_attn(None, s4, None, s4, None, s4, 0, None, 0, 0, None, None, 0, s4,
+                             4, 1, 14, 2, 64, 24, 8, 0.125, None, 0, None)
+    assert rc == _lib.SPK_EINVAL and b"power of two" in lib.spk_last_error()
+    rc = lib.spk_decode_attn(None, s4, None, s4, None, s4, 0, None, 0, 0, None, None, 0, s4,
+                             4, 1, 14, 2, 256, 16, 8, 0.0625, None, 0, None)
+    assert rc == _lib.SPK_EUNSUPPORTED
+    rc = lib.spk_decode_attn(None, s4, None, s4, None, s4, 0, None, 0, 0, None, None, 0, s4,
+                             4, 1, 14, 2, 64, 16, 8, 5.0, None, 0, None)
+    assert rc == _lib.SPK_EINVAL and b"scale" in lib.spk_last_error()
+    # long contexts need a workspace; a missing one is rejected, not faulted
+    rc = lib.spk_decode_attn(None, s4, None, s4, None, s4, 0, None, 0, 0, None, None, 0, s4,
+                             4, 256, 14, 2, 64, 16, 2048, 0.125, None, 0, None)
+    assert rc == _lib.SPK_EINVAL and b"workspace" in lib.spk_last_error()
+    assert lib.spk_lif_multistep(None, 2, _i64(0, 0, 1), None, None, 0, None, None, 0, None,
+                                 0, 4, 4, None) == _lib.SPK_EINVAL
+    assert lib.spk_lif_pack_write(None, 2, _i64(0, 0, 0, 1), None, None, 0, None, _i64(0, 0, 0),
+                                  None, 0, None, 0, 4, 4, 2, 256, None) == _lib.SPK_EUNSUPPORTED
+    assert lib.spk_pack(None, 9, 1, None, 4, 4, None) == _lib.SPK_EINVAL
+
+
+def test_workspace_sizing():
+    lib = _lib.load()
+    # config 3 shape: one partition, no workspace
+    assert lib.spk_decode_attn_workspace_bytes(4, 64, 14, 2, 64, 16, 12) == 0
+    # config 4 shape: 32k context splits into partitions of partial sums
+    ws = lib.spk_decode_attn_workspace_bytes(4, 256, 14, 2, 64, 16, 2048)
+    assert ws > 0 and ws % (4 * 256 * 14 * 65 * 4) == 0
+
+
+def test_python_api_refuses_cpu_tensors():
+    from spikeinfer_amd.kernels import lif_multistep, pack_spikes, paged_spike_attn_decode
+
+    with pytest.raises(ValueError, match="GPU"):
+        pack_spikes(torch.ones(2, 64))
+    with pytest.raises(ValueError, match="GPU"):
+        lif_multistep(torch.ones(4, 2, 64), torch.ones(64), torch.ones(64))
+    q = torch.zeros(4, 1, 14, 2, dtype=torch.int32)
+    kv = torch.zeros(4, 2, 32, 2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="GPU"):
+        paged_spike_attn_decode(q, kv, kv, torch.zeros(1, 2, dtype=torch.int32),
+                                torch.ones(1, dtype=torch.int32), 64, 16, 14, 2)
+    with pytest.raises(ValueError, match="expected 1"):
+        paged_spike_attn_decode(q, kv, kv, torch.zeros(1, 2, dtype=torch.int32),
+                                torch.ones(1, dtype=torch.int32), 32, 16, 14, 2)
