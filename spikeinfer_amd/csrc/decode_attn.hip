@@ -18,43 +18,12 @@
 //     bitwise ops and two v_bcnt per word plus one LDS read;
 //   * value side: lane = channel, v bit selects the weight, fixed summation
 //     order (bit-reproducible run to run).
-#include "common.hpp"
+#include "decode_attn.hpp"
+
+#include <cstdlib>
+#include <cstring>
 
 namespace spk {
-
-constexpr int kAttnThreads = 256;   // 4 waves
-constexpr int kMaxRep = 16;
-
-struct AttnParams {
-  const uint32_t *q;
-  int64_t qs0, qs1, qs2;
-  const uint32_t *k;
-  int64_t ks0, ks1, ks2;
-  const uint32_t *v;
-  int64_t vs0, vs1, vs2;
-  int64_t num_slots;
-  const int32_t *bt;
-  int64_t bts0, bts1;
-  const int32_t *lens;
-  void *out;
-  int out_dtype;
-  int64_t os0, os1, os2, os3;
-  int T, N, Hq, Hkv, head_dim, bs_log2, nrep;
-  float scale;
-  int part_len;      // tokens per partition (multiple of 256 and of block size)
-  int num_parts;     // partitions per sequence at most
-  float *ws;         // [num_parts][T][N][Hq][head_dim + 1] partial sums
-};
-
-// Partition length: long contexts are split so the grid has enough
-// workgroups and no single workgroup walks a 32k-token context alone.
-inline int choose_part_len(int64_t units, int64_t ctx_max) {
-  int part = 4096;
-  // Small decode batches: shorten partitions (down to 512) until the grid
-  // holds about four workgroups per CU.
-  while (part > 512 && units * ((ctx_max + part - 1) / part) < 1024) part >>= 1;
-  return part;
-}
 
 template <int W>
 __device__ __forceinline__ int popc_andn(const uint32_t (&q)[W], const uint32_t (&k)[W]) {
@@ -315,7 +284,11 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
   hipStream_t s = static_cast<hipStream_t>(stream);
   dim3 grid(p.num_parts, T * Hkv, N);
   const int W = (head_dim + 31) / 32;
-  switch (W) {
+  const char *path = getenv("SPIKEINFER_AMD_ATTN_PATH");
+  const bool force_general = path && strcmp(path, "general") == 0;
+  if (!force_general && mfma_path_supported(p)) {
+    launch_decode_mfma(p, grid, s);
+  } else switch (W) {
     case 1: launch_general<1>(p, grid, s); break;
     case 2: launch_general<2>(p, grid, s); break;
     case 3: launch_general<3>(p, grid, s); break;

@@ -1,0 +1,48 @@
+// Parameters and helpers shared by the two decode-attention paths
+// (decode_attn.hip: general VALU path; decode_attn_mfma.hip: matrix cores).
+#pragma once
+
+#include "common.hpp"
+
+namespace spk {
+
+constexpr int kAttnThreads = 256;   // 4 waves
+constexpr int kMaxRep = 16;
+
+struct AttnParams {
+  const uint32_t *q;
+  int64_t qs0, qs1, qs2;
+  const uint32_t *k;
+  int64_t ks0, ks1, ks2;
+  const uint32_t *v;
+  int64_t vs0, vs1, vs2;
+  int64_t num_slots;
+  const int32_t *bt;
+  int64_t bts0, bts1;
+  const int32_t *lens;
+  void *out;
+  int out_dtype;
+  int64_t os0, os1, os2, os3;
+  int T, N, Hq, Hkv, head_dim, bs_log2, nrep;
+  float scale;
+  int part_len;      // tokens per partition (multiple of 256 and of block size)
+  int num_parts;     // partitions per sequence at most
+  float *ws;         // [num_parts][T][N][Hq][head_dim + 1] partial sums
+};
+
+// Partition length: long contexts are split so the grid has enough
+// workgroups and no single workgroup walks a 32k-token context alone.
+inline int choose_part_len(int64_t units, int64_t ctx_max) {
+  int part = 4096;
+  // Small decode batches: shorten partitions (down to 512) until the grid
+  // holds about four workgroups per CU.
+  while (part > 512 && units * ((ctx_max + part - 1) / part) < 1024) part >>= 1;
+  return part;
+}
+
+// Matrix-core path for head_dim 64, n_rep <= 8 (decode_attn_mfma.hip).
+// Returns false when the shape or alignment does not qualify.
+bool mfma_path_supported(const AttnParams &p);
+void launch_decode_mfma(const AttnParams &p, dim3 grid, hipStream_t s);
+
+}  // namespace spk

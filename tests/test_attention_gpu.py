@@ -20,6 +20,14 @@ ABS_TOL = 1e-3
 REL_TOL = 1e-5
 
 
+@pytest.fixture(autouse=True, params=["auto", "general"])
+def attn_path(request, monkeypatch):
+    """Every case runs on the dispatched path (matrix cores where the shape
+    allows: head_dim 64, n_rep <= 8) and on the general VALU path."""
+    monkeypatch.setenv("SPIKEINFER_AMD_ATTN_PATH", request.param)
+    return request.param
+
+
 def _to_dev(case, dev):
     return dict(
         q_packed=torch.from_numpy(case["q"]).to(dev),
