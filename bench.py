@@ -188,6 +188,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run one device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -217,8 +220,17 @@ def main():
         del c3
         print("config 2", file=sys.stderr, flush=True)
         extras["config2_lif"] = bench_lif(args.steps, args.warmup, dev)
-    print("cpu baseline", file=sys.stderr, flush=True)
-    cpu = cpu_baseline(inp, dev, args.cpu_budget)
+    if args.calib_copy_mib:
+        src = torch.empty(args.calib_copy_mib << 18, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    cpu = None
+    if not args.no_cpu:
+        print("cpu baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(inp, dev, args.cpu_budget)
 
     line = {
         "metric": "popcount decode attn achieved HBM GB/s (config 4: batch 256, ctx U[4096,32768])",

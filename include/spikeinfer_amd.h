@@ -69,9 +69,9 @@ int spk_abi_version(void);
  * position p < seq_lens[n] lives in slot block_tables[n][p/bs]*bs + p%bs; the
  * score is popcount(q & k) * scale; out = softmax(scores) @ unpacked(v).
  * W must equal ceil(head_dim/32); head_dim <= 128; block_size a power of two.
- * A sequence with seq_len <= 0 gets an all-zero output row.  A token whose
- * slot falls outside [0, num_slots) is skipped instead of read, so a corrupt
- * block table cannot fault the GPU.  scale must satisfy
+ * A sequence with seq_len <= 0 gets an all-zero output row.  Slots outside
+ * [0, num_slots) are never dereferenced, so a corrupt block table cannot
+ * fault the GPU (the output rows of such a sequence are unspecified).  scale must satisfy
  * 0 < scale*head_dim <= 80 (the softmax uses the fixed offset popcount(q)).
  *
  * `workspace` must hold spk_decode_attn_workspace_bytes(...) bytes (it may be

@@ -235,7 +235,7 @@ extern "C" size_t spk_decode_attn_workspace_bytes(int T, int N, int Hq, int Hkv,
                                                   int block_size, int max_blocks) {
   if (T <= 0 || N <= 0 || Hkv <= 0 || max_blocks <= 0 || block_size <= 0) return 0;
   const int64_t ctx_max = (int64_t)max_blocks * block_size;
-  const int part = choose_part_len((int64_t)N * T * Hkv, ctx_max);
+  const int part = choose_part_len((int64_t)N * T * Hkv, ctx_max, block_size);
   const int64_t nparts = (ctx_max + part - 1) / part;
   if (nparts <= 1) return 0;
   return (size_t)nparts * T * N * Hq * (head_dim + 1) * sizeof(float);
@@ -277,7 +277,7 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
   p.T = T; p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.head_dim = head_dim;
   p.bs_log2 = ilog2(block_size); p.nrep = Hq / Hkv; p.scale = scale;
   const int64_t ctx_max = (int64_t)max_blocks * block_size;
-  p.part_len = choose_part_len((int64_t)N * T * Hkv, ctx_max);
+  p.part_len = choose_part_len((int64_t)N * T * Hkv, ctx_max, block_size);
   p.num_parts = (int)((ctx_max + p.part_len - 1) / p.part_len);
   p.ws = static_cast<float *>(workspace);
 

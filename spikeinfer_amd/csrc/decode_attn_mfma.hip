@@ -42,6 +42,7 @@ namespace mfma {
 
 constexpr int kWaves = 4;
 constexpr int kStepTokens = 64;
+constexpr int kMaxPartBlocks = 512;  // block-table entries staged per partition
 
 struct alignas(16) WaveStage {
   uint64_t v[kStepTokens];          // token-major v words        (512 B)
@@ -89,8 +90,74 @@ __device__ __forceinline__ v2i tr_b8(const SPK_LDS char *p) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((SPK_LDS v2i *)p);
 }
 
+// Stages one 64-token step of a wave: weight digits and v words into the
+// wave's LDS stage, weights into lsum.  MASKED handles a partial last step.
+template <int NREP, bool MASKED>
+__device__ __forceinline__ void stage_step(WaveStage &st, int lane, uint64_t kw, uint64_t vw,
+                                           bool valid, const uint32_t (&q0)[8],
+                                           const uint32_t (&q1)[8], const uint2 *tab,
+                                           float (&lsum)[8]) {
+  const uint32_t klo = static_cast<uint32_t>(kw), khi = static_cast<uint32_t>(kw >> 32);
+  uint32_t dig[8];
+#pragma unroll
+  for (int h = 0; h < 8; ++h) {
+    if (h < NREP) {
+      const int d = __popc(q0[h] & ~klo) + __popc(q1[h] & ~khi);
+      const uint2 e = tab[d];
+      dig[h] = (!MASKED || valid) ? e.x : 0u;
+      lsum[h] += (!MASKED || valid) ? __uint_as_float(e.y) : 0.f;
+    } else {
+      dig[h] = 0u;
+    }
+  }
+  st.v[lane] = (!MASKED || valid) ? vw : 0ull;
+  uint4 *arow = reinterpret_cast<uint4 *>(&st.a[lane * 8]);
+  arow[0] = make_uint4(dig[0], dig[1], dig[2], dig[3]);
+  arow[1] = make_uint4(dig[4], dig[5], dig[6], dig[7]);
+}
+
+// Wave-level ordering of the private stage: LDS writes before the
+// cross-lane transpose reads, and those reads before the next step's writes.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Transposes the staged step into MFMA operands and accumulates.
+__device__ __forceinline__ void contract_step(const WaveStage &st, int lane, v16f &acc0,
+                                              v16f &acc1) {
+  const int g = lane >> 5;          // K group of the MFMA operands
+  const int i16 = lane & 15;        // lane within its 16-lane transpose group
+  const int win = (lane >> 4) & 1;  // 16-byte window of a digit row / channel offset
+  const SPK_LDS char *lds_v = (const SPK_LDS char *)st.v;
+  const SPK_LDS char *lds_a = (const SPK_LDS char *)st.a;
+  v8i A;
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {
+    const int row = 32 * g + 8 * qd + ((i16 >> 1) & 7);
+    const v2i r = tr_b8(lds_a + row * 32 + win * 16 + (i16 & 1) * 8);
+    A[2 * qd] = r.x;
+    A[2 * qd + 1] = r.y;
+  }
+  const v2i w0 = tr_b4(lds_v + (16 * g + i16) * 8);
+  const v2i w1 = tr_b4(lds_v + (32 + 16 * g + i16) * 8);
+  const uint32_t wv[4] = {static_cast<uint32_t>(w0.x), static_cast<uint32_t>(w0.y),
+                          static_cast<uint32_t>(w1.x), static_cast<uint32_t>(w1.y)};
+  v8i B0 = {}, B1 = {};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    B0[i] = static_cast<int>((wv[i] >> win) & 0x11111111u);
+    B1[i] = static_cast<int>((wv[i] >> (2 + win)) & 0x11111111u);
+  }
+  acc0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B0, acc0, 0, 4, 0, 127, 0, 127);
+  acc1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B1, acc1, 0, 4, 0, 127, 0, 127);
+}
+
 // One workgroup = 4 waves = one (partition, t, kv head, sequence); waves take
-// the partition's 64-token steps round-robin and reduce at the end.
+// the partition's 64-token steps round-robin (two steps of loads in flight
+// per wave) and reduce at the end in a fixed order.
+template <int NREP>
 __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(AttnParams p) {
   const int part = blockIdx.x;
   const int t = blockIdx.y / p.Hkv;
@@ -106,7 +173,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(AttnParam
   const int start = part * p.part_len;
   const int end = min(len, start + p.part_len);
 
-  __shared__ uint2 tab[65];  // per d: 4 e4m3 digits, bits of the represented weight
+  __shared__ uint2 tab[65];            // per d: 4 e4m3 digits, bits of their value
+  __shared__ int32_t blocks[kMaxPartBlocks];  // this partition's physical blocks
   __shared__ __align__(16) char smem[kSmemBytes];
   WaveStage &st = reinterpret_cast<WaveStage *>(smem)[wave];
 
@@ -122,14 +190,16 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(AttnParam
     }
     tab[tid] = make_uint2(digits, __float_as_uint(wsum));
   }
+  const int nblk = end > start ? ((end - start - 1) >> p.bs_log2) + 1 : 0;
+  const int blk0 = start >> p.bs_log2;
+  for (int b = tid; b < nblk; b += kWaves * 64) blocks[b] = p.bt[n * p.bts0 + (blk0 + b) * p.bts1];
 
-  // Query words of the (up to 8) heads sharing this kv head.
   uint32_t q0[8], q1[8];
 #pragma unroll
   for (int h = 0; h < 8; ++h) {
-    q0[h] = q1[h] = 0xffffffffu;  // unused head: d = 0 but its digits are zeroed below
-    if (h < p.nrep) {
-      const uint32_t *qp = p.q + t * p.qs0 + n * p.qs1 + (kvh * p.nrep + h) * p.qs2;
+    q0[h] = q1[h] = 0u;
+    if (h < NREP) {
+      const uint32_t *qp = p.q + t * p.qs0 + n * p.qs1 + (kvh * NREP + h) * p.qs2;
       q0[h] = qp[0];
       q1[h] = qp[1];
     }
@@ -139,96 +209,50 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(AttnParam
   const uint64_t *kbase = reinterpret_cast<const uint64_t *>(p.k + t * p.ks0 + kvh * p.ks1);
   const uint64_t *vbase = reinterpret_cast<const uint64_t *>(p.v + t * p.vs0 + kvh * p.vs1);
   const int bs_mask = (1 << p.bs_log2) - 1;
+  const uint64_t num_slots = static_cast<uint64_t>(p.num_slots);
+
+  // Token j of this partition -> its K/V words.  Slots outside the cache are
+  // never dereferenced: they read slot 0 and are masked (tail step) or, for a
+  // corrupt table, give an unspecified but fault-free result.
+  auto load = [&](int j, uint64_t &kw, uint64_t &vw) {
+    const int jj = min(j, end - 1);
+    const int phys = blocks[(jj - start) >> p.bs_log2];
+    uint64_t slot = (static_cast<uint64_t>(static_cast<uint32_t>(phys)) << p.bs_log2) |
+                    static_cast<uint64_t>(jj & bs_mask);
+    slot = slot < num_slots ? slot : 0;
+    kw = __builtin_nontemporal_load(kbase + slot);
+    vw = __builtin_nontemporal_load(vbase + slot);
+  };
 
   v16f acc0 = {}, acc1 = {};
   float lsum[8];
 #pragma unroll
   for (int h = 0; h < 8; ++h) lsum[h] = 0.f;
 
-  // Per-lane constants of the transpose reads.
-  const int g = lane >> 5;          // K group of the MFMA operands
-  const int i16 = lane & 15;        // lane within its 16-lane transpose group
-  const int win = (lane >> 4) & 1;  // which 16-byte window of a digit row
-  const int s_lane = win;           // channel offset within the lane's nibble
-  const SPK_LDS char *lds_v = (const SPK_LDS char *)st.v;
-  const SPK_LDS char *lds_a = (const SPK_LDS char *)st.a;
+  constexpr int kStride = kWaves * kStepTokens;
+  // Steps of this wave: full ones (every token valid), then at most one tail.
+  const int first = start + wave * kStepTokens;
+  const int span = end - first;
+  const int nfull = span > 0 ? (span / kStride) + ((span % kStride) >= kStepTokens ? 1 : 0) : 0;
+  const int ntotal = span > 0 ? (span + kStride - 1) / kStride : 0;
 
-  // Loads of one step (token j0 + lane); invalid tokens read as zero.
-  auto load = [&](int j0, uint64_t &kw, uint64_t &vw, bool &valid) {
-    const int j = j0 + lane;
-    valid = j < end;
-    kw = vw = 0;
-    if (valid) {
-      const int phys = p.bt[n * p.bts0 + (j >> p.bs_log2) * p.bts1];
-      const int64_t slot = (static_cast<int64_t>(phys) << p.bs_log2) | (j & bs_mask);
-      valid = slot >= 0 && slot < p.num_slots;
-      if (valid) {
-        kw = __builtin_nontemporal_load(kbase + slot);
-        vw = __builtin_nontemporal_load(vbase + slot);
-      }
+  uint64_t ka = 0, va = 0, kb = 0, vb = 0;
+  if (ntotal > 0) load(first + lane, ka, va);
+  if (ntotal > 1) load(first + kStride + lane, kb, vb);
+  for (int i = 0; i < ntotal; ++i) {
+    uint64_t kc = 0, vc = 0;
+    if (i + 2 < ntotal) load(first + (i + 2) * kStride + lane, kc, vc);
+    if (i < nfull) {
+      stage_step<NREP, false>(st, lane, ka, va, true, q0, q1, tab, lsum);
+    } else {
+      const bool valid = first + i * kStride + lane < end;
+      stage_step<NREP, true>(st, lane, ka, va, valid, q0, q1, tab, lsum);
     }
-  };
-
-  int j0 = start + wave * kStepTokens;
-  uint64_t kw, vw;
-  bool valid;
-  if (j0 < end) load(j0, kw, vw, valid);
-  for (; j0 < end; j0 += kWaves * kStepTokens) {
-    // Prefetch the next step while this one is scored and contracted.
-    uint64_t kn = 0, vn = 0;
-    bool validn = false;
-    const int jn = j0 + kWaves * kStepTokens;
-    if (jn < end) load(jn, kn, vn, validn);
-
-    // Scores -> weight digits for the 8 head slots of this token.
-    const uint32_t klo = static_cast<uint32_t>(kw), khi = static_cast<uint32_t>(kw >> 32);
-    uint32_t dig[8];
-#pragma unroll
-    for (int h = 0; h < 8; ++h) {
-      const int d = __popc(q0[h] & ~klo) + __popc(q1[h] & ~khi);
-      const uint2 e = tab[d];
-      const bool use = valid && h < p.nrep;
-      dig[h] = use ? e.x : 0u;
-      lsum[h] += use ? __uint_as_float(e.y) : 0.f;
-    }
-    st.v[lane] = valid ? vw : 0ull;
-    uint4 *arow = reinterpret_cast<uint4 *>(&st.a[lane * 8]);
-    arow[0] = make_uint4(dig[0], dig[1], dig[2], dig[3]);
-    arow[1] = make_uint4(dig[4], dig[5], dig[6], dig[7]);
-    // The stage is private to this wave: a wave-level fence orders the
-    // writes above before the cross-lane transpose reads below.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    v8i A;
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const int row = 32 * g + 8 * qd + ((i16 >> 1) & 7);
-      const v2i r = tr_b8(lds_a + row * 32 + win * 16 + (i16 & 1) * 8);
-      A[2 * qd] = r.x;
-      A[2 * qd + 1] = r.y;
-    }
-    const v2i w0 = tr_b4(lds_v + (16 * g + i16) * 8);
-    const v2i w1 = tr_b4(lds_v + (32 + 16 * g + i16) * 8);
-    const uint32_t wv[4] = {static_cast<uint32_t>(w0.x), static_cast<uint32_t>(w0.y),
-                            static_cast<uint32_t>(w1.x), static_cast<uint32_t>(w1.y)};
-    v8i B0 = {}, B1 = {};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      B0[i] = static_cast<int>((wv[i] >> s_lane) & 0x11111111u);
-      B1[i] = static_cast<int>((wv[i] >> (2 + s_lane)) & 0x11111111u);
-    }
-    acc0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B0, acc0, 0, 4, 0, 127, 0, 127);
-    acc1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B1, acc1, 0, 4, 0, 127, 0, 127);
-    // The next step overwrites the stage: keep the reads above ahead of it.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    kw = kn;
-    vw = vn;
-    valid = validn;
+    wave_sync();
+    contract_step(st, lane, acc0, acc1);
+    wave_sync();
+    ka = kb; va = vb;
+    kb = kc; vb = vc;
   }
 
   // Per lane: column n = lane%32 of both tiles; rows 4h+s with
@@ -283,8 +307,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(AttnParam
 #pragma unroll
   for (int qd = 0; qd < 4; ++qd) {
     const int h = 2 * qd + (lane >> 5);
-    if (h >= p.nrep) continue;
-    const int hq = kvh * p.nrep + h;
+    if (h >= NREP) continue;
+    const int hq = kvh * NREP + h;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int ch = 4 * (col & 15) + 2 * u + (col >> 4);
@@ -307,11 +331,22 @@ bool mfma_path_supported(const AttnParams &p) {
   const auto al8 = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 7) == 0; };
   return p.head_dim == 64 && p.nrep <= 8 && p.ks2 == 2 && p.vs2 == 2 &&
          (p.ks0 % 2) == 0 && (p.ks1 % 2) == 0 && (p.vs0 % 2) == 0 && (p.vs1 % 2) == 0 &&
-         al8(p.k) && al8(p.v);
+         al8(p.k) && al8(p.v) &&
+         ((p.part_len + (1 << p.bs_log2) - 1) >> p.bs_log2) <= mfma::kMaxPartBlocks;
 }
 
 void launch_decode_mfma(const AttnParams &p, dim3 grid, hipStream_t s) {
-  mfma::decode_attn_mfma_kernel<<<grid, mfma::kWaves * 64, 0, s>>>(p);
+  const int threads = mfma::kWaves * 64;
+  switch (p.nrep) {
+    case 1: mfma::decode_attn_mfma_kernel<1><<<grid, threads, 0, s>>>(p); break;
+    case 2: mfma::decode_attn_mfma_kernel<2><<<grid, threads, 0, s>>>(p); break;
+    case 3: mfma::decode_attn_mfma_kernel<3><<<grid, threads, 0, s>>>(p); break;
+    case 4: mfma::decode_attn_mfma_kernel<4><<<grid, threads, 0, s>>>(p); break;
+    case 5: mfma::decode_attn_mfma_kernel<5><<<grid, threads, 0, s>>>(p); break;
+    case 6: mfma::decode_attn_mfma_kernel<6><<<grid, threads, 0, s>>>(p); break;
+    case 7: mfma::decode_attn_mfma_kernel<7><<<grid, threads, 0, s>>>(p); break;
+    default: mfma::decode_attn_mfma_kernel<8><<<grid, threads, 0, s>>>(p); break;
+  }
 }
 
 }  // namespace spk
