@@ -33,9 +33,9 @@ struct AttnParams {
 // Partition length: long contexts are split so the grid has enough
 // workgroups and no single workgroup walks a 32k-token context alone.
 inline int choose_part_len(int64_t units, int64_t ctx_max, int block_size) {
-  int part = 4096;
-  // At most 512 block-table entries per partition (they are staged in LDS).
-  while (part > block_size * 512 && part > 256) part >>= 1;
+  int part = 16384;
+  // At most 1024 block-table entries per partition (they are staged in LDS).
+  while (part > block_size * 1024 && part > 256) part >>= 1;
   // Small decode batches: shorten partitions (down to 512) until the grid
   // holds about four workgroups per CU.
   while (part > 512 && part > block_size && units * ((ctx_max + part - 1) / part) < 1024) part >>= 1;

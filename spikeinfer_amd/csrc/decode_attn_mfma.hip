@@ -41,12 +41,18 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 namespace mfma {
 
 constexpr int kWaves = 4;
-constexpr int kStepTokens = 64;
-constexpr int kMaxPartBlocks = 512;  // block-table entries staged per partition
+constexpr int kStepTokens = 128;      // tokens per wave step (2 per lane)
+constexpr int kMaxPartBlocks = 1024;   // block-table entries staged per partition
 
+// Stage of one wave step.  Row r holds token 2r (r < 64) or token
+// 2(r-64)+1 (r >= 64) of the step, so lane l writes rows l and l+64 and every
+// staging write and transpose read touches consecutive 8/16-byte chunks (no
+// LDS bank conflicts).  Digit rows are 32 bytes (byte 4h+s = digit s of head
+// h), stored as two 16-byte windows: a[w][r] = bytes 16w..16w+15 of row r.
 struct alignas(16) WaveStage {
-  uint64_t v[kStepTokens];          // token-major v words        (512 B)
-  uint32_t a[kStepTokens * 8];      // token-major digit words, 8 heads (2 KB)
+  uint64_t v[kStepTokens];            // v word of each row                  (1 KB)
+  uint64_t vs[kStepTokens];           // the same words shifted right by 1   (1 KB)
+  uint4 a[2][kStepTokens];            // digit rows, window-major            (4 KB)
 };
 
 constexpr int kReduceFloats = (kWaves - 1) * 64 * 12;  // 8 values + 4 l per lane
@@ -90,30 +96,42 @@ __device__ __forceinline__ v2i tr_b8(const SPK_LDS char *p) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((SPK_LDS v2i *)p);
 }
 
-// Stages one 64-token step of a wave: weight digits and v words into the
-// wave's LDS stage, weights into lsum.  MASKED handles a partial last step.
+// Digit words of one token for the NREP heads; zero when masked off.
 template <int NREP, bool MASKED>
-__device__ __forceinline__ void stage_step(WaveStage &st, int lane, uint64_t kw, uint64_t vw,
-                                           bool valid, const uint32_t (&q0)[8],
-                                           const uint32_t (&q1)[8], const uint2 *tab,
-                                           float (&lsum)[8]) {
+__device__ __forceinline__ void token_digits(uint64_t kw, bool valid, const uint32_t (&q0)[8],
+                                             const uint32_t (&q1)[8], const uint32_t *tab,
+                                             uint32_t (&dig)[8]) {
   const uint32_t klo = static_cast<uint32_t>(kw), khi = static_cast<uint32_t>(kw >> 32);
-  uint32_t dig[8];
 #pragma unroll
   for (int h = 0; h < 8; ++h) {
     if (h < NREP) {
-      const int d = __popc(q0[h] & ~klo) + __popc(q1[h] & ~khi);
-      const uint2 e = tab[d];
-      dig[h] = (!MASKED || valid) ? e.x : 0u;
-      lsum[h] += (!MASKED || valid) ? __uint_as_float(e.y) : 0.f;
+      const uint32_t d = __popc(q1[h] & ~khi) + __popc(q0[h] & ~klo);
+      dig[h] = (!MASKED || valid) ? tab[d] : 0u;
     } else {
       dig[h] = 0u;
     }
   }
-  st.v[lane] = (!MASKED || valid) ? vw : 0ull;
-  uint4 *arow = reinterpret_cast<uint4 *>(&st.a[lane * 8]);
-  arow[0] = make_uint4(dig[0], dig[1], dig[2], dig[3]);
-  arow[1] = make_uint4(dig[4], dig[5], dig[6], dig[7]);
+}
+
+// Stages one 128-token step of a wave (lane l holds tokens 2l and 2l+1,
+// staged as rows l and l+64):
+// weight digits and v words (plain and shifted) into the wave's LDS stage.
+template <int NREP, bool MASKED>
+__device__ __forceinline__ void stage_step(WaveStage &st, int lane, const uint64_t (&kw)[2],
+                                           const uint64_t (&vw)[2], const bool (&valid)[2],
+                                           const uint32_t (&q0)[8], const uint32_t (&q1)[8],
+                                           const uint32_t *tab) {
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    uint32_t dig[8];
+    token_digits<NREP, MASKED>(kw[e], valid[e], q0, q1, tab, dig);
+    const int row = lane + 64 * e;
+    st.a[0][row] = make_uint4(dig[0], dig[1], dig[2], dig[3]);
+    st.a[1][row] = make_uint4(dig[4], dig[5], dig[6], dig[7]);
+    const uint64_t v = (!MASKED || valid[e]) ? vw[e] : 0ull;
+    st.v[row] = v;
+    st.vs[row] = v >> 1;
+  }
 }
 
 // Wave-level ordering of the private stage: LDS writes before the
@@ -124,19 +142,26 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Transposes the staged step into MFMA operands and accumulates.
-__device__ __forceinline__ void contract_step(const WaveStage &st, int lane, v16f &acc0,
-                                              v16f &acc1) {
+// Contracts staged rows [64u, 64u+64) of the step (its even tokens for u = 0,
+// odd for u = 1): two channel tiles and
+// the all-ones tile that accumulates the softmax denominators.
+//   tile 0 column n: channel 4*(n%16) + n/16      (fp4 0001 = 0.5 per set bit)
+//   tile 1 column n: channel 4*(n%16) + 2 + n/16  (fp4 0100 = 2.0 per set bit)
+// Lanes 16..31 of each half read the shifted copy, so one AND per register
+// selects their channel for both tiles.
+__device__ __forceinline__ void contract_half(const WaveStage &st, int lane, int u, v16f &acc0,
+                                              v16f &acc1, v16f &accl) {
   const int g = lane >> 5;          // K group of the MFMA operands
   const int i16 = lane & 15;        // lane within its 16-lane transpose group
-  const int win = (lane >> 4) & 1;  // 16-byte window of a digit row / channel offset
-  const SPK_LDS char *lds_v = (const SPK_LDS char *)st.v;
-  const SPK_LDS char *lds_a = (const SPK_LDS char *)st.a;
+  const int win = (lane >> 4) & 1;  // 16-byte window of a digit row / shifted copy
+  const SPK_LDS char *lds_v =
+      (const SPK_LDS char *)(win ? st.vs : st.v) + 64 * u * 8;
+  const SPK_LDS char *lds_a = (const SPK_LDS char *)&st.a[win][64 * u];
   v8i A;
 #pragma unroll
   for (int qd = 0; qd < 4; ++qd) {
     const int row = 32 * g + 8 * qd + ((i16 >> 1) & 7);
-    const v2i r = tr_b8(lds_a + row * 32 + win * 16 + (i16 & 1) * 8);
+    const v2i r = tr_b8(lds_a + row * 16 + (i16 & 1) * 8);
     A[2 * qd] = r.x;
     A[2 * qd + 1] = r.y;
   }
@@ -144,21 +169,23 @@ __device__ __forceinline__ void contract_step(const WaveStage &st, int lane, v16
   const v2i w1 = tr_b4(lds_v + (32 + 16 * g + i16) * 8);
   const uint32_t wv[4] = {static_cast<uint32_t>(w0.x), static_cast<uint32_t>(w0.y),
                           static_cast<uint32_t>(w1.x), static_cast<uint32_t>(w1.y)};
-  v8i B0 = {}, B1 = {};
+  v8i B0 = {}, B1 = {}, Bl = {};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    B0[i] = static_cast<int>((wv[i] >> win) & 0x11111111u);
-    B1[i] = static_cast<int>((wv[i] >> (2 + win)) & 0x11111111u);
+    B0[i] = static_cast<int>(wv[i] & 0x11111111u);
+    B1[i] = static_cast<int>(wv[i] & 0x44444444u);
+    Bl[i] = 0x11111111;
   }
   acc0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B0, acc0, 0, 4, 0, 127, 0, 127);
   acc1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B1, acc1, 0, 4, 0, 127, 0, 127);
+  accl = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, Bl, accl, 0, 4, 0, 127, 0, 127);
 }
 
 // One workgroup = 4 waves = one (partition, t, kv head, sequence); waves take
-// the partition's 64-token steps round-robin (two steps of loads in flight
+// the partition's 128-token steps round-robin (two steps of loads in flight
 // per wave) and reduce at the end in a fixed order.
 template <int NREP>
-__global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(AttnParams p) {
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void decode_attn_mfma_kernel(AttnParams p) {
   const int part = blockIdx.x;
   const int t = blockIdx.y / p.Hkv;
   const int kvh = blockIdx.y % p.Hkv;
@@ -173,7 +200,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(AttnParam
   const int start = part * p.part_len;
   const int end = min(len, start + p.part_len);
 
-  __shared__ uint2 tab[65];            // per d: 4 e4m3 digits, bits of their value
+  __shared__ uint32_t tab[65];                // per d: 4 e4m3 digits of exp(-d*scale)
   __shared__ int32_t blocks[kMaxPartBlocks];  // this partition's physical blocks
   __shared__ __align__(16) char smem[kSmemBytes];
   WaveStage &st = reinterpret_cast<WaveStage *>(smem)[wave];
@@ -181,14 +208,12 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(AttnParam
   if (tid <= 64) {
     float x = expf(-static_cast<float>(tid) * p.scale) * 256.f;
     uint32_t digits = 0;
-    float wsum = 0.f;
     for (int s = 0; s < 4; ++s) {
       float q;
       digits |= e4m3_encode(x, &q) << (8 * s);
-      wsum += ldexpf(q, -(8 + 4 * s));
       x = (x - q) * 16.f;
     }
-    tab[tid] = make_uint2(digits, __float_as_uint(wsum));
+    tab[tid] = digits;
   }
   const int nblk = end > start ? ((end - start - 1) >> p.bs_log2) + 1 : 0;
   const int blk0 = start >> p.bs_log2;
@@ -211,72 +236,94 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(AttnParam
   const int bs_mask = (1 << p.bs_log2) - 1;
   const uint64_t num_slots = static_cast<uint64_t>(p.num_slots);
 
-  // Token j of this partition -> its K/V words.  Slots outside the cache are
-  // never dereferenced: they read slot 0 and are masked (tail step) or, for a
-  // corrupt table, give an unspecified but fault-free result.
-  auto load = [&](int j, uint64_t &kw, uint64_t &vw) {
-    const int jj = min(j, end - 1);
+  // Tokens j, j+1 of this partition (j even, same block as block_size >= 2)
+  // -> their K/V words, one 16-byte load each.  Pairs past the partition
+  // re-read its last pair (clamped) so the loads stay unconditional; slots
+  // outside the cache are never dereferenced.
+  auto load = [&](int j, uint64_t (&kw)[2], uint64_t (&vw)[2]) {
+    const int jj = min(j, (end - 1) & ~1);
     const int phys = blocks[(jj - start) >> p.bs_log2];
     uint64_t slot = (static_cast<uint64_t>(static_cast<uint32_t>(phys)) << p.bs_log2) |
                     static_cast<uint64_t>(jj & bs_mask);
-    slot = slot < num_slots ? slot : 0;
-    kw = __builtin_nontemporal_load(kbase + slot);
-    vw = __builtin_nontemporal_load(vbase + slot);
+    slot = slot + 1 < num_slots ? slot : 0;
+    typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
+    const v2u64 k2 = __builtin_nontemporal_load(reinterpret_cast<const v2u64 *>(kbase + slot));
+    const v2u64 v2 = __builtin_nontemporal_load(reinterpret_cast<const v2u64 *>(vbase + slot));
+    kw[0] = k2.x; kw[1] = k2.y;
+    vw[0] = v2.x; vw[1] = v2.y;
   };
 
-  v16f acc0 = {}, acc1 = {};
-  float lsum[8];
-#pragma unroll
-  for (int h = 0; h < 8; ++h) lsum[h] = 0.f;
+  v16f acc0 = {}, acc1 = {}, accl = {};
 
   constexpr int kStride = kWaves * kStepTokens;
-  // Steps of this wave: full ones (every token valid), then at most one tail.
   const int first = start + wave * kStepTokens;
   const int span = end - first;
   const int nfull = span > 0 ? (span / kStride) + ((span % kStride) >= kStepTokens ? 1 : 0) : 0;
   const int ntotal = span > 0 ? (span + kStride - 1) / kStride : 0;
 
-  uint64_t ka = 0, va = 0, kb = 0, vb = 0;
-  if (ntotal > 0) load(first + lane, ka, va);
-  if (ntotal > 1) load(first + kStride + lane, kb, vb);
-  for (int i = 0; i < ntotal; ++i) {
-    uint64_t kc = 0, vc = 0;
-    if (i + 2 < ntotal) load(first + (i + 2) * kStride + lane, kc, vc);
-    if (i < nfull) {
-      stage_step<NREP, false>(st, lane, ka, va, true, q0, q1, tab, lsum);
+  auto step = [&](const uint64_t (&kw)[2], const uint64_t (&vw)[2], bool masked, int j0) {
+    if (!masked) {
+      const bool all[2] = {true, true};
+      stage_step<NREP, false>(st, lane, kw, vw, all, q0, q1, tab);
     } else {
-      const bool valid = first + i * kStride + lane < end;
-      stage_step<NREP, true>(st, lane, ka, va, valid, q0, q1, tab, lsum);
+      const bool valid[2] = {j0 + 2 * lane < end, j0 + 2 * lane + 1 < end};
+      stage_step<NREP, true>(st, lane, kw, vw, valid, q0, q1, tab);
     }
     wave_sync();
-    contract_step(st, lane, acc0, acc1);
+    contract_half(st, lane, 0, acc0, acc1, accl);
+    if (!masked || j0 + 1 < end) contract_half(st, lane, 1, acc0, acc1, accl);  // odd tokens
     wave_sync();
-    ka = kb; va = vb;
-    kb = kc; vb = vc;
+  };
+
+  // Three register buffers in a fixed ring, unrolled by three, so a load in
+  // flight is never copied (a copy would wait for it).
+  uint64_t k0[2], v0[2], k1[2], v1[2], k2[2], v2[2];
+  const int lo = 2 * lane;
+  load(first + lo, k0, v0);
+  load(first + kStride + lo, k1, v1);
+  int i = 0;
+  for (; i + 3 <= nfull; i += 3) {
+    load(first + (i + 2) * kStride + lo, k2, v2);
+    step(k0, v0, false, 0);
+    load(first + (i + 3) * kStride + lo, k0, v0);
+    step(k1, v1, false, 0);
+    load(first + (i + 4) * kStride + lo, k1, v1);
+    step(k2, v2, false, 0);
+  }
+  if (i < nfull) {
+    load(first + (i + 2) * kStride + lo, k2, v2);
+    step(k0, v0, false, 0);
+    ++i;
+    if (i < nfull) {
+      step(k1, v1, false, 0);
+      ++i;
+    }
+  }
+  if (nfull < ntotal) {  // the partial last step: buffer nfull % 3 of the ring
+    const int r = nfull % 3;
+    const int j0 = first + nfull * kStride;
+    if (r == 0) step(k0, v0, true, j0);
+    else if (r == 1) step(k1, v1, true, j0);
+    else step(k2, v2, true, j0);
   }
 
-  // Per lane: column n = lane%32 of both tiles; rows 4h+s with
-  // h = 2*qd + lane/32, s = j%4, for acc index j = 4*qd + s.  The digit scale
-  // 2^-(8+4s) and the fp4 value 0.5 of a set bit fold into one factor.
-  float val[8];
+  // Per lane: column n = lane%32 of the tiles; rows 4h+s with
+  // h = 2*qd + lane/32, s = j%4, for acc index j = 4*qd + s.  Digit s carries
+  // 2^-(8+4s); a set bit is 0.5 (tile 0, ones tile) or 2.0 (tile 1).
+  float val[8], lh[4];
 #pragma unroll
   for (int qd = 0; qd < 4; ++qd) {
-    float a0 = 0.f, a1 = 0.f;
+    float a0 = 0.f, a1 = 0.f, al = 0.f;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const float f = ldexpf(1.f, -(7 + 4 * s));
       a0 += acc0[4 * qd + s] * f;
-      a1 += acc1[4 * qd + s] * f;
+      a1 += acc1[4 * qd + s] * (0.25f * f);
+      al += accl[4 * qd + s] * f;
     }
     val[2 * qd] = a0;
     val[2 * qd + 1] = a1;
-  }
-  float lw[8];
-#pragma unroll
-  for (int h = 0; h < 8; ++h) {
-    float l = lsum[h];
-    for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
-    lw[h] = l;
+    lh[qd] = al;
   }
 
   // Cross-wave reduction (fixed order) through LDS, reusing the stage area.
@@ -285,21 +332,18 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(AttnParam
   if (wave > 0) {
     float *dst = red + ((wave - 1) * 64 + lane) * 12;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dst[i] = val[i];
+    for (int k = 0; k < 8; ++k) dst[k] = val[k];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dst[8 + i] = lw[2 * i + (lane >> 5)];
+    for (int k = 0; k < 4; ++k) dst[8 + k] = lh[k];
   }
   __syncthreads();
   if (wave != 0) return;
-  float lh[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) lh[i] = lw[2 * i + (lane >> 5)];
   for (int w = 1; w < kWaves; ++w) {
     const float *src = red + ((w - 1) * 64 + lane) * 12;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) val[i] += src[i];
+    for (int k = 0; k < 8; ++k) val[k] += src[k];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lh[i] += src[8 + i];
+    for (int k = 0; k < 4; ++k) lh[k] += src[8 + k];
   }
 
   const int col = lane & 31;
@@ -328,10 +372,10 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attn_mfma_kernel(AttnParam
 }  // namespace mfma
 
 bool mfma_path_supported(const AttnParams &p) {
-  const auto al8 = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 7) == 0; };
-  return p.head_dim == 64 && p.nrep <= 8 && p.ks2 == 2 && p.vs2 == 2 &&
-         (p.ks0 % 2) == 0 && (p.ks1 % 2) == 0 && (p.vs0 % 2) == 0 && (p.vs1 % 2) == 0 &&
-         al8(p.k) && al8(p.v) &&
+  const auto al16 = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  return p.head_dim == 64 && p.nrep <= 8 && p.bs_log2 >= 1 && p.ks2 == 2 && p.vs2 == 2 &&
+         (p.ks0 % 4) == 0 && (p.ks1 % 4) == 0 && (p.vs0 % 4) == 0 && (p.vs1 % 4) == 0 &&
+         al16(p.k) && al16(p.v) &&
          ((p.part_len + (1 << p.bs_log2) - 1) >> p.bs_log2) <= mfma::kMaxPartBlocks;
 }
 
