@@ -36,10 +36,13 @@ __device__ __forceinline__ int popc_andn(const uint32_t (&q)[W], const uint32_t 
 template <int W, int REP>
 __global__ __launch_bounds__(kAttnThreads) void decode_attn_general(AttnParams p) {
   constexpr int CPL = (W + 1) / 2;  // channels per lane (64 lanes)
-  const int part = blockIdx.x;
-  const int t = blockIdx.y / p.Hkv;
-  const int kvh = blockIdx.y % p.Hkv;
-  const int n = blockIdx.z;
+  // x = (sequence, timestep, kv head) unit, y = partition: consecutive block
+  // ids (dealt round-robin to the 8 XCDs) are sibling units of similar
+  // length, and every unit's first partition is launched before any tail.
+  const int part = blockIdx.y;
+  const int kvh = blockIdx.x % p.Hkv;
+  const int t = (blockIdx.x / p.Hkv) % p.T;
+  const int n = blockIdx.x / (p.Hkv * p.T);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -282,7 +285,7 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
   p.ws = static_cast<float *>(workspace);
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 grid(p.num_parts, T * Hkv, N);
+  dim3 grid(N * T * Hkv, p.num_parts);
   const int W = (head_dim + 31) / 32;
   const char *path = getenv("SPIKEINFER_AMD_ATTN_PATH");
   const bool force_general = path && strcmp(path, "general") == 0;

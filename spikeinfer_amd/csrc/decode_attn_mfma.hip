@@ -96,6 +96,15 @@ __device__ __forceinline__ v2i tr_b8(const SPK_LDS char *p) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((SPK_LDS v2i *)p);
 }
 
+// popc(a) + popc(b) as v_bcnt with its accumulator operand.  Written out
+// because the compiler otherwise distributes the table-index scaling over both
+// counts (two extra shifts per lookup on the hottest path).
+__device__ __forceinline__ uint32_t popc2(uint32_t a, uint32_t b) {
+  uint32_t d;
+  asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(d) : "v"(b), "v"(__popc(a)));
+  return d;
+}
+
 // Digit words of one token for the NREP heads; zero when masked off.
 template <int NREP, bool MASKED>
 __device__ __forceinline__ void token_digits(uint64_t kw, bool valid, const uint32_t (&q0)[8],
@@ -105,8 +114,7 @@ __device__ __forceinline__ void token_digits(uint64_t kw, bool valid, const uint
 #pragma unroll
   for (int h = 0; h < 8; ++h) {
     if (h < NREP) {
-      const uint32_t d = __popc(q1[h] & ~khi) + __popc(q0[h] & ~klo);
-      dig[h] = (!MASKED || valid) ? tab[d] : 0u;
+      dig[h] = (!MASKED || valid) ? tab[popc2(q0[h] & ~klo, q1[h] & ~khi)] : 0u;
     } else {
       dig[h] = 0u;
     }
@@ -185,11 +193,14 @@ __device__ __forceinline__ void contract_half(const WaveStage &st, int lane, int
 // the partition's 128-token steps round-robin (two steps of loads in flight
 // per wave) and reduce at the end in a fixed order.
 template <int NREP>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void decode_attn_mfma_kernel(AttnParams p) {
-  const int part = blockIdx.x;
-  const int t = blockIdx.y / p.Hkv;
-  const int kvh = blockIdx.y % p.Hkv;
-  const int n = blockIdx.z;
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6))) void decode_attn_mfma_kernel(AttnParams p) {
+  // x = (sequence, timestep, kv head) unit, y = partition: consecutive block
+  // ids (dealt round-robin to the 8 XCDs) are sibling units of similar
+  // length, and every unit's first partition is launched before any tail.
+  const int part = blockIdx.y;
+  const int kvh = blockIdx.x % p.Hkv;
+  const int t = (blockIdx.x / p.Hkv) % p.T;
+  const int n = blockIdx.x / (p.Hkv * p.T);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
