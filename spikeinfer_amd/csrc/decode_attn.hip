@@ -241,7 +241,9 @@ extern "C" size_t spk_decode_attn_workspace_bytes(int T, int N, int Hq, int Hkv,
   const int part = choose_part_len((int64_t)N * T * Hkv, ctx_max, block_size);
   const int64_t nparts = (ctx_max + part - 1) / part;
   if (nparts <= 1) return 0;
-  return (size_t)nparts * T * N * Hq * (head_dim + 1) * sizeof(float);
+  // Partial sums, then the launch order of the matrix-core path.
+  return (size_t)nparts * T * N * Hq * (head_dim + 1) * sizeof(float) +
+         ((size_t)nparts * N * T * Hkv + 1) * sizeof(int32_t);
 }
 
 extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], const int32_t *k_cache,
@@ -290,7 +292,10 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
   const char *path = getenv("SPIKEINFER_AMD_ATTN_PATH");
   const bool force_general = path && strcmp(path, "general") == 0;
   if (!force_general && mfma_path_supported(p)) {
-    launch_decode_mfma(p, grid, s);
+    int32_t *order = p.num_parts > 1
+        ? reinterpret_cast<int32_t *>(p.ws + (size_t)p.num_parts * T * N * Hq * (head_dim + 1))
+        : nullptr;
+    launch_decode_mfma(p, order, s);
   } else switch (W) {
     case 1: launch_general<1>(p, grid, s); break;
     case 2: launch_general<2>(p, grid, s); break;

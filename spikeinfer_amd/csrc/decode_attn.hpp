@@ -28,6 +28,10 @@ struct AttnParams {
   int part_len;      // tokens per partition (multiple of 256 and of block size)
   int num_parts;     // partitions per sequence at most
   float *ws;         // [num_parts][T][N][Hq][head_dim + 1] partial sums
+  // Optional launch order (matrix-core path, split contexts): order[b] is the
+  // work item (part * units + unit) of block b, longest first; order[items]
+  // holds the number of items.  nullptr: block (unit, part) = (x, y).
+  const int32_t *order;
 };
 
 // Partition length: long contexts are split so the grid has enough
@@ -45,6 +49,8 @@ inline int choose_part_len(int64_t units, int64_t ctx_max, int block_size) {
 // Matrix-core path for head_dim 64, n_rep <= 8 (decode_attn_mfma.hip).
 // Returns false when the shape or alignment does not qualify.
 bool mfma_path_supported(const AttnParams &p);
-void launch_decode_mfma(const AttnParams &p, dim3 grid, hipStream_t s);
+// Launches the matrix-core kernel, preceded, when p.num_parts > 1, by the
+// planner that fills `order` (units * num_parts + 1 ints of scratch).
+void launch_decode_mfma(AttnParams p, int32_t *order, hipStream_t s);
 
 }  // namespace spk

@@ -194,13 +194,21 @@ __device__ __forceinline__ void contract_half(const WaveStage &st, int lane, int
 // per wave) and reduce at the end in a fixed order.
 template <int NREP>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6))) void decode_attn_mfma_kernel(AttnParams p) {
-  // x = (sequence, timestep, kv head) unit, y = partition: consecutive block
-  // ids (dealt round-robin to the 8 XCDs) are sibling units of similar
-  // length, and every unit's first partition is launched before any tail.
-  const int part = blockIdx.y;
-  const int kvh = blockIdx.x % p.Hkv;
-  const int t = (blockIdx.x / p.Hkv) % p.T;
-  const int n = blockIdx.x / (p.Hkv * p.T);
+  // Unplanned launch: x = (sequence, timestep, kv head) unit, y = partition.
+  // Either way consecutive block ids (dealt round-robin to the 8 XCDs) are
+  // sibling units of equal length.
+  const int units = p.N * p.T * p.Hkv;
+  int unit = blockIdx.x, part = blockIdx.y;
+  if (p.order) {  // planned launch: longest work items first
+    const int items = units * p.num_parts;
+    if ((int)blockIdx.x >= p.order[items]) return;
+    const int item = p.order[blockIdx.x];
+    unit = item % units;
+    part = item / units;
+  }
+  const int kvh = unit % p.Hkv;
+  const int t = (unit / p.Hkv) % p.T;
+  const int n = unit / (p.Hkv * p.T);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -390,8 +398,69 @@ bool mfma_path_supported(const AttnParams &p) {
          ((p.part_len + (1 << p.bs_log2) - 1) >> p.bs_log2) <= mfma::kMaxPartBlocks;
 }
 
-void launch_decode_mfma(const AttnParams &p, dim3 grid, hipStream_t s) {
+namespace mfma {
+
+// Longest-processing-time-first launch order for split contexts.  One
+// workgroup counting-sorts the (sequence, partition) items by token count in
+// 256-token buckets, largest first; the T*Hkv sibling units of an item stay
+// adjacent.  Items past a sequence's length are left out (their blocks exit).
+// Ties are placed in arbitrary order: each item computes the same sums
+// wherever it runs, so outputs do not depend on it.
+__global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, int N, int UPS,
+                                                        int part_len, int num_parts,
+                                                        int32_t *order) {
+  constexpr int kMaxBuckets = 66;  // part_len <= 16384 tokens, 256 per bucket
+  __shared__ int count[kMaxBuckets];
+  __shared__ int offset[kMaxBuckets];
+  const int tid = threadIdx.x;
+  const int nb = (part_len >> 8) + 2;
+  for (int b = tid; b < nb; b += blockDim.x) count[b] = 0;
+  __syncthreads();
+  auto bucket = [&](int len, int part) {
+    const int size = min(part_len, len - part * part_len);
+    return size <= 0 ? 0 : ((size + 255) >> 8) + 1;  // len <= 0 items: bucket 0
+  };
+  auto exists = [&](int len, int part) {
+    const int nparts = len <= 0 ? 1 : (len + part_len - 1) / part_len;
+    return part < nparts;
+  };
+  for (int i = tid; i < N * num_parts; i += blockDim.x) {
+    const int n = i % N, part = i / N;
+    const int len = lens[n];
+    if (exists(len, part)) atomicAdd(&count[bucket(len, part)], UPS);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int b = nb - 1; b >= 0; --b) {
+      offset[b] = run;
+      run += count[b];
+    }
+    order[N * UPS * num_parts] = run;
+  }
+  __syncthreads();
+  for (int i = tid; i < N * num_parts; i += blockDim.x) {
+    const int n = i % N, part = i / N;
+    const int len = lens[n];
+    if (!exists(len, part)) continue;
+    const int at = atomicAdd(&offset[bucket(len, part)], UPS);
+    for (int ut = 0; ut < UPS; ++ut) order[at + ut] = part * (N * UPS) + n * UPS + ut;
+  }
+}
+
+}  // namespace mfma
+
+void launch_decode_mfma(AttnParams p, int32_t *order, hipStream_t s) {
   const int threads = mfma::kWaves * 64;
+  const int units = p.N * p.T * p.Hkv;
+  dim3 grid(units, p.num_parts);
+  p.order = nullptr;
+  if (p.num_parts > 1 && order) {
+    mfma::decode_attn_plan<<<1, 1024, 0, s>>>(p.lens, p.N, p.T * p.Hkv, p.part_len, p.num_parts,
+                                              order);
+    p.order = order;
+    grid = dim3(units * p.num_parts);
+  }
   switch (p.nrep) {
     case 1: mfma::decode_attn_mfma_kernel<1><<<grid, threads, 0, s>>>(p); break;
     case 2: mfma::decode_attn_mfma_kernel<2><<<grid, threads, 0, s>>>(p); break;
