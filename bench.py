@@ -92,7 +92,7 @@ def time_calls(fn, steps, warmup, stream):
     return start.elapsed_time(end) / steps  # ms per call
 
 
-def bench_attention(inp, steps, warmup, dev, out_dtype=torch.float32):
+def bench_attention(inp, steps, warmup, dev, out_dtype=torch.float32, graph=False):
     from spikeinfer_amd.kernels import decode_attn_workspace_bytes, paged_spike_attn_decode
 
     n = inp["lens"].numel()
@@ -106,7 +106,22 @@ def bench_attention(inp, steps, warmup, dev, out_dtype=torch.float32):
             paged_spike_attn_decode(inp["q"], k, v, inp["tables"], inp["lens"], D, BS, HQ, HKV,
                                     out=out, workspace=ws)
 
-    ms = time_calls(step, steps, warmup, torch.cuda.current_stream(dev))
+    if graph:
+        # One decode step's attention calls captured in a hipGraph (as the
+        # serving runner replays them): launch cost without Python in between.
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                step()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        ms = time_calls(g.replay, steps, warmup, torch.cuda.current_stream(dev))
+    else:
+        ms = time_calls(step, steps, warmup, torch.cuda.current_stream(dev))
     return ms, out
 
 
@@ -214,7 +229,7 @@ def main():
             del alt
         print("config 3", file=sys.stderr, flush=True)
         c3 = make_attn_inputs(64, 128, 192, 0.2, 3000, dev, layers=24)
-        ms3, _ = bench_attention(c3, args.steps, args.warmup, dev, torch.bfloat16)
+        ms3, _ = bench_attention(c3, args.steps, args.warmup, dev, torch.bfloat16, graph=True)
         extras["config3_attn_us_per_step_24_layers"] = round(ms3 * 1000, 1)
         extras["config3_attn_gbs"] = round(attn_bytes(c3["lens_cpu"], 2) * 24 / ms3 / 1e6, 1)
         del c3

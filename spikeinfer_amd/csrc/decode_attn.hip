@@ -292,6 +292,7 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
   const char *path = getenv("SPIKEINFER_AMD_ATTN_PATH");
   const bool force_general = path && strcmp(path, "general") == 0;
   if (!force_general && mfma_path_supported(p)) {
+    build_digit_table(scale, p.digits);
     int32_t *order = p.num_parts > 1
         ? reinterpret_cast<int32_t *>(p.ws + (size_t)p.num_parts * T * N * Hq * (head_dim + 1))
         : nullptr;

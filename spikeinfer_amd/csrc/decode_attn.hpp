@@ -32,7 +32,14 @@ struct AttnParams {
   // work item (part * units + unit) of block b, longest first; order[items]
   // holds the number of items.  nullptr: block (unit, part) = (x, y).
   const int32_t *order;
+  // Matrix-core path: for d = popc(q & ~k) in 0..64, the four e4m3 digits of
+  // exp(-d*scale) * 2^8 (byte s weighs 2^-(4s)), built on the host once per
+  // scale (build_digit_table) and copied into LDS by every workgroup.
+  uint32_t digits[65];
 };
+
+// Fills digits[] for `scale` (host; reuses the last table when unchanged).
+void build_digit_table(float scale, uint32_t digits[65]);
 
 // Partition length: long contexts are split so the grid has enough
 // workgroups and no single workgroup walks a 32k-token context alone.

@@ -13,7 +13,8 @@
 //   A rows  = (head h < 8, digit s < 4): row 4h+s holds, per token, digit s of
 //             the weight w(d) = exp(-d*scale), d = popc(q_h & ~k).  The weight
 //             is split into four e4m3 digits, w = sum_s q_s * 2^-(8+4s)
-//             (relative error <= ~1e-6), looked up in a 65-entry LDS table.
+//             (relative error <= ~1e-6), looked up in a 65-entry LDS table
+//             (built once per scale on the host, passed in the arguments).
 //   B cols  = 32 of the 64 channels; element = fp4 e2m1 0b0001 (= 0.5) where
 //             the v bit is set.  Two MFMAs cover the 64 channels.
 //
@@ -30,6 +31,8 @@
 // K = 32*(k/16) + 16*(l/32) + k%16; D lane l, acc j is row
 // 8*(j/4) + 4*(l/32) + j%4, column l%32.
 #include "decode_attn.hpp"
+
+#include <cmath>
 
 namespace spk {
 
@@ -59,35 +62,6 @@ constexpr int kReduceFloats = (kWaves - 1) * 64 * 12;  // 8 values + 4 l per lan
 constexpr int kSmemBytes =
     (kWaves * (int)sizeof(WaveStage) > kReduceFloats * 4) ? kWaves * (int)sizeof(WaveStage)
                                                             : kReduceFloats * 4;
-
-// x to OCP e4m3 (bias 7, subnormal step 2^-9, sign bit 0x80), round to
-// nearest even; returns the code and stores the value it encodes.  The digit
-// split feeds it signed residuals (rounding up leaves a negative remainder).
-__device__ inline uint32_t e4m3_encode(float x, float *val) {
-  const uint32_t sign = x < 0.f ? 0x80u : 0u;
-  const float a = fabsf(x);
-  float v;
-  uint32_t code;
-  if (!(a > 0.f)) {
-    v = 0.f;
-    code = 0;
-  } else if (a < 0.015625f) {  // below 2^-6: subnormal
-    const float m = rintf(a * 512.f);
-    if (m >= 8.f) { v = 0.015625f; code = 0x08; }
-    else { v = m * (1.f / 512.f); code = static_cast<uint32_t>(m); }
-  } else {
-    int e;
-    frexpf(a, &e);
-    int E = e - 1;  // a in [2^E, 2^(E+1))
-    float m = rintf((ldexpf(a, -E) - 1.f) * 8.f);
-    if (m >= 8.f) { m = 0.f; ++E; }
-    if (E > 8) { E = 8; m = 6.f; }  // saturate at 448 (never reached: |x| <= 256)
-    v = ldexpf(1.f + m * 0.125f, E);
-    code = static_cast<uint32_t>(((E + 7) << 3) | static_cast<int>(m));
-  }
-  *val = sign ? -v : v;
-  return code | (code ? sign : 0u);
-}
 
 __device__ __forceinline__ v2i tr_b4(const SPK_LDS char *p) {
   return __builtin_amdgcn_ds_read_tr4_b64_v2i32((SPK_LDS v2i *)p);
@@ -224,16 +198,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6))
   __shared__ __align__(16) char smem[kSmemBytes];
   WaveStage &st = reinterpret_cast<WaveStage *>(smem)[wave];
 
-  if (tid <= 64) {
-    float x = expf(-static_cast<float>(tid) * p.scale) * 256.f;
-    uint32_t digits = 0;
-    for (int s = 0; s < 4; ++s) {
-      float q;
-      digits |= e4m3_encode(x, &q) << (8 * s);
-      x = (x - q) * 16.f;
-    }
-    tab[tid] = digits;
-  }
+  if (tid <= 64) tab[tid] = p.digits[tid];
   const int nblk = end > start ? ((end - start - 1) >> p.bs_log2) + 1 : 0;
   const int blk0 = start >> p.bs_log2;
   for (int b = tid; b < nblk; b += kWaves * 64) blocks[b] = p.bt[n * p.bts0 + (blk0 + b) * p.bts1];
@@ -389,6 +354,54 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6))
 }
 
 }  // namespace mfma
+
+// x to OCP e4m3 (bias 7, subnormal step 2^-9, sign bit 0x80), round to
+// nearest even; returns the code and stores the value it encodes.  The digit
+// split feeds it signed residuals (rounding up leaves a negative remainder).
+static uint32_t e4m3_encode(float x, float *val) {
+  const uint32_t sign = x < 0.f ? 0x80u : 0u;
+  const float a = std::fabs(x);
+  float v;
+  uint32_t code;
+  if (!(a > 0.f)) {
+    v = 0.f;
+    code = 0;
+  } else if (a < 0.015625f) {  // below 2^-6: subnormal
+    const float m = std::nearbyint(a * 512.f);
+    if (m >= 8.f) { v = 0.015625f; code = 0x08; }
+    else { v = m * (1.f / 512.f); code = static_cast<uint32_t>(m); }
+  } else {
+    int e;
+    std::frexp(a, &e);
+    int E = e - 1;  // a in [2^E, 2^(E+1))
+    float m = std::nearbyint((std::ldexp(a, -E) - 1.f) * 8.f);
+    if (m >= 8.f) { m = 0.f; ++E; }
+    if (E > 8) { E = 8; m = 6.f; }  // saturate at 448 (never reached: |x| <= 256)
+    v = std::ldexp(1.f + m * 0.125f, E);
+    code = static_cast<uint32_t>(((E + 7) << 3) | static_cast<int>(m));
+  }
+  *val = sign ? -v : v;
+  return code | (code ? sign : 0u);
+}
+
+void build_digit_table(float scale, uint32_t digits[65]) {
+  static thread_local float last_scale = -1.f;
+  static thread_local uint32_t last[65];
+  if (scale != last_scale) {
+    for (int d = 0; d <= 64; ++d) {
+      float x = std::exp(-static_cast<float>(d) * scale) * 256.f;
+      uint32_t w = 0;
+      for (int s = 0; s < 4; ++s) {
+        float q;
+        w |= e4m3_encode(x, &q) << (8 * s);
+        x = (x - q) * 16.f;
+      }
+      last[d] = w;
+    }
+    last_scale = scale;
+  }
+  for (int d = 0; d <= 64; ++d) digits[d] = last[d];
+}
 
 bool mfma_path_supported(const AttnParams &p) {
   const auto al16 = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };

@@ -113,6 +113,149 @@ __global__ __launch_bounds__(256) void lif_pack_kernel(LifParams p, int64_t xs0,
   }
 }
 
+
+// ---- vectorised paths: 16 bytes per lane ---------------------------------
+constexpr int kTBatch = 4;  // timesteps whose loads are issued together
+// Element types of the vector paths.
+template <int DT> struct Elem;
+template <> struct Elem<SPK_F32> { typedef float T; static constexpr int kVec = 4; };
+template <> struct Elem<SPK_F16> { typedef uint16_t T; static constexpr int kVec = 8; };
+template <> struct Elem<SPK_BF16> { typedef uint16_t T; static constexpr int kVec = 8; };
+
+template <int DT>
+__device__ __forceinline__ float elem_to_f32(typename Elem<DT>::T v) {
+  if constexpr (DT == SPK_F32) return v;
+  else if constexpr (DT == SPK_BF16) return bf16_bits_to_f32(v);
+  else return static_cast<float>(__builtin_bit_cast(_Float16, v));
+}
+
+template <int DT>
+__device__ __forceinline__ typename Elem<DT>::T spike_elem(bool s) {
+  if constexpr (DT == SPK_F32) return s ? 1.f : 0.f;
+  else if constexpr (DT == SPK_BF16) return s ? 0x3f80 : 0;
+  else return s ? 0x3c00 : 0;
+}
+
+// Dense LIF over rows of N contiguous channels (N % kVec == 0, 16-byte aligned
+// rows): each thread owns kVec consecutive channels of one row, loads and
+// stores 16 bytes per timestep.  Spikes are written in the input's dtype.
+template <int DT>
+__global__ __launch_bounds__(256) void lif_dense_vec_kernel(LifParams p, int64_t xs0, int64_t xs1,
+                                                            const float *mem0, void *spikes,
+                                                            float *u_out, int64_t M, int N) {
+  typedef typename Elem<DT>::T E;
+  constexpr int V = Elem<DT>::kVec;
+  typedef E Vec __attribute__((ext_vector_type(V)));
+  const int64_t groups = M * (N / V);
+  const int64_t total = M * N;
+  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = gi / (N / V);
+    const int c0 = static_cast<int>(gi - m * (N / V)) * V;
+    float beta[V], th[V], u[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      beta[i] = clamp01(load_as_f32(p.beta, c0 + i, p.param_dtype));
+      th[i] = load_as_f32(p.th, c0 + i, p.param_dtype);
+      u[i] = mem0 ? mem0[m * N + c0 + i] : 0.f;
+    }
+    const E *xrow = static_cast<const E *>(p.x) + m * xs1 + c0;
+    E *srow = static_cast<E *>(spikes) + m * N + c0;
+    for (int t0 = 0; t0 < p.T; t0 += kTBatch) {
+      // All loads of up to kTBatch timesteps in flight before the recurrence.
+      Vec xv[kTBatch];
+#pragma unroll
+      for (int k = 0; k < kTBatch; ++k)
+        if (t0 + k < p.T)
+          xv[k] = __builtin_nontemporal_load(reinterpret_cast<const Vec *>(xrow + (t0 + k) * xs0));
+#pragma unroll
+      for (int k = 0; k < kTBatch; ++k) {
+        if (t0 + k >= p.T) break;
+        Vec sv;
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+          sv[i] = spike_elem<DT>(lif_step(u[i], elem_to_f32<DT>(xv[k][i]), beta[i], th[i]));
+        __builtin_nontemporal_store(sv, reinterpret_cast<Vec *>(srow + (t0 + k) * total));
+      }
+    }
+    if (u_out) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) u_out[m * N + c0 + i] = u[i];
+    }
+  }
+}
+
+// Fused LIF + pack for D % 64 == 0 with 16-byte aligned, channel-contiguous
+// rows: each lane owns 8 channels of a (token, head) row (bf16/f16 input),
+// 8 lanes cover 64 channels; per timestep their 8 spike bytes are OR-reduced
+// into the 64-bit word by three xor-shuffles and one lane stores it.
+template <int DT>
+__global__ __launch_bounds__(256) void lif_pack_vec_kernel(LifParams p, int64_t xs0, int64_t xs1,
+                                                           int64_t xs2, uint64_t *packed,
+                                                           int64_t ps0, int64_t ps1, int64_t ps2,
+                                                           const int64_t *slots, int64_t num_slots,
+                                                           int64_t n_tok, int H, int D) {
+  typedef typename Elem<DT>::T E;
+  typedef E Vec __attribute__((ext_vector_type(8)));
+  const int lane = threadIdx.x & 63;
+  const int sub = lane & 7;                  // lane within its 64-channel group
+  const int groups_per_row = D >> 6;
+  const int64_t groups = n_tok * H * groups_per_row;  // 64-channel groups
+  const int64_t gstride = (int64_t)gridDim.x * (blockDim.x >> 3);
+  for (int64_t gi = blockIdx.x * (int64_t)(blockDim.x >> 3) + (threadIdx.x >> 3); gi < groups;
+       gi += gstride) {
+    const int64_t row = gi / groups_per_row;
+    const int grp = static_cast<int>(gi - row * groups_per_row);
+    const int64_t tok = row / H;
+    const int h = static_cast<int>(row - tok * H);
+    const int c0 = grp * 64 + sub * 8;
+    float beta[8], th[8], u[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      beta[i] = clamp01(load_as_f32(p.beta, c0 + i, p.param_dtype));
+      th[i] = load_as_f32(p.th, c0 + i, p.param_dtype);
+      u[i] = 0.f;
+    }
+    bool write = true;
+    int64_t dst;
+    if (slots) {
+      const int64_t slot = slots[tok];
+      write = slot >= 0 && slot < num_slots;
+      dst = h * ps1 + slot * ps2;
+    } else {
+      dst = tok * ps1 + h * ps2;
+    }
+    dst = dst / 2 + grp;  // in uint64 words
+    const E *xrow = static_cast<const E *>(p.x) + tok * xs1 + h * xs2 + c0;
+    for (int t0 = 0; t0 < p.T; t0 += kTBatch) {
+      // All loads of up to kTBatch timesteps in flight before the recurrence.
+      Vec xv[kTBatch];
+#pragma unroll
+      for (int k = 0; k < kTBatch; ++k)
+        if (t0 + k < p.T)
+          xv[k] = __builtin_nontemporal_load(reinterpret_cast<const Vec *>(xrow + (t0 + k) * xs0));
+#pragma unroll
+      for (int k = 0; k < kTBatch; ++k) {
+      if (t0 + k >= p.T) break;
+      const int t = t0 + k;
+      const Vec x = xv[k];
+      uint32_t byte = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) byte |= lif_step(u[i], elem_to_f32<DT>(x[i]), beta[i], th[i]) ? (1u << i) : 0u;
+      // bits of lane `sub` land at channel offsets 8*sub .. 8*sub+7
+      uint32_t lo = sub < 4 ? byte << (8 * sub) : 0u;
+      uint32_t hi = sub < 4 ? 0u : byte << (8 * (sub - 4));
+#pragma unroll
+      for (int off = 1; off < 8; off <<= 1) {
+        lo |= __shfl_xor(lo, off);
+        hi |= __shfl_xor(hi, off);
+      }
+      if (write && sub == 0) packed[t * (ps0 / 2) + dst] = (static_cast<uint64_t>(hi) << 32) | lo;
+      }
+    }
+  }
+}
+
 // ---- pack / unpack ---------------------------------------------------------
 // One wave per row; each 64-channel chunk is one __ballot.
 __global__ __launch_bounds__(256) void pack_kernel(const void *x, int x_dtype, int64_t row_stride,
@@ -165,8 +308,25 @@ extern "C" int spk_lif_multistep(const void *x, int x_dtype, const int64_t x_str
     return fail(SPK_EINVAL, "unsupported dtype (x %d, params %d, spikes %d)", x_dtype, param_dtype, spike_dtype);
   if (M == 0) return SPK_OK;
   LifParams p{x, x_dtype, beta, threshold, param_dtype, T};
-  lif_dense_kernel<<<grid_for(M * N, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
-      p, x_strides[0], x_strides[1], x_strides[2], mem0, spikes, spike_dtype, u_out, M, N);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int vec = x_dtype == SPK_F32 ? 4 : 8;
+  const int esz = x_dtype == SPK_F32 ? 4 : 2;
+  const bool vec_ok = spike_dtype == x_dtype && x_strides[2] == 1 && N % vec == 0 &&
+                      (x_strides[0] * esz) % 16 == 0 && (x_strides[1] * esz) % 16 == 0 &&
+                      (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(spikes) & 15) == 0;
+  if (vec_ok) {
+    const unsigned grid = grid_for(M * (N / vec), 256);
+    if (x_dtype == SPK_BF16)
+      lif_dense_vec_kernel<SPK_BF16><<<grid, 256, 0, s>>>(p, x_strides[0], x_strides[1], mem0, spikes, u_out, M, N);
+    else if (x_dtype == SPK_F16)
+      lif_dense_vec_kernel<SPK_F16><<<grid, 256, 0, s>>>(p, x_strides[0], x_strides[1], mem0, spikes, u_out, M, N);
+    else
+      lif_dense_vec_kernel<SPK_F32><<<grid, 256, 0, s>>>(p, x_strides[0], x_strides[1], mem0, spikes, u_out, M, N);
+  } else {
+    lif_dense_kernel<<<grid_for(M * N, 256), 256, 0, s>>>(
+        p, x_strides[0], x_strides[1], x_strides[2], mem0, spikes, spike_dtype, u_out, M, N);
+  }
   return check_launch("lif_multistep");
 }
 
@@ -187,7 +347,21 @@ extern "C" int spk_lif_pack_write(const void *x, int x_dtype, const int64_t x_st
   hipStream_t s = static_cast<hipStream_t>(stream);
   const unsigned grid = grid_for(n_tok * H, 4);
   uint32_t *pk = reinterpret_cast<uint32_t *>(packed);
-  if (D <= 64)
+  const bool vec_ok = !spikes && (x_dtype == SPK_BF16 || x_dtype == SPK_F16) && D % 64 == 0 &&
+                      x_strides[3] == 1 && (x_strides[0] % 8) == 0 && (x_strides[1] % 8) == 0 &&
+                      (x_strides[2] % 8) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                      (packed_strides[0] % 2) == 0 && (packed_strides[1] % 2) == 0 &&
+                      (packed_strides[2] % 2) == 0 && (reinterpret_cast<uintptr_t>(packed) & 7) == 0;
+  if (vec_ok) {
+    const unsigned vgrid = grid_for(n_tok * H * (D / 64), 32);
+    uint64_t *pk64 = reinterpret_cast<uint64_t *>(packed);
+    if (x_dtype == SPK_BF16)
+      lif_pack_vec_kernel<SPK_BF16><<<vgrid, 256, 0, s>>>(p, x_strides[0], x_strides[1], x_strides[2], pk64,
+          packed_strides[0], packed_strides[1], packed_strides[2], slot_mapping, num_slots, n_tok, H, D);
+    else
+      lif_pack_vec_kernel<SPK_F16><<<vgrid, 256, 0, s>>>(p, x_strides[0], x_strides[1], x_strides[2], pk64,
+          packed_strides[0], packed_strides[1], packed_strides[2], slot_mapping, num_slots, n_tok, H, D);
+  } else if (D <= 64)
     lif_pack_kernel<1><<<grid, 256, 0, s>>>(p, x_strides[0], x_strides[1], x_strides[2], x_strides[3], pk,
                                             packed_strides[0], packed_strides[1], packed_strides[2],
                                             slot_mapping, num_slots, spikes, spike_dtype, n_tok, H, D);

@@ -24,6 +24,7 @@ def _rand_th(rng, n):
 @pytest.mark.parametrize("N", [64, 4864, 63])
 @pytest.mark.parametrize("T", [1, 2, 4, 8])
 def test_lif_multistep_bit_exact(T, N, M, gpu):
+    """fp32 in/out: the 16-byte vector path for N % 4 == 0, scalar for N = 63."""
     from spikeinfer_amd.kernels import lif_multistep
 
     rng = np.random.default_rng(1000 * T + 10 * N + M)
@@ -125,9 +126,11 @@ def test_pack_noncontiguous(gpu):
 
 
 # ---- fused LIF + pack + cache write ---------------------------------------
+@pytest.mark.parametrize("with_dense", [True, False])
 @pytest.mark.parametrize("D", [64, 32, 128, 40])
-@pytest.mark.parametrize("in_dtype", [torch.bfloat16, torch.float32])
-def test_lif_pack_write_packed_buffer(D, in_dtype, gpu):
+@pytest.mark.parametrize("in_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_lif_pack_write_packed_buffer(D, in_dtype, with_dense, gpu):
+    """Vectorised (16-byte, D % 64 == 0, no dense output) and scalar paths."""
     from spikeinfer_amd.kernels import lif_pack_write
 
     rng = np.random.default_rng(D)
@@ -138,14 +141,15 @@ def test_lif_pack_write_packed_buffer(D, in_dtype, gpu):
     x = proj.to(in_dtype).view(T, n_tok, H, D)
     W = (D + 31) // 32
     out = torch.zeros((T, n_tok, H, W), dtype=torch.int32, device=gpu)
-    dense = torch.empty((T, n_tok, H, D), dtype=in_dtype, device=gpu)
+    dense = torch.empty((T, n_tok, H, D), dtype=in_dtype, device=gpu) if with_dense else None
     lif_pack_write(x, torch.from_numpy(beta).to(gpu), torch.from_numpy(th).to(gpu), out,
                    spikes_out=dense)
     want = np.zeros((T, n_tok, H, W), np.int32)
     orc.lif_pack_write(x.float().cpu().numpy(), beta, th, want)
     assert np.array_equal(out.cpu().numpy(), want)
-    ws, _ = orc.lif(x.float().cpu().numpy(), beta, th)
-    assert np.array_equal(dense.to(torch.uint8).cpu().numpy(), ws)
+    if with_dense:
+        ws, _ = orc.lif(x.float().cpu().numpy(), beta, th)
+        assert np.array_equal(dense.to(torch.uint8).cpu().numpy(), ws)
 
 
 def test_lif_pack_write_cache_scatter(gpu):
@@ -184,3 +188,20 @@ def test_lif_pack_write_matches_reference_composition(gpu):
     comp = torch.zeros_like(fused)
     comp.index_copy_(2, slots, pack_spikes(spk))
     assert torch.equal(fused, comp)
+
+
+@pytest.mark.parametrize("in_dtype", [torch.bfloat16, torch.float16])
+def test_lif_gate_vector_path(in_dtype, gpu):
+    """Config-2 MLP-gate shape, reduced: [T, tokens, 4864] half-precision in and
+    out (16-byte vector path), beta 0.9, threshold 1.0."""
+    from spikeinfer_amd.kernels import lif_multistep
+
+    rng = np.random.default_rng(2)
+    x = torch.from_numpy(rng.standard_normal((4, 96, 4864)).astype(np.float32)).to(gpu).to(in_dtype)
+    beta = torch.full((4864,), 0.9, device=gpu)
+    th = torch.full((4864,), 1.0, device=gpu)
+    s, u = lif_multistep(x, beta, th, return_membrane=True)
+    assert s.dtype == in_dtype
+    ws, wu = orc.lif(x.float().cpu().numpy(), beta.cpu().numpy(), th.cpu().numpy())
+    assert np.array_equal(s.float().cpu().numpy().astype(np.uint8), ws)
+    assert np.array_equal(u.cpu().numpy(), wu)
