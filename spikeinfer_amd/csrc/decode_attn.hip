@@ -162,26 +162,30 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_general(AttnParams p
   }
 }
 
-// Sums the partitions of every split sequence (fixed order) and normalises.
-__global__ __launch_bounds__(128) void decode_attn_combine(AttnParams p) {
-  const int row = blockIdx.x;  // (t, n, hq)
-  const int hq = row % p.Hq;
-  const int n = (row / p.Hq) % p.N;
-  const int t = row / (p.Hq * p.N);
+// Sums the partitions of every split sequence (fixed order) and normalises:
+// one thread per output element (t, n, hq, channel), so the few split rows of
+// a batch fill the GPU without one workgroup per row.
+__global__ __launch_bounds__(256) void decode_attn_combine(AttnParams p) {
+  const int hd = p.head_dim;
+  const int64_t total = (int64_t)p.T * p.N * p.Hq * hd;
+  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (e >= total) return;
+  const int ch = static_cast<int>(e % hd);
+  const int64_t row = e / hd;  // (t, n, hq)
+  const int hq = static_cast<int>(row % p.Hq);
+  const int n = static_cast<int>((row / p.Hq) % p.N);
+  const int t = static_cast<int>(row / ((int64_t)p.Hq * p.N));
   const int len = p.lens[n];
   const int nparts = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
   if (nparts <= 1) return;
-  const int hd = p.head_dim;
   const int64_t stride_part = (int64_t)p.T * p.N * p.Hq * (hd + 1);
-  const float *src = p.ws + (((int64_t)t * p.N + n) * p.Hq + hq) * (hd + 1);
-  for (int ch = threadIdx.x; ch < hd; ch += blockDim.x) {
-    float a = 0.f, l = 0.f;
-    for (int q = 0; q < nparts; ++q) {
-      a += src[q * stride_part + ch];
-      l += src[q * stride_part + hd];
-    }
-    store_f32_as(p.out, t * p.os0 + n * p.os1 + hq * p.os2 + ch * p.os3, p.out_dtype, a / l);
+  const float *src = p.ws + row * (hd + 1);
+  float a = 0.f, l = 0.f;
+  for (int q = 0; q < nparts; ++q) {
+    a += src[q * stride_part + ch];
+    l += src[q * stride_part + hd];
   }
+  store_f32_as(p.out, t * p.os0 + n * p.os1 + hq * p.os2 + ch * p.os3, p.out_dtype, a / l);
 }
 
 // Integer scores popc(q & k) for every valid position (score-path check).
@@ -305,7 +309,8 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
   }
   if ((rc = check_launch("decode_attn"))) return rc;
   if (p.num_parts > 1) {
-    decode_attn_combine<<<dim3(T * N * Hq), 128, 0, s>>>(p);
+    const int64_t elems = (int64_t)T * N * Hq * head_dim;
+    decode_attn_combine<<<static_cast<unsigned>((elems + 255) / 256), 256, 0, s>>>(p);
     if ((rc = check_launch("decode_attn_combine"))) return rc;
   }
   return SPK_OK;
