@@ -244,10 +244,10 @@ extern "C" size_t spk_decode_attn_workspace_bytes(int T, int N, int Hq, int Hkv,
   const int64_t ctx_max = (int64_t)max_blocks * block_size;
   const int part = choose_part_len((int64_t)N * T * Hkv, ctx_max, block_size);
   const int64_t nparts = (ctx_max + part - 1) / part;
-  if (nparts <= 1) return 0;
-  // Partial sums, then the launch order of the matrix-core path.
-  return (size_t)nparts * T * N * Hq * (head_dim + 1) * sizeof(float) +
-         ((size_t)nparts * N * T * Hkv + 1) * sizeof(int32_t);
+  // Partial sums of split contexts, then the launch order of long contexts.
+  const size_t partials = nparts <= 1 ? 0 : (size_t)nparts * T * N * Hq * (head_dim + 1) * sizeof(float);
+  const size_t order = plan_launch(ctx_max) ? ((size_t)nparts * N * T * Hkv + 1) * sizeof(int32_t) : 0;
+  return partials + order;
 }
 
 extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], const int32_t *k_cache,
@@ -289,6 +289,7 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
   p.part_len = choose_part_len((int64_t)N * T * Hkv, ctx_max, block_size);
   p.num_parts = (int)((ctx_max + p.part_len - 1) / p.part_len);
   p.ws = static_cast<float *>(workspace);
+  if (p.ws == nullptr && need > 0) return fail(SPK_EINVAL, "workspace required");
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   dim3 grid(N * T * Hkv, p.num_parts);
@@ -297,9 +298,8 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
   const bool force_general = path && strcmp(path, "general") == 0;
   if (!force_general && mfma_path_supported(p)) {
     build_digit_table(scale, p.digits);
-    int32_t *order = p.num_parts > 1
-        ? reinterpret_cast<int32_t *>(p.ws + (size_t)p.num_parts * T * N * Hq * (head_dim + 1))
-        : nullptr;
+    const size_t partial_floats = p.num_parts > 1 ? (size_t)p.num_parts * T * N * Hq * (head_dim + 1) : 0;
+    int32_t *order = plan_launch(ctx_max) ? reinterpret_cast<int32_t *>(p.ws + partial_floats) : nullptr;
     launch_decode_mfma(p, order, s);
   } else switch (W) {
     case 1: launch_general<1>(p, grid, s); break;

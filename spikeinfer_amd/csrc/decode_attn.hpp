@@ -7,6 +7,9 @@
 namespace spk {
 
 constexpr int kAttnThreads = 256;   // 4 waves
+// Block-table entries of one partition staged in LDS by the matrix-core
+// kernel; choose_part_len never makes a partition span more blocks.
+constexpr int kMaxStagedBlocks = 2048;
 constexpr int kMaxRep = 16;
 
 struct AttnParams {
@@ -44,9 +47,9 @@ void build_digit_table(float scale, uint32_t digits[65]);
 // Partition length: long contexts are split so the grid has enough
 // workgroups and no single workgroup walks a 32k-token context alone.
 inline int choose_part_len(int64_t units, int64_t ctx_max, int block_size) {
-  int part = 16384;
-  // At most 1024 block-table entries per partition (they are staged in LDS).
-  while (part > block_size * 1024 && part > 256) part >>= 1;
+  int part = 32768;
+  // At most kMaxStagedBlocks block-table entries per partition.
+  while (part > block_size * kMaxStagedBlocks && part > 256) part >>= 1;
   // Small decode batches: shorten partitions (down to 512) until the grid
   // holds about four workgroups per CU.
   while (part > 512 && part > block_size && units * ((ctx_max + part - 1) / part) < 1024) part >>= 1;
@@ -56,8 +59,10 @@ inline int choose_part_len(int64_t units, int64_t ctx_max, int block_size) {
 // Matrix-core path for head_dim 64, n_rep <= 8 (decode_attn_mfma.hip).
 // Returns false when the shape or alignment does not qualify.
 bool mfma_path_supported(const AttnParams &p);
-// Launches the matrix-core kernel, preceded, when p.num_parts > 1, by the
-// planner that fills `order` (units * num_parts + 1 ints of scratch).
+// Launches the matrix-core kernel, preceded, for long contexts
+// (plan_launch), by the planner that fills `order` (units * num_parts + 1
+// ints of scratch).
+inline bool plan_launch(int64_t ctx_max) { return ctx_max >= 8192; }
 void launch_decode_mfma(AttnParams p, int32_t *order, hipStream_t s);
 
 }  // namespace spk

@@ -45,7 +45,7 @@ namespace mfma {
 
 constexpr int kWaves = 4;
 constexpr int kStepTokens = 128;      // tokens per wave step (2 per lane)
-constexpr int kMaxPartBlocks = 1024;   // block-table entries staged per partition
+constexpr int kMaxPartBlocks = kMaxStagedBlocks;  // block-table entries staged per partition
 
 // Stage of one wave step.  Row r holds token 2r (r < 64) or token
 // 2(r-64)+1 (r >= 64) of the step, so lane l writes rows l and l+64 and every
@@ -422,7 +422,7 @@ namespace mfma {
 __global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, int N, int UPS,
                                                         int part_len, int num_parts,
                                                         int32_t *order) {
-  constexpr int kMaxBuckets = 66;  // part_len <= 16384 tokens, 256 per bucket
+  constexpr int kMaxBuckets = 130;  // part_len <= 32768 tokens, 256 per bucket
   __shared__ int count[kMaxBuckets];
   __shared__ int offset[kMaxBuckets];
   const int tid = threadIdx.x;
@@ -468,7 +468,7 @@ void launch_decode_mfma(AttnParams p, int32_t *order, hipStream_t s) {
   const int units = p.N * p.T * p.Hkv;
   dim3 grid(units, p.num_parts);
   p.order = nullptr;
-  if (p.num_parts > 1 && order) {
+  if (order) {
     mfma::decode_attn_plan<<<1, 1024, 0, s>>>(p.lens, p.N, p.T * p.Hkv, p.part_len, p.num_parts,
                                               order);
     p.order = order;

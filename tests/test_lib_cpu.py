@@ -64,9 +64,13 @@ def test_workspace_sizing():
     lib = _lib.load()
     # config 3 shape: one partition, no workspace
     assert lib.spk_decode_attn_workspace_bytes(4, 64, 14, 2, 64, 16, 12) == 0
-    # config 4 shape: 32k context splits into partitions of partial sums
+    # config 4 shape: whole-sequence partitions, longest-first launch order
+    # (one int per work item + the item count)
     ws = lib.spk_decode_attn_workspace_bytes(4, 256, 14, 2, 64, 16, 2048)
-    assert ws > 0 and ws % (4 * 256 * 14 * 65 * 4) == 0
+    assert ws == (256 * 4 * 2 + 1) * 4
+    # a small batch of long contexts splits them: partial sums + order
+    ws = lib.spk_decode_attn_workspace_bytes(4, 8, 14, 2, 64, 16, 2048)
+    assert ws > 8 * 4 * 14 * 65 * 4
 
 
 def test_python_api_refuses_cpu_tensors():
