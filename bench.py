@@ -30,6 +30,20 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_attn_mfma_config4_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the config-4 decode kernel, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (copy-kernel calibrated), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 T, HQ, HKV, D, BS = 4, 14, 2, 64, 16
 
 
@@ -265,7 +279,9 @@ def main():
                    "block_size": BS, "density": 0.2, "out_dtype": "f32",
                    "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
+                     "kernel": "decode_attn_mfma_kernel<7> (+ its 5 us planner, timed together)"},
         "cpu_baseline": cpu,
         "extras": extras,
     }

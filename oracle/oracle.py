@@ -178,3 +178,28 @@ def brute_attn(q, k, v, tables, lens, head_dim, block_size, num_q_heads, num_kv_
                 for d in range(head_dim):
                     out[t, n, h, d] = sum(e[j] * int(vb[t, kvh, slots[j], d]) for j in range(L)) / z
     return out
+
+
+def prefill_attn(q_bits, k_cache, v_cache, table, context_len, head_dim, block_size,
+                 num_q_heads, num_kv_heads):
+    """One prefill chunk (spikeinfer/attention.py:161-178): ``q_bits`` 0/1
+    ``[T, Hq, q_len, D]`` at positions ``[context_len, context_len + q_len)``,
+    attending causally to the sequence's cached positions ``[0, context_len +
+    q_len)`` read through ``table`` (slot = table[p // bs] * bs + p % bs,
+    block_manager.py:71-77).  Float64 textbook softmax over the unpacked bits,
+    max-subtracted; returns ``[T, Hq, q_len, D]``."""
+    T, _, q_len, _ = q_bits.shape
+    total = context_len + q_len
+    nrep = num_q_heads // num_kv_heads
+    pos = np.arange(total)
+    slots = np.asarray(table, np.int64)[pos // block_size] * block_size + pos % block_size
+    kb = np_unpack(k_cache[:, :, slots], head_dim).astype(np.float64)  # [T, Hkv, total, D]
+    vb = np_unpack(v_cache[:, :, slots], head_dim).astype(np.float64)
+    kb = np.repeat(kb, nrep, axis=1)
+    vb = np.repeat(vb, nrep, axis=1)
+    s = np.einsum("thqd,thkd->thqk", q_bits.astype(np.float64), kb) / math.sqrt(head_dim)
+    visible = pos[None, :] <= (context_len + np.arange(q_len))[:, None]  # [q_len, total]
+    s = np.where(visible, s, -np.inf)
+    s -= s.max(axis=-1, keepdims=True)
+    e = np.exp(s)
+    return np.einsum("thqk,thkd->thqd", e, vb) / e.sum(axis=-1, keepdims=True)

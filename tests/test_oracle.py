@@ -253,3 +253,37 @@ def test_softmax_is_shift_invariant_closed_form():
     w0 = 1 / (1 + math.exp(-7 / 8))
     np.testing.assert_allclose(out[0, 0, 0, :2], [w0, 1 - w0], rtol=1e-14)
     assert np.all(out[0, 0, 0, 2:] == 0)
+
+
+# ---- prefill chunk oracle --------------------------------------------------
+def _prefill_case(ctx, q_len, seed=3, T=2, Hq=4, Hkv=2, D=64, bs=4):
+    c = attn_case([ctx + q_len], block_size=bs, T=T, q_heads=Hq, kv_heads=Hkv,
+                  head_dim=D, seed=seed)
+    rng = np.random.default_rng(seed + 100)
+    q_bits = random_bits(rng, (T, Hq, q_len, D), 0.4)
+    return c, q_bits
+
+
+@pytest.mark.parametrize("ctx,q_len", [(0, 1), (0, 7), (5, 3), (13, 6)])
+def test_prefill_rows_equal_decode_at_their_length(ctx, q_len):
+    """Row i of a chunk sees exactly positions [0, ctx + i], so it must equal an
+    independent decode (C oracle) with seq_len = ctx + i + 1."""
+    c, q_bits = _prefill_case(ctx, q_len)
+    got = orc.prefill_attn(q_bits, c["k"], c["v"], c["tables"][0], ctx, 64, 4, 4, 2)
+    for i in range(q_len):
+        q = orc.np_pack(q_bits[:, :, i][:, None])  # [T, 1, Hq, W]
+        want = orc.decode_attn(q, c["k"], c["v"], c["tables"], np.array([ctx + i + 1], np.int32),
+                               64, 4, 4, 2)
+        np.testing.assert_allclose(got[:, :, i], want[:, 0], rtol=0, atol=1e-12)
+
+
+def test_prefill_zero_query_is_running_mean():
+    c, q_bits = _prefill_case(4, 5)
+    q_bits[:] = 0
+    got = orc.prefill_attn(q_bits, c["k"], c["v"], c["tables"][0], 4, 64, 4, 4, 2)
+    pos = np.arange(9)
+    slots = c["tables"][0][pos // 4] * 4 + pos % 4
+    vb = orc.np_unpack(c["v"][:, :, slots], 64).astype(np.float64)  # [T, Hkv, 9, D]
+    for i in range(5):
+        want = vb[:, :, : 4 + i + 1].mean(axis=2)  # [T, Hkv, D]
+        np.testing.assert_allclose(got[:, :, i], np.repeat(want, 2, axis=1), atol=1e-12)
