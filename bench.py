@@ -10,8 +10,10 @@ combine), inputs resident in HBM.
 
 Also reported: the density sweep {0.05, 0.2, 0.5} (runtime must be flat),
 config 3 (batch 64, ctx U[128,192], 24 layers -> attention time per decode
-step), config 2 (fused LIF + pack + cache write, 4096 tokens), and the CPU
-oracle timed on a bounded sample of config 4 on the host cores.
+step), config 2 (fused LIF + pack + cache write, 4096 tokens), config 5 (decode
+tok/s of the whole spiking decoder step at batch 64, replayed from one
+hipGraph), and the CPU oracle timed on a bounded sample of config 4 on the host
+cores.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip-extras]
 """
@@ -210,6 +212,50 @@ def bench_lif(steps, warmup, dev):
     }
 
 
+def bench_decode_step(steps, warmup, dev):
+    """Config 5: random-init Qwen2.5-0.5B-shaped spiking decoder (bf16 weights
+    N(0, 0.02)), batch 64, 128-token random prompts, T=4; one decode step
+    (24 layers + lm_head + sampling with temperature 0.8 / top-k 50 / top-p 0.9
+    / repetition 1.1 + device-side advance) replayed from one hipGraph.  Prefill
+    is eager and untimed.  tok/s = 64 tokens per step / step time."""
+    from spikeinfer_amd.model import SpikingDecoder, SpikingQwenConfig
+    from spikeinfer_amd.runner import DecodeRunner
+    from spikeinfer_amd.sampler import SamplingParams
+    from spikeinfer_amd.spike_cache import PagedSpikeCache
+
+    cfg = SpikingQwenConfig()
+    B, plen = 64, 128
+    new = warmup + steps + 1
+    model = SpikingDecoder(cfg, device=dev, seed=5000)
+    max_len = plen + new + 1
+    blocks = B * math.ceil(max_len / BS) + 1
+    cache = PagedSpikeCache(cfg.num_hidden_layers, cfg.T, cfg.num_key_value_heads, cfg.head_dim,
+                            blocks, BS, device=dev)
+    runner = DecodeRunner(model, cache, B, max_len, max_new_tokens=new + 1)
+    g = torch.Generator().manual_seed(5001)
+    prompts = torch.randint(0, cfg.vocab_size, (B, plen), generator=g).tolist()
+    params = [SamplingParams(temperature=0.8, top_k=50, top_p=0.9, repetition_penalty=1.1)] * B
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    runner.start(prompts, params, shuffle_blocks=5002)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    runner.capture()
+    stream = torch.cuda.current_stream(dev)
+    ms = time_calls(lambda: runner.replay(1), steps, warmup, stream)
+    toks = runner.history[:B, :steps + warmup + 1]
+    return {
+        "decode_tok_s": round(B / ms * 1000, 1),
+        "ms_per_step": round(ms, 4),
+        "weight_gbs": round(model.weight_bytes / ms / 1e6, 1),
+        "weight_bytes_per_step": model.weight_bytes,
+        "prefill_s_eager": round(prefill_s, 3),
+        "batch": B, "prompt_len": plen, "T": cfg.T,
+        "sampling": "temperature 0.8, top_k 50, top_p 0.9, repetition 1.1 (on device)",
+        "distinct_tokens": int(torch.unique(toks).numel()),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,6 +295,8 @@ def main():
         del c3
         print("config 2", file=sys.stderr, flush=True)
         extras["config2_lif"] = bench_lif(args.steps, args.warmup, dev)
+        print("config 5", file=sys.stderr, flush=True)
+        extras["config5_decode"] = bench_decode_step(args.steps, args.warmup, dev)
     if args.calib_copy_mib:
         src = torch.empty(args.calib_copy_mib << 18, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)

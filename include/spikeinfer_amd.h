@@ -169,6 +169,111 @@ int spk_pack(const void *x, int x_dtype, int64_t x_row_stride, int32_t *out,
 int spk_unpack(const int32_t *words, int64_t rows, int C, void *out,
                int out_dtype, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Decoder-step operators around the GEMMs (whole-step decode, hipGraph).
+ * ------------------------------------------------------------------------ */
+
+/*
+ * Residual add + RMSNorm over rows of `hidden` contiguous elements, dtype in
+ * {F32, F16, BF16}.  When delta != NULL, h <- round(h + delta) in place; then
+ * out = round(weight * round(x * rsqrt(mean(x^2) + eps))), x = float(h).
+ * Replaces `h = h + sublayer(...)` followed by Qwen2RMSNorm
+ * (spikeinfer/modeling_fast.py:206-211).  Buffers 16-byte aligned.
+ */
+int spk_add_rmsnorm(void *h, const void *delta, const void *weight, void *out,
+                    int dtype, int64_t rows, int hidden, float eps, void *stream);
+
+/*
+ * Final RMSNorm and rate-coded readout: h [T, rows, hidden] contiguous ->
+ * out [rows, hidden] = round(sum_t RMSNorm(h_t) * (1/T)), 1 <= T <= 8.
+ * Replaces `self.norm(h).mean(dim=0)` (spikeinfer/modeling_fast.py:319).
+ */
+int spk_rmsnorm_mean_t(const void *h, const void *weight, void *out, int dtype,
+                       int T, int64_t rows, int hidden, float eps, void *stream);
+
+/*
+ * Fused q/k/v site of one attention layer: RoPE -> LIF -> bit-pack -> packed
+ * q buffer and paged k/v cache slots.  Replaces _apply_rope_t + three
+ * lif_multistep calls (spikeinfer/modeling_fast.py:89-99, :121-135) and the
+ * packing / cache scatter of paged_attention (spikeinfer/attention.py:138-149).
+ *
+ *   x        x_dtype (BF16/F16) [T, n_tok, (Hq + 2*Hkv) * D], channel stride 1,
+ *            strides {t, token} in elements: q heads, then k, then v heads
+ *            (the concatenated q/k/v projection output)
+ *   cos, sin x_dtype [n_tok, D] contiguous (rotary tables of each token)
+ *   beta, threshold  param_dtype [3, D] contiguous: q, k and v sites
+ *   q_packed int32 [T, n_q, Hq, W] at q_strides: tokens [0, n_q) (the decode
+ *            prefix) are packed here
+ *   k_cache, v_cache int32 [T, Hkv, num_slots, W] at cache_strides; token i
+ *            goes to slot_mapping[i] (outside [0, num_slots): skipped)
+ *   dense_q/k/v optional x_dtype [T, H, n_tok, D] contiguous 0/1 spikes (the
+ *            prefill path's SDPA operands), NULL to skip
+ * RoPE is evaluated as the composition rounds it: round(round(x*cos) +
+ * round(rotate_half(x)*sin)).  D is a power of two in [64, 512].
+ */
+int spk_qkv_rope_lif_pack(const void *x, int x_dtype, const int64_t x_strides[2],
+                          const void *cos, const void *sin, const void *beta,
+                          const void *threshold, int param_dtype, int32_t *q_packed,
+                          const int64_t q_strides[3], int64_t n_q, int32_t *k_cache,
+                          int32_t *v_cache, const int64_t cache_strides[3],
+                          const int64_t *slot_mapping, int64_t num_slots, void *dense_q,
+                          void *dense_k, void *dense_v, int T, int64_t n_tok, int Hq,
+                          int Hkv, int D, void *stream);
+
+/*
+ * MLP gate: x [T, rows, 2*I] (gate in columns [0, I), up in [I, 2I); strides
+ * {t, row} in elements, channel stride 1) -> out [T, rows, I] contiguous =
+ * round(LIF(gate) * up).  Replaces lif_multistep(gate_proj(x)) * up_proj(x)
+ * (spikeinfer/modeling_fast.py:186-190) after one concatenated GEMM.
+ */
+int spk_lif_gate_mul(const void *x, int dtype, const int64_t x_strides[2],
+                     const void *beta, const void *threshold, int param_dtype,
+                     void *out, int T, int64_t rows, int I, void *stream);
+
+/*
+ * Device-side advance of a decode batch after sampling: for rows i < n_live,
+ * where n_live = n_rows, or min(n_rows, *live) when `live` is given (a device
+ * count, so a captured step serves any live batch up to n_rows),
+ * input_ids[i] = next_tokens[i], positions[i] += 1, seq_lens[i] =
+ * positions[i] + 1, slot_mapping[i] = table[i][pos / bs] * bs + pos % bs
+ * (spikeinfer/engine/model_runner.py:89-100, block_manager.py:71-77).  A row
+ * whose next position is past its table stays put.  When history != NULL,
+ * next_tokens[i] is also stored at history[i * hist_cap + *step] and *step is
+ * incremented.  No reference counterpart as a kernel: the reference rebuilds
+ * these tensors on the host every step.
+ */
+int spk_decode_advance(const int64_t *next_tokens, int64_t *input_ids, int64_t *positions,
+                       int32_t *seq_lens, int64_t *slot_mapping, const int32_t *block_tables,
+                       int64_t bt_stride0, int64_t bt_stride1, int max_blocks,
+                       int block_size, int n_rows, const int32_t *live, int64_t *history,
+                       int32_t *step, int hist_cap, void *stream);
+
+/*
+ * Batched sampler, one workgroup per row (spikeinfer/engine/sampler.py:48-177):
+ * penalties over the row's generated tokens (repetition, then presence +
+ * frequency), temperature, min_p, top_k, top_p, then a draw.  Per-row
+ * parameters are device arrays of `rows` entries (NULL = disabled: top_k -1,
+ * top_p 1, min_p 0, penalties neutral).  Rows with temperature < 1e-5 take the
+ * argmax of the penalised logits (lowest index on ties).
+ *
+ * Equal logits are ordered by index (the reference leaves that order to
+ * torch.topk).  The draw is the inverse CDF, in index order, of the kept
+ * softmax weights at uniforms[row] in [0, 1).  history int64 [rows,
+ * history_stride] holds generated tokens, history_len[row *
+ * history_len_stride] of them (stride 0: one count for every row; at most
+ * 2048 are used).  vocab <= 262144.  Result: out_tokens int64 [rows].
+ */
+int spk_sample(const void *logits, int logits_dtype, int64_t row_stride, int rows, int vocab,
+               const float *temperature, const int32_t *top_k, const float *top_p,
+               const float *min_p, const float *repetition_penalty,
+               const float *presence_penalty, const float *frequency_penalty,
+               const int64_t *history, int64_t history_stride, const int32_t *history_len,
+               int64_t history_len_stride, const float *uniforms, int64_t *out_tokens,
+               void *stream);
+
+/* LDS bytes one spk_sample workgroup uses (for occupancy planning). */
+size_t spk_sample_shared_bytes(void);
+
 #ifdef __cplusplus
 }
 #endif

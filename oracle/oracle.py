@@ -203,3 +203,68 @@ def prefill_attn(q_bits, k_cache, v_cache, table, context_len, head_dim, block_s
     s -= s.max(axis=-1, keepdims=True)
     e = np.exp(s)
     return np.einsum("thqk,thkd->thqd", e, vb) / e.sum(axis=-1, keepdims=True)
+
+
+# ---- sampling ----------------------------------------------------------------
+def sample_row(logits, temperature=1.0, top_k=-1, top_p=1.0, min_p=0.0, rep=1.0,
+               presence=0.0, frequency=0.0, history=(), u=0.0):
+    """One row of spikeinfer/engine/sampler.py:48-177 in numpy.
+
+    Penalties in float32 over the generated tokens (:98-119: repetition
+    ``v / r if v > 0 else v * r``, then ``v - (presence + frequency * count)``),
+    ``x = v / temperature`` in float32 (:69-75), then in float64: min_p on the
+    softmax (:137-141), top_k on the descending order (:143-153), top_p on the
+    mass strictly before each token (:155-159).  Equal values are ordered by
+    index (a stable sort; the reference leaves it to torch.topk).  The draw is
+    the first index, in index order, whose inclusive cumulative kept weight
+    exceeds ``u`` times the total.
+
+    Returns (token, kept bool mask, kept probabilities, margin): ``margin`` is
+    the smallest distance of a filter cut (min_p, top_p) from its decision
+    boundary -- below ~1e-6 the float32 kernel may legitimately decide the
+    other way.  The draw's own boundaries are the cumulative sums of the
+    returned probabilities.
+    """
+    v = np.asarray(logits, np.float32).copy()
+    counts = {}
+    for t in history:
+        counts[int(t)] = counts.get(int(t), 0) + 1
+    for t, c in counts.items():
+        if rep != 1.0:
+            v[t] = v[t] / np.float32(rep) if v[t] > 0 else v[t] * np.float32(rep)
+        if presence or frequency:
+            v[t] = v[t] - (np.float32(presence) + np.float32(frequency) * np.float32(c))
+    V = v.shape[0]
+    if temperature < 1e-5:
+        tok = int(np.argmax(v))
+        kept = np.zeros(V, bool)
+        kept[tok] = True
+        return tok, kept, kept.astype(np.float64), np.inf
+    x = (v / np.float32(temperature)).astype(np.float32)
+    m = float(x.max())
+    w = np.exp(x.astype(np.float64) - m)
+    margin = np.inf
+    alive = np.ones(V, bool)
+    if min_p > 0:
+        alive = w >= min_p
+        margin = min(margin, float(np.min(np.abs(w - min_p))))
+    order = np.lexsort((np.arange(V), -x.astype(np.float64)))  # value desc, index asc
+    order = order[alive[order]]
+    if 0 < top_k < len(order):
+        order = order[:top_k]
+    if top_p < 1.0:
+        p = w[order] / w[order].sum()
+        before = np.cumsum(p) - p
+        keep = before < top_p
+        margin = min(margin, float(np.min(np.abs(before - top_p))))
+        order = order[keep]
+    kept = np.zeros(V, bool)
+    kept[order] = True
+    probs = np.where(kept, w, 0.0)
+    probs /= probs.sum()
+    cdf = np.cumsum(probs)
+    tok = int(np.searchsorted(cdf, u, side="right"))
+    tok = min(tok, V - 1)
+    while not kept[tok]:  # u landed exactly on a boundary of zero-weight entries
+        tok += 1
+    return tok, kept, probs, margin

@@ -9,6 +9,7 @@
 // exactly as PyTorch eager does, or a membrane that lands within an ulp of the
 // threshold flips its spike.
 #include "common.hpp"
+#include "lif_math.hpp"
 
 namespace spk {
 
@@ -21,15 +22,6 @@ struct LifParams {
   int T;
 };
 
-// One LIF step on the fp32 membrane; returns the spike.  The delayed reset
-// uses the membrane of the previous step (lif_triton.py:98-101).
-__device__ __forceinline__ bool lif_step(float &u, float cur, float beta, float th) {
-  const float r = (u - th > 0.f) ? 1.f : 0.f;
-  u = (beta * u + cur) - r * th;
-  return u - th > 0.f;
-}
-
-__device__ __forceinline__ float clamp01(float b) { return fminf(fmaxf(b, 0.f), 1.f); }
 
 // ---- dense LIF: [T, M, N] -> spikes [T, M, N] -----------------------------
 __global__ __launch_bounds__(256) void lif_dense_kernel(LifParams p, int64_t xs0, int64_t xs1,
@@ -116,26 +108,6 @@ __global__ __launch_bounds__(256) void lif_pack_kernel(LifParams p, int64_t xs0,
 
 // ---- vectorised paths: 16 bytes per lane ---------------------------------
 constexpr int kTBatch = 4;  // timesteps whose loads are issued together
-// Element types of the vector paths.
-template <int DT> struct Elem;
-template <> struct Elem<SPK_F32> { typedef float T; static constexpr int kVec = 4; };
-template <> struct Elem<SPK_F16> { typedef uint16_t T; static constexpr int kVec = 8; };
-template <> struct Elem<SPK_BF16> { typedef uint16_t T; static constexpr int kVec = 8; };
-
-template <int DT>
-__device__ __forceinline__ float elem_to_f32(typename Elem<DT>::T v) {
-  if constexpr (DT == SPK_F32) return v;
-  else if constexpr (DT == SPK_BF16) return bf16_bits_to_f32(v);
-  else return static_cast<float>(__builtin_bit_cast(_Float16, v));
-}
-
-template <int DT>
-__device__ __forceinline__ typename Elem<DT>::T spike_elem(bool s) {
-  if constexpr (DT == SPK_F32) return s ? 1.f : 0.f;
-  else if constexpr (DT == SPK_BF16) return s ? 0x3f80 : 0;
-  else return s ? 0x3c00 : 0;
-}
-
 // Dense LIF over rows of N contiguous channels (N % kVec == 0, 16-byte aligned
 // rows): each thread owns kVec consecutive channels of one row, loads and
 // stores 16 bytes per timestep.  Spikes are written in the input's dtype.

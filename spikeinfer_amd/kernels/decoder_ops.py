@@ -1,0 +1,207 @@
+"""Decoder-step operators around the GEMMs (HIP, through the C-ABI).
+
+Each replaces a torch composition of the reference's layer-major forward
+(spikeinfer/modeling_fast.py) with one launch; shapes follow that forward's
+flattened, paged form ``[T, n_tok, ...]``.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+_VEC_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def _contig_rows(t: torch.Tensor, name: str) -> None:
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def add_rmsnorm(h: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tensor,
+                eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``h += delta`` (in place, rounded to h's dtype), then Qwen2RMSNorm(h).
+
+    ``h``/``delta``/``out`` ``[..., hidden]`` contiguous, ``weight [hidden]``.
+    Returns ``out`` (allocated like ``h`` when None).
+    """
+    dev = _lib.require_gpu(h, delta, weight, out)
+    if h.dtype not in _VEC_DTYPES:
+        raise ValueError(f"add_rmsnorm: unsupported dtype {h.dtype}")
+    for name, t in (("h", h), ("delta", delta), ("weight", weight), ("out", out)):
+        if t is not None:
+            _contig_rows(t, name)
+            if t.dtype != h.dtype:
+                raise ValueError(f"add_rmsnorm: {name} is {t.dtype}, h is {h.dtype}")
+    if delta is not None and delta.shape != h.shape:
+        raise ValueError(f"add_rmsnorm: delta {tuple(delta.shape)} vs h {tuple(h.shape)}")
+    hidden = h.shape[-1]
+    if weight.numel() != hidden:
+        raise ValueError(f"add_rmsnorm: weight has {weight.numel()} entries, hidden is {hidden}")
+    if out is None:
+        out = torch.empty_like(h)
+    _lib.check(
+        _lib.load().spk_add_rmsnorm(
+            h.data_ptr(), _lib.ptr(delta), weight.data_ptr(), out.data_ptr(),
+            _lib.dtype_code(h.dtype), h.numel() // hidden, hidden, float(eps), _lib.stream_of(dev),
+        ),
+        "add_rmsnorm",
+    )
+    return out
+
+
+def rmsnorm_mean_t(h: torch.Tensor, weight: torch.Tensor, eps: float,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """``RMSNorm(h).mean(dim=0)`` for ``h [T, rows, hidden]`` contiguous."""
+    dev = _lib.require_gpu(h, weight, out)
+    if h.ndim != 3:
+        raise ValueError("rmsnorm_mean_t: expected h as [T, rows, hidden]")
+    _contig_rows(h, "h")
+    T, rows, hidden = h.shape
+    if out is None:
+        out = torch.empty((rows, hidden), dtype=h.dtype, device=dev)
+    _lib.check(
+        _lib.load().spk_rmsnorm_mean_t(
+            h.data_ptr(), weight.data_ptr(), out.data_ptr(), _lib.dtype_code(h.dtype), T, rows,
+            hidden, float(eps), _lib.stream_of(dev),
+        ),
+        "rmsnorm_mean_t",
+    )
+    return out
+
+
+def qkv_rope_lif_pack(
+    qkv: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    beta: torch.Tensor,
+    threshold: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    num_q_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    q_packed: torch.Tensor | None = None,
+    n_q: int = 0,
+    dense: tuple[torch.Tensor | None, torch.Tensor | None, torch.Tensor | None] | None = None,
+) -> torch.Tensor | None:
+    """RoPE -> LIF -> pack for the q/k/v site of one layer.
+
+    Args:
+        qkv: ``[T, n_tok, (Hq + 2 Hkv) * D]`` concatenated projection output
+            (channel stride 1).
+        cos, sin: ``[n_tok, D]`` rotary tables in qkv's dtype.
+        beta, threshold: ``[3, D]`` (q, k, v sites).
+        k_cache, v_cache: the layer's ``int32 [T, Hkv, slots, W]`` caches;
+            token ``i`` is written at ``slot_mapping[i]``.
+        q_packed: ``int32 [T, n_q, Hq, W]`` receiving tokens ``[0, n_q)``.
+        dense: optional ``[T, H, n_tok, D]`` outputs of the 0/1 spikes per site.
+    Returns ``q_packed``.
+    """
+    dev = _lib.require_gpu(qkv, cos, sin, beta, threshold, k_cache, v_cache, slot_mapping, q_packed)
+    if qkv.ndim != 3 or qkv.stride(-1) != 1:
+        raise ValueError("qkv must be [T, n_tok, C] with a contiguous channel axis")
+    T, n_tok, C = qkv.shape
+    if C != (num_q_heads + 2 * num_kv_heads) * head_dim:
+        raise ValueError(f"qkv has {C} channels, expected {(num_q_heads + 2 * num_kv_heads) * head_dim}")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if tuple(t.shape) != (n_tok, head_dim) or not t.is_contiguous() or t.dtype != qkv.dtype:
+            raise ValueError(f"{name} must be a contiguous [{n_tok}, {head_dim}] {qkv.dtype} tensor")
+    beta = beta.reshape(3, head_dim).contiguous()
+    threshold = threshold.reshape(3, head_dim).to(beta.dtype).contiguous()
+    if slot_mapping.dtype != torch.int64:
+        slot_mapping = slot_mapping.to(torch.int64)
+    slot_mapping = slot_mapping.contiguous()
+    if slot_mapping.numel() < n_tok:
+        raise ValueError(f"slot_mapping has {slot_mapping.numel()} entries for {n_tok} tokens")
+    qs = _lib.strides(q_packed) if q_packed is not None else (_lib.ctypes.c_int64 * 3)(0, 0, 0)
+    if q_packed is not None:
+        if q_packed.dtype != torch.int32 or q_packed.ndim != 4 or q_packed.shape[0] != T \
+                or q_packed.shape[1] < n_q or q_packed.shape[2] != num_q_heads:
+            raise ValueError(f"q_packed must be int32 [T, >= {n_q}, {num_q_heads}, W]")
+        qs = (_lib.ctypes.c_int64 * 3)(*q_packed.stride()[:3])
+    elif n_q:
+        raise ValueError("n_q > 0 needs q_packed")
+    dq, dk, dv = dense if dense is not None else (None, None, None)
+    for t, H in ((dq, num_q_heads), (dk, num_kv_heads), (dv, num_kv_heads)):
+        if t is not None and (tuple(t.shape) != (T, H, n_tok, head_dim) or not t.is_contiguous()
+                              or t.dtype != qkv.dtype):
+            raise ValueError(f"dense spikes must be contiguous [T, {H}, {n_tok}, {head_dim}] {qkv.dtype}")
+    if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+        raise ValueError("k and v caches must have the same shape and strides")
+    _lib.check(
+        _lib.load().spk_qkv_rope_lif_pack(
+            qkv.data_ptr(), _lib.dtype_code(qkv.dtype), (_lib.ctypes.c_int64 * 2)(*qkv.stride()[:2]),
+            cos.data_ptr(), sin.data_ptr(), beta.data_ptr(), threshold.data_ptr(),
+            _lib.dtype_code(beta.dtype), _lib.ptr(q_packed), qs, n_q,
+            k_cache.data_ptr(), v_cache.data_ptr(), (_lib.ctypes.c_int64 * 3)(*k_cache.stride()[:3]),
+            slot_mapping.data_ptr(), k_cache.shape[2], _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+            T, n_tok, num_q_heads, num_kv_heads, head_dim, _lib.stream_of(dev),
+        ),
+        "qkv_rope_lif_pack",
+    )
+    return q_packed
+
+
+def lif_gate_mul(gate_up: torch.Tensor, beta: torch.Tensor, threshold: torch.Tensor,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """``LIF(gate) * up`` for ``gate_up [T, rows, 2I]`` (gate columns first).
+
+    Returns ``[T, rows, I]`` contiguous in gate_up's dtype.
+    """
+    dev = _lib.require_gpu(gate_up, beta, threshold, out)
+    if gate_up.ndim != 3 or gate_up.stride(-1) != 1:
+        raise ValueError("gate_up must be [T, rows, 2I] with a contiguous channel axis")
+    T, rows, I2 = gate_up.shape
+    I = I2 // 2
+    if I2 % 2 or beta.numel() != I or threshold.numel() != I:
+        raise ValueError(f"gate_up has {I2} channels; beta/threshold need {I} entries")
+    if out is None:
+        out = torch.empty((T, rows, I), dtype=gate_up.dtype, device=dev)
+    elif tuple(out.shape) != (T, rows, I) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{T}, {rows}, {I}]")
+    beta = beta.contiguous()
+    threshold = threshold.to(beta.dtype).contiguous()
+    _lib.check(
+        _lib.load().spk_lif_gate_mul(
+            gate_up.data_ptr(), _lib.dtype_code(gate_up.dtype),
+            (_lib.ctypes.c_int64 * 2)(*gate_up.stride()[:2]), beta.data_ptr(), threshold.data_ptr(),
+            _lib.dtype_code(beta.dtype), out.data_ptr(), T, rows, I, _lib.stream_of(dev),
+        ),
+        "lif_gate_mul",
+    )
+    return out
+
+
+def decode_advance(next_tokens, input_ids, positions, seq_lens, slot_mapping, block_tables,
+                   block_size: int, n_rows: int, live=None, history=None, step=None) -> None:
+    """Moves rows ``[0, n_live)`` of a decode batch to their next token on the
+    device (no host sync); ``n_live = min(n_rows, live[0])`` when the int32
+    device count ``live`` is given, else ``n_rows``."""
+    dev = _lib.require_gpu(next_tokens, input_ids, positions, seq_lens, slot_mapping, block_tables,
+                           live, history, step)
+    if live is not None and live.dtype != torch.int32:
+        raise ValueError("live must be an int32 device count")
+    for name, t, dt in (("next_tokens", next_tokens, torch.int64), ("input_ids", input_ids, torch.int64),
+                        ("positions", positions, torch.int64), ("seq_lens", seq_lens, torch.int32),
+                        ("slot_mapping", slot_mapping, torch.int64),
+                        ("block_tables", block_tables, torch.int32)):
+        if t.dtype != dt:
+            raise ValueError(f"{name} must be {dt}")
+        if t.ndim == 1 and not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    hist_cap = 0
+    if history is not None:
+        if step is None or history.dtype != torch.int64 or not history.is_contiguous():
+            raise ValueError("history must be contiguous int64 [rows, cap] with an int32 step counter")
+        hist_cap = history.shape[1]
+    _lib.check(
+        _lib.load().spk_decode_advance(
+            next_tokens.data_ptr(), input_ids.data_ptr(), positions.data_ptr(), seq_lens.data_ptr(),
+            slot_mapping.data_ptr(), block_tables.data_ptr(), block_tables.stride(0),
+            block_tables.stride(1), block_tables.shape[1], block_size, n_rows,
+            _lib.ptr(live), _lib.ptr(history), _lib.ptr(step), hist_cap, _lib.stream_of(dev),
+        ),
+        "decode_advance",
+    )

@@ -1,0 +1,266 @@
+"""Whole decode step on the GPU: each fused decoder operator against the torch
+composition it replaces, the model against a torch-only restatement of the
+reference forward (tests/model_ref.py), and the captured runner against eager.
+
+Bars: spike bits, packed bytes and the LIF(gate)*up product are bit-exact
+against the composition on identical inputs.  Norms differ from torch's only
+in fp32 summation order and rsqrt rounding, so they are checked at one bf16
+ulp.  Whole-model outputs are checked as the reference checks its own fast
+model against its original (modeling_fast.py:42-54): a spike whose membrane
+lands on its threshold may flip, so logits agree to a loose relative bound
+and nearly every cache bit agrees.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from model_ref import forward_paged_ref, lif_ref, pack_ref, rms_norm, rotate_half
+from spikeinfer_amd.attention import AttentionMetadata
+from spikeinfer_amd.kernels.decoder_ops import (add_rmsnorm, decode_advance, lif_gate_mul,
+                                                qkv_rope_lif_pack, rmsnorm_mean_t)
+from spikeinfer_amd.model import SpikingDecoder, SpikingQwenConfig
+from spikeinfer_amd.runner import DecodeRunner
+from spikeinfer_amd.sampler import SamplingParams
+from spikeinfer_amd.spike_cache import PagedSpikeCache, slot_mapping
+
+pytestmark = pytest.mark.gpu
+BF16_ULP = 2.0**-7  # relative spacing of bf16 at 1.0
+
+
+def _ulps(a, b):
+    """Max distance in bf16 ulps (same sign region assumed)."""
+    ai = a.view(torch.int16).to(torch.int32)
+    bi = b.view(torch.int16).to(torch.int32)
+    return int((ai - bi).abs().max())
+
+
+@pytest.mark.parametrize("with_delta", [False, True])
+def test_add_rmsnorm_matches_qwen2_rmsnorm(gpu, with_delta):
+    g = torch.Generator(device=gpu).manual_seed(1)
+    h = torch.randn((4, 37, 896), generator=g, device=gpu).to(torch.bfloat16)
+    d = torch.randn((4, 37, 896), generator=g, device=gpu).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(896, generator=g, device=gpu)).to(torch.bfloat16)
+    h_ref = h + d if with_delta else h.clone()
+    want = rms_norm(h_ref, w, 1e-6)
+    hk = h.clone()
+    got = add_rmsnorm(hk, d if with_delta else None, w, 1e-6)
+    assert torch.equal(hk, h_ref)  # the residual add is bit-exact
+    assert _ulps(got, want) <= 1
+    assert (got != want).float().mean() < 1e-3
+
+
+def test_rmsnorm_mean_t_matches_norm_then_mean(gpu):
+    g = torch.Generator(device=gpu).manual_seed(2)
+    h = torch.randn((4, 29, 896), generator=g, device=gpu).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(896, generator=g, device=gpu)).to(torch.bfloat16)
+    want = rms_norm(h, w, 1e-6).mean(dim=0)
+    got = rmsnorm_mean_t(h, w, 1e-6)
+    assert (got.float() - want.float()).abs().max() <= BF16_ULP * want.float().abs().max()
+
+
+def _rope_tables(positions, D, dtype, theta=1e6):
+    inv = 1.0 / (theta ** (torch.arange(0, D, 2, dtype=torch.int64).float() / D))
+    f = positions.float()[:, None].cpu() * inv[None]
+    e = torch.cat((f, f), -1)
+    return e.cos().to(dtype).to(positions.device), e.sin().to(dtype).to(positions.device)
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 14, 2), (128, 4, 4), (64, 2, 1)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_qkv_rope_lif_pack_bit_exact(gpu, D, Hq, Hkv, dtype):
+    T, n, n_q = 4, 23, 9
+    g = torch.Generator(device=gpu).manual_seed(D + Hq)
+    qkv = (torch.randn((T, n, (Hq + 2 * Hkv) * D), generator=g, device=gpu) * 1.5 + 0.3).to(dtype)
+    beta = (0.6 + 0.4 * torch.rand((3, D), generator=g, device=gpu)).to(dtype)
+    th = (0.5 + torch.rand((3, D), generator=g, device=gpu)).to(dtype)
+    pos = torch.randint(0, 5000, (n,), generator=g, device=gpu)
+    cos, sin = _rope_tables(pos, D, dtype)
+    slots_n = 200
+    slots = torch.randperm(slots_n, generator=g, device=gpu)[:n]
+    slots[3] = -1  # skipped token
+    W = D // 32
+    kc = torch.zeros((T, Hkv, slots_n, W), dtype=torch.int32, device=gpu)
+    vc = torch.zeros_like(kc)
+    qp = torch.zeros((T, n_q, Hq, W), dtype=torch.int32, device=gpu)
+    dense = tuple(torch.empty((T, H, n, D), dtype=dtype, device=gpu) for H in (Hq, Hkv, Hkv))
+    qkv_rope_lif_pack(qkv, cos, sin, beta, th, kc, vc, slots, Hq, Hkv, D, q_packed=qp, n_q=n_q,
+                      dense=dense)
+
+    q = qkv[..., :Hq * D].view(T, n, Hq, D)
+    k = qkv[..., Hq * D:(Hq + Hkv) * D].view(T, n, Hkv, D)
+    v = qkv[..., (Hq + Hkv) * D:].view(T, n, Hkv, D)
+    c, s = cos[None, :, None], sin[None, :, None]
+    q, k = (q * c) + (rotate_half(q) * s), (k * c) + (rotate_half(k) * s)
+    sq, sk, sv = lif_ref(q, beta[0], th[0]), lif_ref(k, beta[1], th[1]), lif_ref(v, beta[2], th[2])
+    assert torch.equal(qp, pack_ref(sq[:, :n_q]))
+    keep = slots >= 0
+    kw, vw = torch.zeros_like(kc), torch.zeros_like(vc)
+    kw[:, :, slots[keep]] = pack_ref(sk[:, keep].transpose(1, 2))
+    vw[:, :, slots[keep]] = pack_ref(sv[:, keep].transpose(1, 2))
+    assert torch.equal(kc, kw) and torch.equal(vc, vw)
+    for got, want in zip(dense, (sq, sk, sv)):
+        assert torch.equal(got, want.transpose(1, 2))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_lif_gate_mul_bit_exact(gpu, dtype):
+    T, rows, I = 4, 33, 4864
+    g = torch.Generator(device=gpu).manual_seed(5)
+    gu = (torch.randn((T, rows, 2 * I), generator=g, device=gpu) * 1.3 + 0.2).to(dtype)
+    beta = torch.full((I,), 0.9, dtype=dtype, device=gpu)
+    th = torch.ones(I, dtype=dtype, device=gpu)
+    got = lif_gate_mul(gu, beta, th)
+    want = lif_ref(gu[..., :I], beta, th) * gu[..., I:]
+    assert torch.equal(got, want)
+
+
+def test_decode_advance_moves_live_rows_only(gpu):
+    B, mb, bs = 5, 4, 16
+    tables = torch.arange(B * mb, dtype=torch.int32, device=gpu).view(B, mb).flip(1).contiguous()
+    pos = torch.tensor([0, 15, 16, 63, 7], device=gpu)
+    ids = torch.zeros(B, dtype=torch.int64, device=gpu)
+    lens = (pos + 1).to(torch.int32)
+    slots = torch.zeros(B, dtype=torch.int64, device=gpu)
+    nxt = torch.tensor([11, 12, 13, 14, 15], device=gpu)
+    hist = torch.zeros((B, 8), dtype=torch.int64, device=gpu)
+    step = torch.tensor([2], dtype=torch.int32, device=gpu)
+    live = torch.tensor([4], dtype=torch.int32, device=gpu)
+    decode_advance(nxt, ids, pos, lens, slots, tables, bs, B, live, hist, step)
+    p = [1, 16, 17, 63, 7]  # row 3 is at the end of its table; row 4 is not live
+    assert pos.tolist() == p
+    assert lens.tolist() == [2, 17, 18, 64, 8]
+    assert ids.tolist() == [11, 12, 13, 0, 0]
+    t = tables.cpu()
+    want = [int(t[i, p[i] // bs]) * bs + p[i] % bs for i in range(3)]
+    assert slots[:3].tolist() == want and slots[3:].tolist() == [0, 0]
+    assert hist[:, 2].tolist() == [11, 12, 13, 14, 0] and int(step) == 3
+
+
+def _small_model(gpu, layers=2, seed=0):
+    cfg = SpikingQwenConfig(vocab_size=1024, hidden_size=256, intermediate_size=512,
+                            num_hidden_layers=layers, num_attention_heads=4, num_key_value_heads=2,
+                            head_dim=64)
+    # Larger weights than the 0.02 of config 5 so that the small model spikes.
+    return SpikingDecoder(cfg, device=gpu, seed=seed, init_std=0.08)
+
+
+def _prefill_meta(prompts, tables, bs, gpu, ctx=None):
+    ctx = ctx or [0] * len(prompts)
+    slots, starts, ids, pos = [], [], [], []
+    for p, t, c in zip(prompts, tables, ctx):
+        starts.append(len(ids))
+        ids += p
+        pos += range(c, c + len(p))
+        slots += slot_mapping(t, c, len(p), bs)
+    meta = AttentionMetadata(
+        slot_mapping=torch.tensor(slots, device=gpu), block_size=bs, num_decode_tokens=0,
+        prefill_query_starts=starts, prefill_query_lens=[len(p) for p in prompts],
+        prefill_context_lens=list(ctx),
+        prefill_block_tables=[torch.tensor(t, dtype=torch.int32, device=gpu) for t in tables])
+    return torch.tensor(ids, device=gpu), torch.tensor(pos, device=gpu), meta
+
+
+def test_model_matches_reference_forward(gpu):
+    """Prefill (two fresh prompts of one length, one of another) then a mixed
+    step (two decodes + a chunk continuing a cached prefix)."""
+    m = _small_model(gpu)
+    bs = 16
+    cache = PagedSpikeCache(2, m.T, m.Hkv, m.D, 40, bs, device=gpu)
+    ref = PagedSpikeCache(2, m.T, m.Hkv, m.D, 40, bs, device=gpu)
+    g = torch.Generator().manual_seed(3)
+    prompts = [torch.randint(0, 1024, (n,), generator=g).tolist() for n in (20, 20, 33)]
+    tables = [[0, 5, 9], [1, 6, 10], [2, 7, 11]]
+    ids, pos, meta = _prefill_meta(prompts, tables, bs, gpu)
+    got = m.forward_paged(ids, pos, cache.layers, meta)
+    want = forward_paged_ref(m, ids, pos, ref.layers, meta)
+    torch.cuda.synchronize()
+    _compare(got, want, cache, ref, m)
+
+    # Step 2: decodes for sequences 0 and 1, a 7-token chunk for sequence 2.
+    d_ids = torch.randint(0, 1024, (2,), generator=g).tolist()
+    chunk = torch.randint(0, 1024, (7,), generator=g).tolist()
+    slots = slot_mapping(tables[0], 20, 1, bs) + slot_mapping(tables[1], 20, 1, bs) + \
+        slot_mapping(tables[2], 33, 7, bs)
+    meta2 = AttentionMetadata(
+        slot_mapping=torch.tensor(slots, device=gpu), block_size=bs, num_decode_tokens=2,
+        block_tables=torch.tensor(tables[:2] + [], dtype=torch.int32, device=gpu),
+        seq_lens=torch.tensor([21, 21], dtype=torch.int32, device=gpu),
+        prefill_query_starts=[2], prefill_query_lens=[7], prefill_context_lens=[33],
+        prefill_block_tables=[torch.tensor(tables[2], dtype=torch.int32, device=gpu)])
+    ids2 = torch.tensor(d_ids + chunk, device=gpu)
+    pos2 = torch.tensor([20, 20] + list(range(33, 40)), device=gpu)
+    got = m.forward_paged(ids2, pos2, cache.layers, meta2)
+    want = forward_paged_ref(m, ids2, pos2, ref.layers, meta2)
+    torch.cuda.synchronize()
+    _compare(got, want, cache, ref, m)
+
+
+def _compare(got, want, cache, ref, m):
+    assert got.shape == want.shape and got.dtype == want.dtype
+    scale = want.float().abs().max()
+    rel = float((got.float() - want.float()).abs().max() / scale)
+    assert rel < 0.05, f"hidden rel err {rel}"
+    lg, lw = m.compute_logits(got).float(), m.compute_logits(want).float()
+    agree = float((lg.argmax(-1) == lw.argmax(-1)).float().mean())
+    assert agree >= 0.9, f"argmax agreement {agree}"
+    for (kc, vc), (kr, vr) in zip(cache.layers, ref.layers):
+        for a, b in ((kc, kr), (vc, vr)):
+            diff = (a ^ b).view(torch.uint8)
+            bits = sum(int(((diff >> i) & 1).sum()) for i in range(8))
+            assert bits <= 1e-3 * a.numel() * 32, f"{bits} cache bits differ"
+    # Layer 0's cache depends only on the embedding, one norm and one GEMM:
+    # it must be (all but) identical.
+    assert torch.equal(cache.layers[0][0], ref.layers[0][0]) or \
+        (cache.layers[0][0] != ref.layers[0][0]).float().mean() < 1e-3
+
+
+def test_runner_graph_greedy_matches_eager_steps(gpu):
+    """Greedy generation through the captured step equals stepping the same
+    batch eagerly (same kernels, so the tokens are identical)."""
+    m = _small_model(gpu, seed=7)
+    bs, n, plen, new = 16, 3, 12, 9
+    g = torch.Generator().manual_seed(11)
+    prompts = [torch.randint(0, 1024, (plen,), generator=g).tolist() for _ in range(n)]
+    params = [SamplingParams(temperature=0.0) for _ in range(n)]
+
+    cache = PagedSpikeCache(2, m.T, m.Hkv, m.D, 64, bs, device=gpu)
+    runner = DecodeRunner(m, cache, batch_size=4, max_model_len=plen + new + 1, max_new_tokens=32)
+    toks = runner.generate(prompts, params, new, shuffle_blocks=5)
+
+    eager = DecodeRunner(m, PagedSpikeCache(2, m.T, m.Hkv, m.D, 64, bs, device=gpu), batch_size=4,
+                         max_model_len=plen + new + 1, max_new_tokens=32)
+    eager.start(prompts, params, shuffle_blocks=5)
+    for _ in range(new - 1):
+        eager._step()
+    torch.cuda.synchronize()
+    assert torch.equal(toks, eager.history[:n, :new])
+    # Replaying again continues from where the batch is (positions advance).
+    assert runner.positions[:n].tolist() == [plen + new - 1] * n
+
+
+def test_runner_sampling_in_graph_stays_in_top_k(gpu):
+    """Sampling inside the graph: every token is one of the row's top-k of the
+    eager logits at that step (checked on the first decode step)."""
+    m = _small_model(gpu, seed=9)
+    bs, n, plen = 16, 4, 10
+    g = torch.Generator().manual_seed(2)
+    prompts = [torch.randint(0, 1024, (plen,), generator=g).tolist() for _ in range(n)]
+    params = [SamplingParams(temperature=0.8, top_k=5, top_p=0.9) for _ in range(n)]
+    cache = PagedSpikeCache(2, m.T, m.Hkv, m.D, 64, bs, device=gpu)
+    runner = DecodeRunner(m, cache, batch_size=n, max_model_len=64, max_new_tokens=16)
+    runner.start(prompts, params, shuffle_blocks=1)
+    runner.capture()
+    # Logits of the step the graph is about to take, computed eagerly on a copy
+    # of the cache.
+    saved = [(k.clone(), v.clone()) for k, v in cache.layers]
+    hidden = m.forward_paged(runner.input_ids, runner.positions, cache.layers, runner.meta)
+    logits = m.compute_logits(hidden).float()
+    for (k, v), (ks, vs) in zip(cache.layers, saved):
+        k.copy_(ks)
+        v.copy_(vs)
+    runner.replay(1)
+    torch.cuda.synchronize()
+    tok = runner.history[:n, 1]
+    top5 = logits.topk(5, dim=-1).indices
+    assert all(int(tok[i]) in top5[i].tolist() for i in range(n))

@@ -287,3 +287,42 @@ def test_prefill_zero_query_is_running_mean():
     for i in range(5):
         want = vb[:, :, : 4 + i + 1].mean(axis=2)  # [T, Hkv, D]
         np.testing.assert_allclose(got[:, :, i], np.repeat(want, 2, axis=1), atol=1e-12)
+
+
+# ---- sampler oracle (spikeinfer/engine/sampler.py semantics) ----------------
+def test_sample_closed_form_distribution():
+    """logits ln(1..4): probabilities k/10, CDF boundaries at .1, .3, .6."""
+    lg = np.log(np.arange(1, 5, dtype=np.float64)).astype(np.float32)
+    _, kept, probs, _ = orc.sample_row(lg)
+    assert kept.all()
+    np.testing.assert_allclose(probs, [0.1, 0.2, 0.3, 0.4], atol=1e-7)
+    toks = [orc.sample_row(lg, u=u)[0] for u in (0.05, 0.15, 0.29, 0.31, 0.59, 0.61, 0.99)]
+    assert toks == [0, 1, 1, 2, 2, 3, 3]
+
+
+def test_sample_top_k_top_p_min_p_known_answers():
+    lg = np.log(np.array([1, 2, 3, 4], np.float64)).astype(np.float32)
+    assert orc.sample_row(lg, top_k=2)[1].tolist() == [False, False, True, True]
+    # top_p 0.5: mass before 0.4 is 0 and before 0.3 is 0.4 (< 0.5): keep {3, 2}
+    assert orc.sample_row(lg, top_p=0.5)[1].tolist() == [False, False, True, True]
+    # top_p 0.35: the second token has 0.4 before it, not < 0.35: keep {3}
+    assert orc.sample_row(lg, top_p=0.35)[1].tolist() == [False, False, False, True]
+    # min_p 0.45: keep p >= 0.45 * 0.4 = 0.18
+    assert orc.sample_row(lg, min_p=0.45)[1].tolist() == [False, True, True, True]
+    assert orc.sample_row(lg, top_k=1)[0] == 3
+    assert orc.sample_row(lg, temperature=0.0)[0] == 3
+
+
+def test_sample_penalties_known_answers():
+    lg = np.array([2.0, -2.0, 1.0, 0.5], np.float32)
+    # repetition 2 on tokens 0 and 1: 2 -> 1, -2 -> -4; greedy picks token 0 vs 2 (1.0 tie: lowest index)
+    assert orc.sample_row(lg, temperature=0.0, rep=2.0, history=[0, 1])[0] == 0
+    assert orc.sample_row(lg, temperature=0.0, rep=4.0, history=[0])[0] == 2
+    # frequency 0.5 x 3 occurrences + presence 0.25 on token 0: 2 - 1.75 = 0.25 < 0.5
+    assert orc.sample_row(lg, temperature=0.0, presence=0.25, frequency=0.5, history=[0, 0, 0])[0] == 2
+
+
+def test_sample_ties_ordered_by_index():
+    lg = np.array([1.0, 3.0, 3.0, 3.0, 0.0], np.float32)
+    assert orc.sample_row(lg, top_k=2)[1].tolist() == [False, True, True, False, False]
+    assert orc.sample_row(lg, temperature=0.0)[0] == 1

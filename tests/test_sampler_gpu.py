@@ -1,0 +1,139 @@
+"""The HIP sampler against the sampler oracle (oracle.sample_row, a numpy
+restatement of spikeinfer/engine/sampler.py:48-177) on identical logits and
+uniforms.  The kernel's token must be in the oracle's kept set and its
+interval of the oracle's index-order CDF must contain u (widened by 1e-6, the
+float32 weights' rounding); where u is farther than that from every boundary
+this is the same token as the oracle's.  Rows whose filter cut lies within
+rounding of its boundary (oracle margin < 1e-6) only need a kept token, and
+must stay rare."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from spikeinfer_amd.sampler import BatchSampler, SamplingParams, sample_tokens
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(gpu, logits, params, histories, uniforms, dtype=torch.float32):
+    n, V = logits.shape
+    lg = torch.from_numpy(logits).to(gpu, dtype)
+    f = lambda k, dflt: torch.tensor([p.get(k, dflt) for p in params], dtype=torch.float32, device=gpu)
+    cap = max(1, max(len(h) for h in histories))
+    hist = torch.zeros((n, cap), dtype=torch.int64, device=gpu)
+    for i, h in enumerate(histories):
+        if h:
+            hist[i, :len(h)] = torch.tensor(h)
+    hlen = torch.tensor([len(h) for h in histories], dtype=torch.int32, device=gpu)
+    out = sample_tokens(
+        lg, f("temperature", 1.0),
+        torch.tensor([p.get("top_k", -1) for p in params], dtype=torch.int32, device=gpu),
+        f("top_p", 1.0), f("min_p", 0.0), f("rep", 1.0), f("presence", 0.0), f("frequency", 0.0),
+        hist, hlen, torch.tensor(uniforms, dtype=torch.float32, device=gpu))
+    return out.cpu().tolist(), lg.float().cpu().numpy()
+
+
+CASES = [
+    dict(temperature=0.8, top_k=50, top_p=0.9, rep=1.1),  # config 5
+    dict(temperature=1.0),
+    dict(temperature=0.7, top_k=1),
+    dict(temperature=1.3, top_p=0.5),
+    dict(temperature=0.9, min_p=0.05),
+    dict(temperature=1.0, top_k=200, min_p=0.01, top_p=0.95),
+    dict(temperature=0.5, top_k=10, presence=0.5, frequency=0.25, rep=1.3),
+    dict(temperature=0.0, rep=1.5),
+    dict(temperature=2.0, top_k=100000),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_sampler_matches_oracle(gpu, case, dtype):
+    rng = np.random.default_rng(case)
+    rows, V = 16, 151936
+    logits = (rng.standard_normal((rows, V)) * 3).astype(np.float32)
+    params = [CASES[case]] * rows
+    histories = [rng.integers(0, V, size=rng.integers(0, 40)).tolist() for _ in range(rows)]
+    # Make some history tokens strong so the penalties matter.
+    for i, h in enumerate(histories):
+        for t in h[:3]:
+            logits[i, t] = 12.0 + rng.standard_normal()
+    us = rng.random(rows).astype(np.float32).tolist()
+    got, used = _run(gpu, logits, params, histories, us, dtype)
+    skipped = 0
+    for i in range(rows):
+        p = params[i]
+        tok, kept, _probs, margin = orc.sample_row(
+            used[i], temperature=p.get("temperature", 1.0), top_k=p.get("top_k", -1),
+            top_p=p.get("top_p", 1.0), min_p=p.get("min_p", 0.0), rep=p.get("rep", 1.0),
+            presence=p.get("presence", 0.0), frequency=p.get("frequency", 0.0),
+            history=histories[i], u=us[i])
+        if margin < 1e-6:
+            skipped += 1
+            continue
+        t = got[i]
+        assert kept[t], f"row {i}: token {t} not kept (oracle {tok})"
+        cdf = np.cumsum(_probs)
+        lo, hi = cdf[t] - _probs[t], cdf[t]
+        assert lo - 1e-6 <= us[i] <= hi + 1e-6, f"row {i}: u={us[i]} outside [{lo}, {hi}] of {t}"
+        if lo + 1e-6 < us[i] < hi - 1e-6:
+            assert t == tok
+    assert skipped <= 2
+
+
+def test_sampler_ties_and_tiny_vocab(gpu):
+    """bf16-style ties at the top-k cut are kept in index order."""
+    logits = np.array([[1.0, 3.0, 3.0, 3.0, 0.0, 3.0]] * 4, np.float32)
+    params = [dict(temperature=1.0, top_k=2)] * 4
+    us = [0.0, 0.49, 0.51, 0.999]
+    got, _ = _run(gpu, logits, params, [[]] * 4, us)
+    assert got == [1, 1, 2, 2]
+
+
+def test_sampler_uniform_sweep_follows_closed_form(gpu):
+    """logits ln(1..4): CDF boundaries at 0.1, 0.3, 0.6 (index order)."""
+    lg = np.log(np.arange(1, 5, dtype=np.float64)).astype(np.float32)
+    us = [0.05, 0.15, 0.29, 0.31, 0.59, 0.61, 0.99]
+    got, _ = _run(gpu, np.stack([lg] * len(us)), [dict()] * len(us), [[]] * len(us), us)
+    assert got == [0, 1, 1, 2, 2, 3, 3]
+
+
+def test_sampler_history_len_shared_count(gpu):
+    """history_len with one entry applies the same count to every row."""
+    V = 64
+    lg = torch.zeros((3, V), device=gpu)
+    lg[:, 7] = 5.0
+    lg[:, 9] = 4.0
+    hist = torch.tensor([[7, 1], [2, 3], [7, 7]], device=gpu)
+    t = torch.zeros(3, device=gpu)  # greedy
+    rep = torch.full((3,), 2.0, device=gpu)
+    one = torch.tensor([1], dtype=torch.int32, device=gpu)
+    out = sample_tokens(lg, t, repetition_penalty=rep, history=hist, history_len=one)
+    assert out.tolist() == [9, 7, 9]
+
+
+def test_batch_sampler_records_and_penalises(gpu):
+    V = 32
+    bsz = BatchSampler(2, gpu, history_cap=8)
+    bsz.set_params([SamplingParams(temperature=0.0, repetition_penalty=10.0),
+                    SamplingParams(temperature=0.0)])
+    lg = torch.zeros((2, V), device=gpu)
+    lg[:, 3] = 2.0
+    lg[:, 4] = 1.0
+    first = bsz.sample(lg).tolist()
+    second = bsz.sample(lg).tolist()
+    assert first == [3, 3] and second == [4, 3]
+    assert bsz.history_len.tolist() == [2, 2]
+
+
+def test_sampler_rejects_bad_arguments(gpu):
+    lg = torch.zeros((2, 10), device=gpu)
+    with pytest.raises(ValueError):
+        sample_tokens(lg, torch.ones(2, dtype=torch.float64, device=gpu))
+    with pytest.raises(ValueError):
+        sample_tokens(lg.t(), torch.ones(10, device=gpu))
+    with pytest.raises(ValueError):
+        SamplingParams(top_k=0)
