@@ -264,6 +264,8 @@ def main():
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=["config2", "config3", "config5"],
+                    help="run just this extra workload and print its figures (profiling)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -273,6 +275,17 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.only:
+        if args.only == "config2":
+            res = bench_lif(args.steps, args.warmup, dev)
+        elif args.only == "config5":
+            res = bench_decode_step(args.steps, args.warmup, dev)
+        else:
+            c3 = make_attn_inputs(64, 128, 192, 0.2, 3000, dev, layers=24)
+            ms3, _ = bench_attention(c3, args.steps, args.warmup, dev, torch.bfloat16, graph=True)
+            res = {"config3_attn_us_per_step_24_layers": round(ms3 * 1000, 1)}
+        print(json.dumps({"workload": args.only, **res}), flush=True)
+        return
 
     print("config 4: generating inputs", file=sys.stderr, flush=True)
     inp = make_attn_inputs(256, 4096, 32768, 0.2, 4000, dev)

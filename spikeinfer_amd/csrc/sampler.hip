@@ -24,11 +24,12 @@
 // Histograms, the seen-token bitmap and the count hash live in LDS; the row
 // itself is re-read from L2 on each pass.
 #include "common.hpp"
+#include "lif_math.hpp"
 
 namespace spk {
 namespace smp {
 
-constexpr int kThreads = 1024;
+constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kBins = 2048;            // 11-bit digits
 constexpr int kMaxVocab = 262144;      // bitmap capacity (32 KB)
@@ -37,31 +38,25 @@ constexpr int kHashSlots = 2 * kMaxHist;
 constexpr float kGreedyTemp = 1e-5f;
 constexpr double kMassScale = 1099511627776.0;  // 2^40
 
-struct Row {
-  const void *logits;
-  int dtype;
-  int V;
+constexpr int kCand = 8192;  // LDS candidate capacity (the fast path)
+
+struct Params {
   float temp, min_p, top_p, rep, presence, frequency;
   int top_k;
+  bool use_hash;
 };
 
 struct Shared {
-  uint32_t seen[kMaxVocab / 32];
-  int32_t hkey[kHashSlots];
+  uint32_t seen[kMaxVocab / 32];      // generated-token bitmap
+  int32_t hkey[kHashSlots];           // token + 1 -> count (frequency penalty)
   int32_t hcnt[kHashSlots];
-  unsigned long long hist[kBins];
+  unsigned long long hist[kBins];     // radix histograms (counts or fixed-point mass)
+  float cx[kCand];                    // candidates, in index order: value x ...
+  int32_t ci[kCand];                  // ... and vocabulary index
   unsigned long long wsum[kWaves];
   unsigned long long bcast[4];
   float fbcast[kWaves];
 };
-
-__device__ __forceinline__ float logit_at(const Row &r, int i) {
-  switch (r.dtype) {
-    case SPK_F32: return static_cast<const float *>(r.logits)[i];
-    case SPK_F16: return static_cast<float>(static_cast<const _Float16 *>(r.logits)[i]);
-    default: return bf16_bits_to_f32(static_cast<const uint16_t *>(r.logits)[i]);
-  }
-}
 
 // Order-preserving unsigned key of a float (larger float -> larger key).
 __device__ __forceinline__ uint32_t fkey(float x) {
@@ -78,18 +73,17 @@ __device__ __forceinline__ int hash_slot(int tok) {
 
 // Penalised logit (sampler.py:98-119): repetition first, then presence and
 // frequency, for tokens generated so far.
-__device__ __forceinline__ float penalised(const Row &r, const Shared &sh, int i, bool use_hash) {
-  float v = logit_at(r, i);
+__device__ __forceinline__ float penalise(const Params &P, const Shared &sh, int i, float v) {
   if (!((sh.seen[i >> 5] >> (i & 31)) & 1u)) return v;
-  if (r.rep != 1.f) v = v > 0.f ? v / r.rep : v * r.rep;
-  if (r.presence != 0.f || r.frequency != 0.f) {
+  if (P.rep != 1.f) v = v > 0.f ? v / P.rep : v * P.rep;
+  if (P.presence != 0.f || P.frequency != 0.f) {
     float cnt = 1.f;
-    if (use_hash) {
+    if (P.use_hash) {
       int s = hash_slot(i);
       while (sh.hkey[s] != i + 1) s = (s + 1) % kHashSlots;
       cnt = static_cast<float>(sh.hcnt[s]);
     }
-    v = v - (r.presence + r.frequency * cnt);
+    v = v - (P.presence + P.frequency * cnt);
   }
   return v;
 }
@@ -101,7 +95,7 @@ __device__ __forceinline__ unsigned long long shfl_up_u64(unsigned long long v, 
 }
 
 // Exclusive prefix sum over the workgroup in thread order; *total gets the sum.
-__device__ unsigned long long block_exclusive_scan(unsigned long long v, Shared &sh,
+__device__ __forceinline__ unsigned long long block_exclusive_scan(unsigned long long v, Shared &sh,
                                                    unsigned long long *total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   unsigned long long inc = v;
@@ -123,7 +117,7 @@ __device__ unsigned long long block_exclusive_scan(unsigned long long v, Shared 
   return before + inc - v;
 }
 
-__device__ float block_max(float v, Shared &sh) {
+__device__ __forceinline__ float block_max(float v, Shared &sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d));
@@ -135,7 +129,7 @@ __device__ float block_max(float v, Shared &sh) {
   return m;
 }
 
-__device__ unsigned long long block_max_u64(unsigned long long v, Shared &sh) {
+__device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v, Shared &sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) {
@@ -155,22 +149,24 @@ __device__ unsigned long long block_max_u64(unsigned long long v, Shared &sh) {
 // Given the 2048-bin histogram in sh.hist, finds the bin b (scanning from the
 // top) with above < target <= above + hist[b], where above = base + the bins
 // over b.  Writes b and its `above` to sh.bcast[0..1]; bcast[2] = 1 if found.
-__device__ void select_bin(Shared &sh, unsigned long long base, double target) {
-  const int j = threadIdx.x;
-  const int b1 = kBins - 1 - 2 * j, b2 = b1 - 1;
-  const unsigned long long h1 = sh.hist[b1], h2 = sh.hist[b2];
+constexpr int kBinsPerThread = kBins / kThreads;
+__device__ __forceinline__ void select_bin(Shared &sh, unsigned long long base, double target) {
+  const int top = kBins - 1 - kBinsPerThread * static_cast<int>(threadIdx.x);  // this thread's highest bin
+  unsigned long long h[kBinsPerThread], sum = 0;
+#pragma unroll
+  for (int r = 0; r < kBinsPerThread; ++r) sum += (h[r] = sh.hist[top - r]);
   unsigned long long total;
-  const unsigned long long before = base + block_exclusive_scan(h1 + h2, sh, &total);
-  if (j == 0) sh.bcast[2] = 0;
+  unsigned long long before = base + block_exclusive_scan(sum, sh, &total);
+  if (threadIdx.x == 0) sh.bcast[2] = 0;
   __syncthreads();
-  if ((double)before < target && target <= (double)(before + h1)) {
-    sh.bcast[0] = b1;
-    sh.bcast[1] = before;
-    sh.bcast[2] = 1;
-  } else if ((double)(before + h1) < target && target <= (double)(before + h1 + h2)) {
-    sh.bcast[0] = b2;
-    sh.bcast[1] = before + h1;
-    sh.bcast[2] = 1;
+#pragma unroll
+  for (int r = 0; r < kBinsPerThread; ++r) {
+    if ((double)before < target && target <= (double)(before + h[r])) {
+      sh.bcast[0] = top - r;
+      sh.bcast[1] = before;
+      sh.bcast[2] = 1;
+    }
+    before += h[r];
   }
   __syncthreads();
 }
@@ -179,38 +175,257 @@ __device__ __forceinline__ unsigned long long mass_of(float x, float m) {
   return static_cast<unsigned long long>(static_cast<double>(expf(x - m)) * kMassScale);
 }
 
+__device__ __forceinline__ void zero_hist(Shared &sh) {
+  __syncthreads();
+  for (int b = threadIdx.x; b < kBins; b += kThreads) sh.hist[b] = 0;
+  __syncthreads();
+}
+
+// ---- element sources ----------------------------------------------------------------
+// each(f): every element once, f(index, x), any order; chunk(f): this thread's
+// contiguous range, in index order (ranges ascend with the thread id).
+
+// The logits row in global memory; x = penalise(raw) / temperature.
+template <int DT, bool VEC>
+struct GlobalSrc {
+  typedef typename Elem<DT>::T E;
+  static constexpr int W = VEC ? Elem<DT>::kVec : 1;  // 16 bytes per load
+  typedef E Vec __attribute__((ext_vector_type(W)));
+  const E *p;
+  int V;
+  Params P;
+  const Shared *sh;
+
+  __device__ __forceinline__ float x(int i, E raw) const {
+    return penalise(P, *sh, i, elem_to_f32<DT>(raw)) / P.temp;
+  }
+  template <class F> __device__ __forceinline__ void each_raw(F f) const {
+    const int nv = V / W;
+    const Vec *pv = reinterpret_cast<const Vec *>(p);
+    int v = threadIdx.x;
+    for (; v + kThreads < nv; v += 2 * kThreads) {
+      const Vec a0 = pv[v], a1 = pv[v + kThreads];
+#pragma unroll
+      for (int j = 0; j < W; ++j) f(v * W + j, a0[j]);
+#pragma unroll
+      for (int j = 0; j < W; ++j) f((v + kThreads) * W + j, a1[j]);
+    }
+    for (; v < nv; v += kThreads) {
+      const Vec a = pv[v];
+#pragma unroll
+      for (int j = 0; j < W; ++j) f(v * W + j, a[j]);
+    }
+    for (int i = nv * W + threadIdx.x; i < V; i += kThreads) f(i, p[i]);
+  }
+  template <class F> __device__ __forceinline__ void each(F f) const {
+    each_raw([&](int i, E raw) { f(i, x(i, raw)); });
+  }
+  template <class F> __device__ __forceinline__ void chunk(F f) const {
+    const int per = ((V + kThreads - 1) / kThreads + W - 1) / W * W;
+    const int lo = min(V, static_cast<int>(threadIdx.x) * per), hi = min(V, lo + per);
+    int i = lo;
+    for (; i + W <= hi; i += W) {
+      const Vec a = *reinterpret_cast<const Vec *>(p + i);
+#pragma unroll
+      for (int j = 0; j < W; ++j) f(i + j, x(i + j, a[j]));
+    }
+    for (; i < hi; ++i) f(i, x(i, p[i]));
+  }
+};
+
+// The candidates gathered into LDS (index order).
+struct CandSrc {
+  const Shared *sh;
+  int n;
+  template <class F> __device__ __forceinline__ void each(F f) const {
+    for (int j = threadIdx.x; j < n; j += kThreads) f(sh->ci[j], sh->cx[j]);
+  }
+  template <class F> __device__ __forceinline__ void chunk(F f) const {
+    const int per = (n + kThreads - 1) / kThreads;
+    const int lo = min(n, static_cast<int>(threadIdx.x) * per), hi = min(n, lo + per);
+    for (int j = lo; j < hi; ++j) f(sh->ci[j], sh->cx[j]);
+  }
+};
+
+// min_p -> top_k -> top_p -> draw over a source; returns the token.  `Z_all`
+// (when have_Z) is the alive mass of the whole row, needed when the source is
+// a candidate subset and no top-k cut bounds the survivors inside it.
+template <class Src>
+__device__ __forceinline__ int64_t filter_and_draw(const Src src, Shared &sh, const Params P, float m,
+                                   long long k_req, bool have_Z, unsigned long long Z_all,
+                                   float u) {
+  auto alive = [&](float x) { return P.min_p <= 0.f || expf(x - m) >= P.min_p; };
+
+  // top-k: cut (Kk, tk) on element counts.
+  uint32_t Kk = 0;                // elements with key > Kk are kept
+  unsigned long long tk = ~0ull;  // ties at Kk kept, in index order (~0: all)
+  if (k_req > 0) {
+    unsigned long long c = 0;
+    src.each([&](int, float x) { c += alive(x) ? 1 : 0; });
+    unsigned long long alive_cnt;
+    block_exclusive_scan(c, sh, &alive_cnt);
+    if (static_cast<unsigned long long>(k_req) < alive_cnt) {
+      uint32_t prefix = 0;
+      unsigned long long above = 0;
+      for (int pass = 0; pass < 3; ++pass) {
+        const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+        const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
+        const int hi_shift = shift + (pass == 2 ? 10 : 11);
+        zero_hist(sh);
+        src.each([&](int, float x) {
+          if (!alive(x)) return;
+          const uint32_t k = fkey(x);
+          if (pass > 0 && (k >> hi_shift) != (prefix >> hi_shift)) return;
+          atomicAdd(&sh.hist[(k >> shift) & dmask], 1ull);
+        });
+        __syncthreads();
+        select_bin(sh, above, static_cast<double>(k_req));
+        prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
+        above = sh.bcast[1];
+      }
+      Kk = prefix;
+      tk = static_cast<unsigned long long>(k_req) - above;
+    }
+  }
+  const bool k_partial = tk != ~0ull;
+  auto in_s_nontie = [&](float x, uint32_t k) {
+    return alive(x) && (k > Kk || (k == Kk && !k_partial));
+  };
+  const unsigned long long wK = k_partial ? mass_of(unkey(Kk), m) : 0;
+
+  // top-p: cut (Kf, tf) on the survivors' probability mass.
+  uint32_t Kf = Kk;
+  unsigned long long tf = tk;
+  if (P.top_p < 1.f) {
+    unsigned long long Z;
+    if (have_Z && !k_partial) {
+      Z = Z_all;
+    } else {
+      unsigned long long z = 0;
+      src.each([&](int, float x) {
+        if (in_s_nontie(x, fkey(x))) z += mass_of(x, m);
+      });
+      block_exclusive_scan(z, sh, &Z);
+      if (k_partial) Z += tk * wK;
+    }
+    const double target = static_cast<double>(P.top_p) * static_cast<double>(Z);
+    uint32_t prefix = 0;
+    unsigned long long above = 0;
+    bool found = true;
+    for (int pass = 0; pass < 3 && found; ++pass) {
+      const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+      const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
+      const int hi_shift = shift + (pass == 2 ? 10 : 11);
+      zero_hist(sh);
+      src.each([&](int, float x) {
+        const uint32_t k = fkey(x);
+        if (!in_s_nontie(x, k)) return;
+        if (pass > 0 && (k >> hi_shift) != (prefix >> hi_shift)) return;
+        atomicAdd(&sh.hist[(k >> shift) & dmask], mass_of(x, m));
+      });
+      __syncthreads();
+      // The kept ties of the top-k cut all weigh wK: add them analytically.
+      if (threadIdx.x == 0 && k_partial && (pass == 0 || (Kk >> hi_shift) == (prefix >> hi_shift)))
+        sh.hist[(Kk >> shift) & dmask] += tk * wK;
+      __syncthreads();
+      select_bin(sh, above, target);
+      found = sh.bcast[2] != 0;
+      prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
+      above = sh.bcast[1];
+    }
+    if (found) {
+      Kf = prefix;
+      const unsigned long long w = mass_of(unkey(Kf), m);
+      // Ties at Kf kept: the first j with above + (j - 1) * w < target.
+      unsigned long long j =
+          w ? static_cast<unsigned long long>(ceil((target - static_cast<double>(above)) / static_cast<double>(w)))
+            : 1;
+      if (j < 1) j = 1;
+      if (Kf == Kk && k_partial && j > tk) j = tk;
+      tf = j;
+    }
+  }
+
+  // Draw: inverse CDF in index order over the kept weights.  Ties at Kf are
+  // ranked by a scan of per-thread tie counts.
+  const bool f_partial = tf != ~0ull;
+  unsigned long long wsum = 0, ties = 0;
+  src.chunk([&](int, float x) {
+    const uint32_t k = fkey(x);
+    if (!alive(x) || k < Kf) return;
+    if (k == Kf && f_partial) {
+      ++ties;
+      return;
+    }
+    wsum += mass_of(x, m);
+  });
+  unsigned long long tot_ties;
+  const unsigned long long rank0 = block_exclusive_scan(ties, sh, &tot_ties);
+  unsigned long long kept_ties = 0;
+  if (f_partial) kept_ties = rank0 >= tf ? 0 : (tf - rank0 < ties ? tf - rank0 : ties);
+  const unsigned long long wf = f_partial ? mass_of(unkey(Kf), m) : 0;
+  const unsigned long long mine = wsum + kept_ties * wf;
+  unsigned long long Wtot;
+  const unsigned long long before = block_exclusive_scan(mine, sh, &Wtot);
+  unsigned long long target =
+      static_cast<unsigned long long>(static_cast<double>(u) * static_cast<double>(Wtot));
+  if (target >= Wtot) target = Wtot ? Wtot - 1 : 0;
+  if (threadIdx.x == 0) sh.bcast[3] = 0;  // unreachable fallback: the top element always weighs 2^40
+  __syncthreads();
+  if (mine > 0 && before <= target && target < before + mine) {
+    unsigned long long acc = before, seen_ties = 0;
+    bool done = false;
+    src.chunk([&](int i, float x) {
+      if (done) return;
+      const uint32_t k = fkey(x);
+      if (!alive(x) || k < Kf) return;
+      unsigned long long w;
+      if (k == Kf && f_partial) {
+        if (seen_ties++ >= kept_ties) return;
+        w = wf;
+      } else {
+        w = mass_of(x, m);
+      }
+      acc += w;
+      if (acc > target) {
+        sh.bcast[3] = static_cast<unsigned long long>(i);
+        done = true;
+      }
+    });
+  }
+  __syncthreads();
+  return static_cast<int64_t>(sh.bcast[3]);
+}
+
+template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void sample_kernel(
-    const void *logits, int dtype, int64_t row_stride, int V, const float *temperature,
+    const void *logits, int64_t row_stride, int V, const float *temperature,
     const int32_t *top_k, const float *top_p, const float *min_p, const float *rep,
     const float *presence, const float *frequency, const int64_t *history, int64_t hist_stride,
     const int32_t *hist_len, int64_t hist_len_stride, const float *uniforms, int64_t *out) {
+  typedef typename Elem<DT>::T E;
   extern __shared__ __align__(16) char smem_raw[];
   Shared &sh = *reinterpret_cast<Shared *>(smem_raw);
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
-  Row r;
-  r.logits = static_cast<const char *>(logits) +
-             row * row_stride * (dtype == SPK_F32 ? 4 : 2);
-  r.dtype = dtype;
-  r.V = V;
-  r.temp = temperature[row];
-  r.top_k = top_k ? top_k[row] : -1;
-  r.top_p = top_p ? top_p[row] : 1.f;
-  r.min_p = min_p ? min_p[row] : 0.f;
-  r.rep = rep ? rep[row] : 1.f;
-  r.presence = presence ? presence[row] : 0.f;
-  r.frequency = frequency ? frequency[row] : 0.f;
+  Params P;
+  P.temp = temperature[row];
+  P.top_k = top_k ? top_k[row] : -1;
+  P.top_p = top_p ? top_p[row] : 1.f;
+  P.min_p = min_p ? min_p[row] : 0.f;
+  P.rep = rep ? rep[row] : 1.f;
+  P.presence = presence ? presence[row] : 0.f;
+  P.frequency = frequency ? frequency[row] : 0.f;
+  P.use_hash = P.frequency != 0.f;
 
   // ---- history -> seen bitmap (+ counts) ------------------------------------
   const int nwords = (V + 31) >> 5;
   for (int w = tid; w < nwords; w += kThreads) sh.seen[w] = 0u;
-  const bool use_hash = r.frequency != 0.f;
-  if (use_hash)
+  if (P.use_hash)
     for (int s = tid; s < kHashSlots; s += kThreads) sh.hkey[s] = 0, sh.hcnt[s] = 0;
   __syncthreads();
-  int nh = 0;
   if (history && hist_len) {
-    nh = hist_len[row * hist_len_stride];
+    int nh = hist_len[row * hist_len_stride];
     // At most one row of history (the row stride) and kMaxHist tokens.
     const int64_t cap = hist_stride < kMaxHist ? hist_stride : kMaxHist;
     nh = nh < 0 ? 0 : (nh > cap ? static_cast<int>(cap) : nh);
@@ -219,7 +434,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
       if (tok < 0 || tok >= V) continue;
       const int t32 = static_cast<int>(tok);
       atomicOr(&sh.seen[t32 >> 5], 1u << (t32 & 31));
-      if (use_hash) {
+      if (P.use_hash) {
         int s = hash_slot(t32);
         while (true) {
           const int prev = atomicCAS(&sh.hkey[s], 0, t32 + 1);
@@ -232,185 +447,123 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
   }
   __syncthreads();
 
+  GlobalSrc<DT, VEC> g;
+  g.p = reinterpret_cast<const E *>(logits) + row * row_stride;
+  g.V = V;
+  g.P = P;
+  g.sh = &sh;
+
   // ---- greedy: argmax of the penalised logits, first index on ties ------------
-  if (r.temp < kGreedyTemp) {
+  if (P.temp < kGreedyTemp) {
     unsigned long long best = 0;
-    for (int i = tid; i < V; i += kThreads) {
-      const unsigned long long k = (static_cast<unsigned long long>(fkey(penalised(r, sh, i, use_hash))) << 32) |
-                                   (0xffffffffu - static_cast<uint32_t>(i));
+    g.each_raw([&](int i, E raw) {
+      const unsigned long long k =
+          (static_cast<unsigned long long>(fkey(penalise(P, sh, i, elem_to_f32<DT>(raw)))) << 32) |
+          (0xffffffffu - static_cast<uint32_t>(i));
       best = k > best ? k : best;
-    }
+    });
     best = block_max_u64(best, sh);
     if (tid == 0) out[row] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
     return;
   }
 
-  // ---- max of x = penalised / temperature --------------------------------------
-  float m = -INFINITY;
-  for (int i = tid; i < V; i += kThreads) m = fmaxf(m, penalised(r, sh, i, use_hash) / r.temp);
-  m = block_max(m, sh);
-  const float min_p_v = r.min_p;
-  auto alive = [&](float x) { return min_p_v <= 0.f || expf(x - m) >= min_p_v; };
-
-  // ---- top-k: cut (Kk, tk) on element counts ----------------------------------------
-  uint32_t Kk = 0;                // cut key; elements with key > Kk all kept
-  unsigned long long tk = ~0ull;  // ties at Kk kept (in index order); ~0 = all
-  unsigned long long alive_cnt = 0;
-  {
-    unsigned long long c = 0;
-    for (int i = tid; i < V; i += kThreads) c += alive(penalised(r, sh, i, use_hash) / r.temp) ? 1 : 0;
-    unsigned long long tot;
-    block_exclusive_scan(c, sh, &tot);
-    alive_cnt = tot;
-  }
-  const long long k_req = (r.top_k < 0 || r.top_k >= V) ? -1 : r.top_k;
-  if (k_req > 0 && static_cast<unsigned long long>(k_req) < alive_cnt) {
-    uint32_t prefix = 0;
-    unsigned long long above = 0;
-    for (int pass = 0; pass < 3; ++pass) {
-      const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-      const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
-      const int hi_shift = shift + (pass == 2 ? 10 : 11);
-      for (int b = tid; b < kBins; b += kThreads) sh.hist[b] = 0;
-      __syncthreads();
-      for (int i = tid; i < V; i += kThreads) {
-        const float x = penalised(r, sh, i, use_hash) / r.temp;
-        if (!alive(x)) continue;
-        const uint32_t k = fkey(x);
-        if (pass > 0 && (k >> hi_shift) != (prefix >> hi_shift)) continue;
-        atomicAdd(&sh.hist[(k >> shift) & dmask], 1ull);
-      }
-      __syncthreads();
-      select_bin(sh, above, static_cast<double>(k_req));
-      prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
-      above = sh.bcast[1];
-      __syncthreads();
-    }
-    Kk = prefix;
-    tk = static_cast<unsigned long long>(k_req) - above;
-  }
-
-  // Membership in the survivors of min_p and top_k, ties at Kk aside.
-  const bool k_partial = tk != ~0ull;
-  auto in_s_nontie = [&](float x, uint32_t k) {
-    return alive(x) && (k > Kk || (k == Kk && !k_partial));
-  };
-  const float xK = unkey(Kk);
-  const unsigned long long wK = k_partial ? mass_of(xK, m) : 0;
-
-  // ---- top-p: cut (Kf, tf) on probability mass of the survivors ----------------------
-  uint32_t Kf = Kk;
-  unsigned long long tf = tk;
-  if (r.top_p < 1.f) {
-    unsigned long long z = 0;
-    for (int i = tid; i < V; i += kThreads) {
-      const float x = penalised(r, sh, i, use_hash) / r.temp;
-      if (in_s_nontie(x, fkey(x))) z += mass_of(x, m);
-    }
-    unsigned long long Z;
-    block_exclusive_scan(z, sh, &Z);
-    if (k_partial) Z += tk * wK;
-    const double target = static_cast<double>(r.top_p) * static_cast<double>(Z);
-    uint32_t prefix = 0;
-    unsigned long long above = 0;
-    bool found = true;
-    for (int pass = 0; pass < 3; ++pass) {
-      const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-      const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
-      const int hi_shift = shift + (pass == 2 ? 10 : 11);
-      for (int b = tid; b < kBins; b += kThreads) sh.hist[b] = 0;
-      __syncthreads();
-      for (int i = tid; i < V; i += kThreads) {
-        const float x = penalised(r, sh, i, use_hash) / r.temp;
-        const uint32_t k = fkey(x);
-        if (!in_s_nontie(x, k)) continue;
-        if (pass > 0 && (k >> hi_shift) != (prefix >> hi_shift)) continue;
-        atomicAdd(&sh.hist[(k >> shift) & dmask], mass_of(x, m));
-      }
-      __syncthreads();
-      // The kept ties of the top-k cut all weigh wK: add them analytically.
-      if (tid == 0 && k_partial && (pass == 0 || (Kk >> hi_shift) == (prefix >> hi_shift)))
-        sh.hist[(Kk >> shift) & dmask] += tk * wK;
-      __syncthreads();
-      select_bin(sh, above, target);
-      if (!sh.bcast[2]) found = false;
-      prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
-      above = sh.bcast[1];
-      __syncthreads();
-      if (!found) break;
-    }
-    if (found) {
-      Kf = prefix;
-      const unsigned long long w = mass_of(unkey(Kf), m);
-      // Ties at Kf kept: the first j with above + (j - 1) * w < target.
-      unsigned long long j = w ? static_cast<unsigned long long>(ceil((target - static_cast<double>(above)) / static_cast<double>(w))) : 1;
-      if (j < 1) j = 1;
-      if (Kf == Kk && k_partial && j > tk) j = tk;
-      tf = j;
-    }
-  }
-
-  // ---- draw: inverse CDF in index order over the kept weights --------------------------
-  // Thread tid owns the contiguous chunk [lo, hi); ties at Kf are ranked by a
-  // scan of per-chunk tie counts.
-  const int chunk = (V + kThreads - 1) / kThreads;
-  const int lo = min(V, tid * chunk), hi = min(V, lo + chunk);
-  const bool f_partial = tf != ~0ull;
-  unsigned long long wsum = 0, ties = 0;
-  for (int i = lo; i < hi; ++i) {
-    const float x = penalised(r, sh, i, use_hash) / r.temp;
-    const uint32_t k = fkey(x);
-    if (!alive(x) || k < Kf) continue;
-    if (k == Kf && f_partial) {
-      ++ties;
-      continue;
-    }
-    wsum += mass_of(x, m);
-  }
-  unsigned long long tot_ties;
-  const unsigned long long rank0 = block_exclusive_scan(ties, sh, &tot_ties);
-  unsigned long long kept_ties = 0;
-  if (f_partial) {
-    kept_ties = rank0 >= tf ? 0 : (tf - rank0 < ties ? tf - rank0 : ties);
-  }
-  const unsigned long long wf = f_partial ? mass_of(unkey(Kf), m) : 0;
-  const unsigned long long mine = wsum + kept_ties * wf;
-  unsigned long long Wtot;
-  const unsigned long long before = block_exclusive_scan(mine, sh, &Wtot);
+  const long long k_req = (P.top_k < 0 || P.top_k >= V) ? -1 : P.top_k;
   const float u = uniforms ? uniforms[row] : 0.f;
-  unsigned long long target = static_cast<unsigned long long>(static_cast<double>(u) * static_cast<double>(Wtot));
-  if (target >= Wtot) target = Wtot ? Wtot - 1 : 0;
-  if (tid == 0) sh.bcast[3] = ~0ull;
-  __syncthreads();
-  if (mine > 0 && before <= target && target < before + mine) {
-    unsigned long long acc = before, seen_ties = 0;
-    for (int i = lo; i < hi; ++i) {
-      const float x = penalised(r, sh, i, use_hash) / r.temp;
-      const uint32_t k = fkey(x);
-      if (!alive(x) || k < Kf) continue;
-      unsigned long long w;
-      if (k == Kf && f_partial) {
-        if (seen_ties++ >= kept_ties) continue;
-        w = wf;
-      } else {
-        w = mass_of(x, m);
-      }
-      acc += w;
-      if (acc > target) {
-        sh.bcast[3] = static_cast<unsigned long long>(i);
-        break;
-      }
+
+  // ---- pass A: max, and the top-digit count histogram for a top-k cut ----------
+  zero_hist(sh);
+  float m = -INFINITY;
+  g.each([&](int, float x) {
+    m = fmaxf(m, x);
+    if (k_req > 0) atomicAdd(&sh.hist[fkey(x) >> 21], 1ull);
+  });
+  m = block_max(m, sh);
+  auto alive = [&](float x) { return P.min_p <= 0.f || expf(x - m) >= P.min_p; };
+
+  // ---- candidate bound: every kept element has key >= L --------------------------
+  // With top-k: the first-digit bin of the k-th largest element (alive or not:
+  // the k largest alive are the k largest when k are alive, and otherwise all
+  // alive elements are above that bin anyway).  With top-p only: the
+  // first-digit bin where the alive mass, from the top, reaches top_p of the
+  // whole.
+  bool fast = false, have_Z = false;
+  uint32_t L = 0;
+  unsigned long long Z_all = 0;
+  if (k_req > 0) {
+    select_bin(sh, 0, static_cast<double>(k_req));
+    L = static_cast<uint32_t>(sh.bcast[0]) << 21;
+    fast = sh.bcast[1] + sh.hist[sh.bcast[0]] <= static_cast<unsigned long long>(kCand);
+  } else if (P.top_p < 1.f) {
+    zero_hist(sh);
+    g.each([&](int, float x) {
+      if (alive(x)) atomicAdd(&sh.hist[fkey(x) >> 21], mass_of(x, m));
+    });
+    __syncthreads();
+    unsigned long long mine = 0;
+    for (int b = tid; b < kBins; b += kThreads) mine += sh.hist[b];
+    block_exclusive_scan(mine, sh, &Z_all);
+    select_bin(sh, 0, static_cast<double>(P.top_p) * static_cast<double>(Z_all));
+    L = static_cast<uint32_t>(sh.bcast[0]) << 21;
+    have_Z = fast = sh.bcast[2] != 0;
+  }
+  int64_t tok;
+  if (fast) {
+    // Ordered compaction of the elements with key >= L into LDS.
+    unsigned long long c = 0;
+    g.chunk([&](int, float x) { c += fkey(x) >= L ? 1 : 0; });
+    unsigned long long n_c;
+    const unsigned long long off = block_exclusive_scan(c, sh, &n_c);
+    fast = n_c <= static_cast<unsigned long long>(kCand);
+    if (fast) {
+      int o = static_cast<int>(off);
+      g.chunk([&](int i, float x) {
+        if (fkey(x) >= L) {
+          sh.cx[o] = x;
+          sh.ci[o] = i;
+          ++o;
+        }
+      });
+      __syncthreads();
+      CandSrc cs;
+      cs.sh = &sh;
+      cs.n = static_cast<int>(n_c);
+      tok = filter_and_draw(cs, sh, P, m, k_req, have_Z, Z_all, u);
     }
   }
-  __syncthreads();
-  if (tid == 0) {
-    unsigned long long pick = sh.bcast[3];
-    if (pick == ~0ull) {
-      // Every kept weight rounded to zero: fall back to the top element.
-      pick = 0;
-    }
-    out[row] = static_cast<int64_t>(pick);
+  if (!fast) tok = filter_and_draw(g, sh, P, m, k_req, false, 0, u);
+  if (tid == 0) out[row] = tok;
+}
+
+struct Args {
+  const void *logits;
+  int64_t row_stride;
+  int V;
+  const float *temperature;
+  const int32_t *top_k;
+  const float *top_p, *min_p, *rep, *presence, *frequency;
+  const int64_t *history;
+  int64_t hist_stride;
+  const int32_t *hist_len;
+  int64_t hist_len_stride;
+  const float *uniforms;
+  int64_t *out;
+};
+
+template <int DT, bool VEC>
+int launch(const Args &a, int rows, hipStream_t stream) {
+  static bool attr_set = false;  // per instantiation
+  const size_t shm = sizeof(Shared);
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&sample_kernel<DT, VEC>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(shm));
+    if (e != hipSuccess) return fail(SPK_EHIP, "sample: %s", hipGetErrorString(e));
+    attr_set = true;
   }
+  sample_kernel<DT, VEC><<<rows, kThreads, shm, stream>>>(
+      a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.top_p, a.min_p, a.rep, a.presence,
+      a.frequency, a.history, a.hist_stride, a.hist_len, a.hist_len_stride, a.uniforms, a.out);
+  return check_launch("sample");
 }
 
 }  // namespace smp
@@ -436,18 +589,15 @@ extern "C" int spk_sample(const void *logits, int logits_dtype, int64_t row_stri
   if (history && (!history_len || history_stride < 1))
     return fail(SPK_EINVAL, "sample: history needs history_len and a row stride >= 1");
   if (rows == 0) return SPK_OK;
-  static bool attr_set = false;
-  const size_t shm = sizeof(smp::Shared);
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&smp::sample_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(shm));
-    if (e != hipSuccess) return fail(SPK_EHIP, "sample: %s", hipGetErrorString(e));
-    attr_set = true;
+  smp::Args a{logits, row_stride, vocab, temperature, top_k, top_p, min_p, repetition_penalty,
+              presence_penalty, frequency_penalty, history, history_stride, history_len,
+              history_len_stride, uniforms, out_tokens};
+  const size_t esz = logits_dtype == SPK_F32 ? 4 : 2;
+  const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (row_stride * esz) % 16 == 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (logits_dtype) {
+    case SPK_F32: return vec ? smp::launch<SPK_F32, true>(a, rows, s) : smp::launch<SPK_F32, false>(a, rows, s);
+    case SPK_F16: return vec ? smp::launch<SPK_F16, true>(a, rows, s) : smp::launch<SPK_F16, false>(a, rows, s);
+    default: return vec ? smp::launch<SPK_BF16, true>(a, rows, s) : smp::launch<SPK_BF16, false>(a, rows, s);
   }
-  smp::sample_kernel<<<rows, smp::kThreads, shm, static_cast<hipStream_t>(stream)>>>(
-      logits, logits_dtype, row_stride, vocab, temperature, top_k, top_p, min_p,
-      repetition_penalty, presence_penalty, frequency_penalty, history, history_stride,
-      history_len, history_len_stride, uniforms, out_tokens);
-  return check_launch("sample");
 }
