@@ -184,12 +184,14 @@ int spk_add_rmsnorm(void *h, const void *delta, const void *weight, void *out,
                     int dtype, int64_t rows, int hidden, float eps, void *stream);
 
 /*
- * Final RMSNorm and rate-coded readout: h [T, rows, hidden] contiguous ->
- * out [rows, hidden] = round(sum_t RMSNorm(h_t) * (1/T)), 1 <= T <= 8.
- * Replaces `self.norm(h).mean(dim=0)` (spikeinfer/modeling_fast.py:319).
+ * Final residual add, RMSNorm and rate-coded readout: h [T, rows, hidden]
+ * contiguous (plus delta of the same shape when not NULL, rounded to dtype; h
+ * is only read) -> out [rows, hidden] = round(sum_t RMSNorm(h_t) * (1/T)),
+ * 1 <= T <= 8.  Replaces `h = h + mlp(...)` of the last layer and
+ * `self.norm(h).mean(dim=0)` (spikeinfer/modeling_fast.py:210, :319).
  */
-int spk_rmsnorm_mean_t(const void *h, const void *weight, void *out, int dtype,
-                       int T, int64_t rows, int hidden, float eps, void *stream);
+int spk_rmsnorm_mean_t(const void *h, const void *delta, const void *weight, void *out,
+                       int dtype, int T, int64_t rows, int hidden, float eps, void *stream);
 
 /*
  * Fused q/k/v site of one attention layer: RoPE -> LIF -> bit-pack -> packed
@@ -273,6 +275,7 @@ int spk_sample(const void *logits, int logits_dtype, int64_t row_stride, int row
 
 /* LDS bytes one spk_sample workgroup uses (for occupancy planning). */
 size_t spk_sample_shared_bytes(void);
+
 
 #ifdef __cplusplus
 }

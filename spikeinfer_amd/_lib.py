@@ -53,7 +53,7 @@ _SIGNATURES = {
     "spk_pack": (_i32, [_vp, _i32, _i64, _vp, _i64, _i32, _vp]),
     "spk_unpack": (_i32, [_vp, _i64, _i32, _vp, _i32, _vp]),
     "spk_add_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _f32, _vp]),
-    "spk_rmsnorm_mean_t": (_i32, [_vp, _vp, _vp, _i32, _i32, _i64, _i32, _f32, _vp]),
+    "spk_rmsnorm_mean_t": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i64, _i32, _f32, _vp]),
     "spk_qkv_rope_lif_pack": (_i32, [
         _vp, _i32, _i64p, _vp, _vp, _vp, _vp, _i32, _vp, _i64p, _i64, _vp, _vp, _i64p, _vp,
         _i64, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _vp]),

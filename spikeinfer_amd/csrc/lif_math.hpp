@@ -54,4 +54,41 @@ __device__ __forceinline__ typename Elem<DT>::T spike_elem(bool s) {
   else return s ? 0x3c00 : 0;
 }
 
+// V consecutive per-channel parameters from p[off .. off + V) of dtype `dt`,
+// as fp32: 16-byte vector loads when the run is 16-byte aligned (the usual
+// case: contiguous fp32/bf16/f16 parameter vectors and off % V == 0), scalar
+// loads otherwise.
+template <int V>
+__device__ __forceinline__ void load_params(const void *p, int dt, int64_t off, float (&out)[V]) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  if (dt == SPK_F32 && ((a + off * 4) & 15) == 0 && V % 4 == 0) {
+    typedef float F4 __attribute__((ext_vector_type(4)));
+    const F4 *q = reinterpret_cast<const F4 *>(static_cast<const float *>(p) + off);
+#pragma unroll
+    for (int v = 0; v < V / 4; ++v) {
+      const F4 x = q[v];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out[4 * v + j] = x[j];
+    }
+  } else if ((dt == SPK_BF16 || dt == SPK_F16) && ((a + off * 2) & 15) == 0 && V % 8 == 0) {
+    typedef uint16_t H8 __attribute__((ext_vector_type(8)));
+    const H8 *q = reinterpret_cast<const H8 *>(static_cast<const uint16_t *>(p) + off);
+#pragma unroll
+    for (int v = 0; v < V / 8; ++v) {
+      const H8 x = q[v];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        // Through a scalar: a bit-cast applied to the vector element itself
+        // has been compiled as a cast of element 0 for every j.
+        const uint16_t e = x[j];
+        out[8 * v + j] = dt == SPK_BF16 ? bf16_bits_to_f32(e)
+                                        : static_cast<float>(__builtin_bit_cast(_Float16, e));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) out[j] = load_as_f32(p, off + j, dt);
+  }
+}
+
 }  // namespace spk

@@ -125,10 +125,11 @@ __global__ __launch_bounds__(256) void lif_dense_vec_kernel(LifParams p, int64_t
     const int64_t m = gi / (N / V);
     const int c0 = static_cast<int>(gi - m * (N / V)) * V;
     float beta[V], th[V], u[V];
+    load_params(p.beta, p.param_dtype, c0, beta);
+    load_params(p.th, p.param_dtype, c0, th);
 #pragma unroll
     for (int i = 0; i < V; ++i) {
-      beta[i] = clamp01(load_as_f32(p.beta, c0 + i, p.param_dtype));
-      th[i] = load_as_f32(p.th, c0 + i, p.param_dtype);
+      beta[i] = clamp01(beta[i]);
       u[i] = mem0 ? mem0[m * N + c0 + i] : 0.f;
     }
     const E *xrow = static_cast<const E *>(p.x) + m * xs1 + c0;
@@ -182,10 +183,11 @@ __global__ __launch_bounds__(256) void lif_pack_vec_kernel(LifParams p, int64_t 
     const int h = static_cast<int>(row - tok * H);
     const int c0 = grp * 64 + sub * 8;
     float beta[8], th[8], u[8];
+    load_params(p.beta, p.param_dtype, c0, beta);
+    load_params(p.th, p.param_dtype, c0, th);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      beta[i] = clamp01(load_as_f32(p.beta, c0 + i, p.param_dtype));
-      th[i] = load_as_f32(p.th, c0 + i, p.param_dtype);
+      beta[i] = clamp01(beta[i]);
       u[i] = 0.f;
     }
     bool write = true;

@@ -21,6 +21,7 @@ namespace spk {
 
 constexpr int kTBatchQkv = 4;  // timesteps whose loads are issued together
 constexpr int kMaxMeanT = 8;   // timesteps rmsnorm_mean_t keeps in registers
+constexpr int kNormRegVecs = 4;  // 16-byte vectors per lane add_rmsnorm keeps in registers
 
 // ---- residual add + RMSNorm ---------------------------------------------------
 // One wave per row.  h <- round(h + delta) (when delta is given), then
@@ -39,29 +40,28 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(typename Elem<DT>::T *
   if (row >= rows) return;
   Vec *hr = reinterpret_cast<Vec *>(h + row * hidden);
   const Vec *dr = delta ? reinterpret_cast<const Vec *>(delta + row * hidden) : nullptr;
+  const Vec *wr = reinterpret_cast<const Vec *>(weight);
+  Vec *orow = reinterpret_cast<Vec *>(out + row * hidden);
   const int nv = hidden / V;
-  float ss = 0.f;
-  for (int v = lane; v < nv; v += 64) {
-    Vec x = hr[v];
+  auto add = [&](Vec x, int v) {
     if (dr) {
       const Vec d = dr[v];
 #pragma unroll
       for (int i = 0; i < V; ++i) x[i] = f32_to_elem<DT>(elem_to_f32<DT>(x[i]) + elem_to_f32<DT>(d[i]));
       hr[v] = x;
     }
+    return x;
+  };
+  auto sumsq = [&](const Vec &x) {
+    float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < V; ++i) {
       const float f = elem_to_f32<DT>(x[i]);
       ss += f * f;
     }
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-  const float r = rsqrtf(ss * (1.f / static_cast<float>(hidden)) + eps);
-  const Vec *wr = reinterpret_cast<const Vec *>(weight);
-  Vec *orow = reinterpret_cast<Vec *>(out + row * hidden);
-  for (int v = lane; v < nv; v += 64) {
-    const Vec x = hr[v];
+    return ss;
+  };
+  auto norm = [&](const Vec &x, int v, float r) {
     const Vec w = wr[v];
     Vec y;
 #pragma unroll
@@ -70,13 +70,42 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(typename Elem<DT>::T *
       y[i] = f32_to_elem<DT>(elem_to_f32<DT>(w[i]) * n);
     }
     orow[v] = y;
+  };
+  float ss = 0.f;
+  if (nv <= 64 * kNormRegVecs) {
+    // The row stays in registers between the two halves.
+    Vec xs[kNormRegVecs];
+#pragma unroll
+    for (int k = 0; k < kNormRegVecs; ++k) {
+      const int v = lane + 64 * k;
+      if (v < nv) {
+        xs[k] = add(hr[v], v);
+        ss += sumsq(xs[k]);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    const float r = rsqrtf(ss * (1.f / static_cast<float>(hidden)) + eps);
+#pragma unroll
+    for (int k = 0; k < kNormRegVecs; ++k) {
+      const int v = lane + 64 * k;
+      if (v < nv) norm(xs[k], v, r);
+    }
+    return;
   }
+  for (int v = lane; v < nv; v += 64) ss += sumsq(add(hr[v], v));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  const float r = rsqrtf(ss * (1.f / static_cast<float>(hidden)) + eps);
+  for (int v = lane; v < nv; v += 64) norm(hr[v], v, r);
 }
 
 // ---- final RMSNorm + mean over the T timesteps --------------------------------
-// h [T, rows, hidden] -> out [rows, hidden] = round(sum_t norm_t * (1/T)).
+// h [T, rows, hidden] (+ delta, rounded, when given; h is not written) ->
+// out [rows, hidden] = round(sum_t norm_t * (1/T)).
 template <int DT>
 __global__ __launch_bounds__(256) void rmsnorm_mean_t_kernel(const typename Elem<DT>::T *h,
+                                                             const typename Elem<DT>::T *delta,
                                                              const typename Elem<DT>::T *weight,
                                                              typename Elem<DT>::T *out, int T,
                                                              int64_t rows, int hidden, float eps) {
@@ -89,15 +118,23 @@ __global__ __launch_bounds__(256) void rmsnorm_mean_t_kernel(const typename Elem
   const int nv = hidden / V;
   const Vec *wr = reinterpret_cast<const Vec *>(weight);
   Vec *orow = reinterpret_cast<Vec *>(out + row * hidden);
+  auto load = [&](int t, int v) {
+    Vec x = reinterpret_cast<const Vec *>(h + (t * rows + row) * hidden)[v];
+    if (delta) {
+      const Vec d = reinterpret_cast<const Vec *>(delta + (t * rows + row) * hidden)[v];
+#pragma unroll
+      for (int i = 0; i < V; ++i) x[i] = f32_to_elem<DT>(elem_to_f32<DT>(x[i]) + elem_to_f32<DT>(d[i]));
+    }
+    return x;
+  };
   // Pass 1: the T inverse RMS values.
   float rs[kMaxMeanT];
 #pragma unroll
   for (int t = 0; t < kMaxMeanT; ++t) {
     if (t >= T) break;
-    const Vec *hr = reinterpret_cast<const Vec *>(h + (t * rows + row) * hidden);
     float ss = 0.f;
     for (int v = lane; v < nv; v += 64) {
-      const Vec x = hr[v];
+      const Vec x = load(t, v);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         const float f = elem_to_f32<DT>(x[i]);
@@ -117,7 +154,7 @@ __global__ __launch_bounds__(256) void rmsnorm_mean_t_kernel(const typename Elem
 #pragma unroll
     for (int t = 0; t < kMaxMeanT; ++t) {
       if (t >= T) break;
-      const Vec x = reinterpret_cast<const Vec *>(h + (t * rows + row) * hidden)[v];
+      const Vec x = load(t, v);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         const float n = round_to<DT>(elem_to_f32<DT>(x[i]) * rs[t]);
@@ -175,10 +212,11 @@ __global__ __launch_bounds__(256) void qkv_rope_lif_pack_kernel(QkvParams p) {
   float beta[8], th[8], u[8], cs[8], sn[8];
   const Vec cv = active ? reinterpret_cast<const Vec *>(static_cast<const E *>(p.cos) + tok * p.D)[sub] : Vec{};
   const Vec sv = active ? reinterpret_cast<const Vec *>(static_cast<const E *>(p.sin) + tok * p.D)[sub] : Vec{};
+  load_params(p.beta, p.param_dtype, site * p.D + cl, beta);
+  load_params(p.th, p.param_dtype, site * p.D + cl, th);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    beta[i] = clamp01(load_as_f32(p.beta, site * p.D + cl + i, p.param_dtype));
-    th[i] = load_as_f32(p.th, site * p.D + cl + i, p.param_dtype);
+    beta[i] = clamp01(beta[i]);
     u[i] = 0.f;
     cs[i] = elem_to_f32<DT>(cv[i]);
     sn[i] = elem_to_f32<DT>(sv[i]);
@@ -276,10 +314,11 @@ __global__ __launch_bounds__(256) void lif_gate_mul_kernel(const typename Elem<D
   const int64_t row = gi / (I / V);
   const int c0 = static_cast<int>(gi - row * (I / V)) * V;
   float beta[V], th[V], u[V];
+  load_params(beta_p, param_dtype, c0, beta);
+  load_params(th_p, param_dtype, c0, th);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
-    beta[i] = clamp01(load_as_f32(beta_p, c0 + i, param_dtype));
-    th[i] = load_as_f32(th_p, c0 + i, param_dtype);
+    beta[i] = clamp01(beta[i]);
     u[i] = 0.f;
   }
   const E *grow = x + row * xs1 + c0;
@@ -370,15 +409,16 @@ extern "C" int spk_add_rmsnorm(void *h, const void *delta, const void *weight, v
   return check_launch("add_rmsnorm");
 }
 
-extern "C" int spk_rmsnorm_mean_t(const void *h, const void *weight, void *out, int dtype, int T,
-                                  int64_t rows, int hidden, float eps, void *stream) {
+extern "C" int spk_rmsnorm_mean_t(const void *h, const void *delta, const void *weight, void *out,
+                                  int dtype, int T, int64_t rows, int hidden, float eps,
+                                  void *stream) {
   if (!vec_dtype(dtype)) return fail(SPK_EINVAL, "rmsnorm_mean_t: dtype %d is not a float type", dtype);
   if (!h || !weight || !out) return fail(SPK_EINVAL, "rmsnorm_mean_t: null pointer");
   if (T < 1 || T > kMaxMeanT) return fail(SPK_EUNSUPPORTED, "rmsnorm_mean_t: T=%d outside [1, %d]", T, kMaxMeanT);
   if (rows < 0 || hidden <= 0 || hidden % vec_of(dtype))
     return fail(SPK_EINVAL, "rmsnorm_mean_t: hidden=%d must be a positive multiple of %d", hidden,
                 vec_of(dtype));
-  if (!aligned16(h) || !aligned16(weight) || !aligned16(out))
+  if (!aligned16(h) || !aligned16(weight) || !aligned16(out) || (delta && !aligned16(delta)))
     return fail(SPK_EINVAL, "rmsnorm_mean_t: buffers must be 16-byte aligned");
   if (rows == 0) return SPK_OK;
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
@@ -387,8 +427,9 @@ extern "C" int spk_rmsnorm_mean_t(const void *h, const void *weight, void *out, 
 #define SPK_CASE(DT)                                                                          \
   case DT:                                                                                    \
     rmsnorm_mean_t_kernel<DT><<<grid, 256, 0, s>>>(                                           \
-        static_cast<const Elem<DT>::T *>(h), static_cast<const Elem<DT>::T *>(weight),        \
-        static_cast<Elem<DT>::T *>(out), T, rows, hidden, eps);                               \
+        static_cast<const Elem<DT>::T *>(h), static_cast<const Elem<DT>::T *>(delta),         \
+        static_cast<const Elem<DT>::T *>(weight), static_cast<Elem<DT>::T *>(out), T, rows,   \
+        hidden, eps);                                                                         \
     break;
     SPK_CASE(SPK_F32) SPK_CASE(SPK_F16) SPK_CASE(SPK_BF16)
 #undef SPK_CASE

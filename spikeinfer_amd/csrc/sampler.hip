@@ -203,12 +203,17 @@ struct GlobalSrc {
     const int nv = V / W;
     const Vec *pv = reinterpret_cast<const Vec *>(p);
     int v = threadIdx.x;
-    for (; v + kThreads < nv; v += 2 * kThreads) {
-      const Vec a0 = pv[v], a1 = pv[v + kThreads];
+    for (; v + 3 * kThreads < nv; v += 4 * kThreads) {
+      const Vec a0 = pv[v], a1 = pv[v + kThreads], a2 = pv[v + 2 * kThreads],
+                a3 = pv[v + 3 * kThreads];
 #pragma unroll
       for (int j = 0; j < W; ++j) f(v * W + j, a0[j]);
 #pragma unroll
       for (int j = 0; j < W; ++j) f((v + kThreads) * W + j, a1[j]);
+#pragma unroll
+      for (int j = 0; j < W; ++j) f((v + 2 * kThreads) * W + j, a2[j]);
+#pragma unroll
+      for (int j = 0; j < W; ++j) f((v + 3 * kThreads) * W + j, a3[j]);
     }
     for (; v < nv; v += kThreads) {
       const Vec a = pv[v];
@@ -224,6 +229,19 @@ struct GlobalSrc {
     const int per = ((V + kThreads - 1) / kThreads + W - 1) / W * W;
     const int lo = min(V, static_cast<int>(threadIdx.x) * per), hi = min(V, lo + per);
     int i = lo;
+    // Four 16-byte loads in flight per iteration.
+    for (; i + 4 * W <= hi; i += 4 * W) {
+      const Vec *q = reinterpret_cast<const Vec *>(p + i);
+      const Vec a0 = q[0], a1 = q[1], a2 = q[2], a3 = q[3];
+#pragma unroll
+      for (int j = 0; j < W; ++j) f(i + j, x(i + j, a0[j]));
+#pragma unroll
+      for (int j = 0; j < W; ++j) f(i + W + j, x(i + W + j, a1[j]));
+#pragma unroll
+      for (int j = 0; j < W; ++j) f(i + 2 * W + j, x(i + 2 * W + j, a2[j]));
+#pragma unroll
+      for (int j = 0; j < W; ++j) f(i + 3 * W + j, x(i + 3 * W + j, a3[j]));
+    }
     for (; i + W <= hi; i += W) {
       const Vec a = *reinterpret_cast<const Vec *>(p + i);
 #pragma unroll

@@ -51,18 +51,23 @@ def add_rmsnorm(h: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tenso
 
 
 def rmsnorm_mean_t(h: torch.Tensor, weight: torch.Tensor, eps: float,
-                   out: torch.Tensor | None = None) -> torch.Tensor:
-    """``RMSNorm(h).mean(dim=0)`` for ``h [T, rows, hidden]`` contiguous."""
-    dev = _lib.require_gpu(h, weight, out)
+                   out: torch.Tensor | None = None, delta: torch.Tensor | None = None) -> torch.Tensor:
+    """``RMSNorm(h + delta).mean(dim=0)`` for ``h [T, rows, hidden]``
+    contiguous (``delta`` optional, same shape; h is not modified)."""
+    dev = _lib.require_gpu(h, weight, out, delta)
     if h.ndim != 3:
         raise ValueError("rmsnorm_mean_t: expected h as [T, rows, hidden]")
     _contig_rows(h, "h")
+    if delta is not None:
+        _contig_rows(delta, "delta")
+        if delta.shape != h.shape or delta.dtype != h.dtype:
+            raise ValueError("rmsnorm_mean_t: delta must match h")
     T, rows, hidden = h.shape
     if out is None:
         out = torch.empty((rows, hidden), dtype=h.dtype, device=dev)
     _lib.check(
         _lib.load().spk_rmsnorm_mean_t(
-            h.data_ptr(), weight.data_ptr(), out.data_ptr(), _lib.dtype_code(h.dtype), T, rows,
+            h.data_ptr(), _lib.ptr(delta), weight.data_ptr(), out.data_ptr(), _lib.dtype_code(h.dtype), T, rows,
             hidden, float(eps), _lib.stream_of(dev),
         ),
         "rmsnorm_mean_t",

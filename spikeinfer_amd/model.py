@@ -187,8 +187,7 @@ class SpikingDecoder:
             x = add_rmsnorm(h, o, L.post_norm, c.rms_norm_eps, out=x)
             gu = F.linear(x, L.w_gu)
             delta = F.linear(lif_gate_mul(gu, L.lif_gate_beta, L.lif_gate_th), L.w_down)
-        h.add_(delta)
-        return rmsnorm_mean_t(h, self.final_norm, c.rms_norm_eps)
+        return rmsnorm_mean_t(h, self.final_norm, c.rms_norm_eps, delta=delta)
 
     def _prefill_attention(self, dense, k_cache, v_cache, meta: AttentionMetadata, attn) -> None:
         """Prefill chunks (attention.py:161-178): SDPA on the chunk's dense

@@ -50,12 +50,16 @@ def test_add_rmsnorm_matches_qwen2_rmsnorm(gpu, with_delta):
     assert (got != want).float().mean() < 1e-3
 
 
-def test_rmsnorm_mean_t_matches_norm_then_mean(gpu):
+@pytest.mark.parametrize("with_delta", [False, True])
+def test_rmsnorm_mean_t_matches_norm_then_mean(gpu, with_delta):
     g = torch.Generator(device=gpu).manual_seed(2)
     h = torch.randn((4, 29, 896), generator=g, device=gpu).to(torch.bfloat16)
+    d = torch.randn((4, 29, 896), generator=g, device=gpu).to(torch.bfloat16)
     w = (1 + 0.1 * torch.randn(896, generator=g, device=gpu)).to(torch.bfloat16)
-    want = rms_norm(h, w, 1e-6).mean(dim=0)
-    got = rmsnorm_mean_t(h, w, 1e-6)
+    want = rms_norm(h + d if with_delta else h, w, 1e-6).mean(dim=0)
+    h0 = h.clone()
+    got = rmsnorm_mean_t(h, w, 1e-6, delta=d if with_delta else None)
+    assert torch.equal(h, h0)
     assert (got.float() - want.float()).abs().max() <= BF16_ULP * want.float().abs().max()
 
 
@@ -103,13 +107,15 @@ def test_qkv_rope_lif_pack_bit_exact(gpu, D, Hq, Hkv, dtype):
         assert torch.equal(got, want.transpose(1, 2))
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_lif_gate_mul_bit_exact(gpu, dtype):
+    """Per-channel parameters in the activation dtype (so every 16-bit lane
+    of the vector parameter load is checked with distinct values)."""
     T, rows, I = 4, 33, 4864
     g = torch.Generator(device=gpu).manual_seed(5)
     gu = (torch.randn((T, rows, 2 * I), generator=g, device=gpu) * 1.3 + 0.2).to(dtype)
-    beta = torch.full((I,), 0.9, dtype=dtype, device=gpu)
-    th = torch.ones(I, dtype=dtype, device=gpu)
+    beta = (0.5 + 0.5 * torch.rand(I, generator=g, device=gpu)).to(dtype)
+    th = (0.5 + torch.rand(I, generator=g, device=gpu)).to(dtype)
     got = lif_gate_mul(gu, beta, th)
     want = lif_ref(gu[..., :I], beta, th) * gu[..., I:]
     assert torch.equal(got, want)
