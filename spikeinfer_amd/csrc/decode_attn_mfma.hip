@@ -54,7 +54,6 @@ constexpr int kMaxPartBlocks = kMaxStagedBlocks;  // block-table entries staged 
 // h), stored as two 16-byte windows: a[w][r] = bytes 16w..16w+15 of row r.
 struct alignas(16) WaveStage {
   uint64_t v[kStepTokens];            // v word of each row                  (1 KB)
-  uint64_t vs[kStepTokens];           // the same words shifted right by 1   (1 KB)
   uint4 a[2][kStepTokens];            // digit rows, window-major            (4 KB)
 };
 
@@ -97,7 +96,7 @@ __device__ __forceinline__ void token_digits(uint64_t kw, bool valid, const uint
 
 // Stages one 128-token step of a wave (lane l holds tokens 2l and 2l+1,
 // staged as rows l and l+64):
-// weight digits and v words (plain and shifted) into the wave's LDS stage.
+// weight digits and v words into the wave's LDS stage.
 template <int NREP, bool MASKED>
 __device__ __forceinline__ void stage_step(WaveStage &st, int lane, const uint64_t (&kw)[2],
                                            const uint64_t (&vw)[2], const bool (&valid)[2],
@@ -112,7 +111,6 @@ __device__ __forceinline__ void stage_step(WaveStage &st, int lane, const uint64
     st.a[1][row] = make_uint4(dig[4], dig[5], dig[6], dig[7]);
     const uint64_t v = (!MASKED || valid[e]) ? vw[e] : 0ull;
     st.v[row] = v;
-    st.vs[row] = v >> 1;
   }
 }
 
@@ -129,15 +127,14 @@ __device__ __forceinline__ void wave_sync() {
 // the all-ones tile that accumulates the softmax denominators.
 //   tile 0 column n: channel 4*(n%16) + n/16      (fp4 0001 = 0.5 per set bit)
 //   tile 1 column n: channel 4*(n%16) + 2 + n/16  (fp4 0100 = 2.0 per set bit)
-// Lanes 16..31 of each half read the shifted copy, so one AND per register
-// selects their channel for both tiles.
+// Lanes 16..31 of each half shift their transposed v words right by one, so
+// one AND per register selects their channel for both tiles.
 __device__ __forceinline__ void contract_half(const WaveStage &st, int lane, int u, v16f &acc0,
                                               v16f &acc1, v16f &accl) {
   const int g = lane >> 5;          // K group of the MFMA operands
   const int i16 = lane & 15;        // lane within its 16-lane transpose group
-  const int win = (lane >> 4) & 1;  // 16-byte window of a digit row / shifted copy
-  const SPK_LDS char *lds_v =
-      (const SPK_LDS char *)(win ? st.vs : st.v) + 64 * u * 8;
+  const int win = (lane >> 4) & 1;  // 16-byte window of a digit row / odd channels
+  const SPK_LDS char *lds_v = (const SPK_LDS char *)st.v + 64 * u * 8;
   const SPK_LDS char *lds_a = (const SPK_LDS char *)&st.a[win][64 * u];
   v8i A;
 #pragma unroll
@@ -149,8 +146,11 @@ __device__ __forceinline__ void contract_half(const WaveStage &st, int lane, int
   }
   const v2i w0 = tr_b4(lds_v + (16 * g + i16) * 8);
   const v2i w1 = tr_b4(lds_v + (32 + 16 * g + i16) * 8);
-  const uint32_t wv[4] = {static_cast<uint32_t>(w0.x), static_cast<uint32_t>(w0.y),
-                          static_cast<uint32_t>(w1.x), static_cast<uint32_t>(w1.y)};
+  // Lanes of the second 16-lane group take the odd channel of each pair:
+  // shifted right by one, bit 0 / bit 2 of every nibble are channels 4i+1 /
+  // 4i+3 (bit 3 takes the next nibble's bit 0 and is masked off below).
+  const uint32_t wv[4] = {static_cast<uint32_t>(w0.x) >> win, static_cast<uint32_t>(w0.y) >> win,
+                          static_cast<uint32_t>(w1.x) >> win, static_cast<uint32_t>(w1.y) >> win};
   v8i B0 = {}, B1 = {}, Bl = {};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
