@@ -259,8 +259,8 @@ int spk_decode_advance(const int64_t *next_tokens, int64_t *input_ids, int64_t *
  * argmax of the penalised logits (lowest index on ties).
  *
  * Equal logits are ordered by index (the reference leaves that order to
- * torch.topk).  The draw is the inverse CDF, in index order, of the kept
- * softmax weights at uniforms[row] in [0, 1).  history int64 [rows,
+ * torch.topk).  The draw is the inverse CDF of the kept softmax weights at
+ * uniforms[row] in [0, 1), tokens taken by logit descending, index ascending.  history int64 [rows,
  * history_stride] holds generated tokens, history_len[row *
  * history_len_stride] of them (stride 0: one count for every row; at most
  * 2048 are used).  vocab <= 262144.  Result: out_tokens int64 [rows].

@@ -215,15 +215,16 @@ def sample_row(logits, temperature=1.0, top_k=-1, top_p=1.0, min_p=0.0, rep=1.0,
     ``x = v / temperature`` in float32 (:69-75), then in float64: min_p on the
     softmax (:137-141), top_k on the descending order (:143-153), top_p on the
     mass strictly before each token (:155-159).  Equal values are ordered by
-    index (a stable sort; the reference leaves it to torch.topk).  The draw is
-    the first index, in index order, whose inclusive cumulative kept weight
-    exceeds ``u`` times the total.
+    index (a stable sort; the reference leaves it to torch.topk).  The draw
+    walks the kept tokens in the same order (value descending, index
+    ascending) and takes the first whose inclusive cumulative probability
+    exceeds ``u``.
 
-    Returns (token, kept bool mask, kept probabilities, margin): ``margin`` is
-    the smallest distance of a filter cut (min_p, top_p) from its decision
-    boundary -- below ~1e-6 the float32 kernel may legitimately decide the
-    other way.  The draw's own boundaries are the cumulative sums of the
-    returned probabilities.
+    Returns (token, kept bool mask, kept probabilities, margin, order):
+    ``margin`` is the smallest distance of a filter cut (min_p, top_p) from its
+    decision boundary -- below ~1e-6 the float32 kernel may legitimately
+    decide the other way; ``order`` lists the kept tokens in draw order (the
+    cumulative sums of ``probs[order]`` are the draw's boundaries).
     """
     v = np.asarray(logits, np.float32).copy()
     counts = {}
@@ -239,7 +240,7 @@ def sample_row(logits, temperature=1.0, top_k=-1, top_p=1.0, min_p=0.0, rep=1.0,
         tok = int(np.argmax(v))
         kept = np.zeros(V, bool)
         kept[tok] = True
-        return tok, kept, kept.astype(np.float64), np.inf
+        return tok, kept, kept.astype(np.float64), np.inf, np.array([tok])
     x = (v / np.float32(temperature)).astype(np.float32)
     m = float(x.max())
     w = np.exp(x.astype(np.float64) - m)
@@ -262,9 +263,6 @@ def sample_row(logits, temperature=1.0, top_k=-1, top_p=1.0, min_p=0.0, rep=1.0,
     kept[order] = True
     probs = np.where(kept, w, 0.0)
     probs /= probs.sum()
-    cdf = np.cumsum(probs)
-    tok = int(np.searchsorted(cdf, u, side="right"))
-    tok = min(tok, V - 1)
-    while not kept[tok]:  # u landed exactly on a boundary of zero-weight entries
-        tok += 1
-    return tok, kept, probs, margin
+    cdf = np.cumsum(probs[order])
+    pos = min(int(np.searchsorted(cdf, u, side="right")), len(order) - 1)
+    return int(order[pos]), kept, probs, margin, order

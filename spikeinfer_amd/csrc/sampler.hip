@@ -9,20 +9,24 @@
 // MI355X design.  No sort of the 151,936-entry row.  Every filter keeps a
 // prefix of the row in one total order -- value descending, index ascending
 // (the reference leaves the order of equal logits to torch.topk; this kernel
-// fixes it) -- so the result is one cut (key K, first t elements of key K):
+// fixes it) -- so each cut is a key K plus, among the elements of key K, the
+// ones up to some index:
 //   * min_p keeps exp(x - max) >= min_p (a value threshold);
-//   * top_k: a 3-pass radix select (11/11/10 bits of the order-preserving
-//     key) on element counts finds the k-th element;
-//   * top_p: the same radix select on probability mass finds the last element
-//     whose preceding mass is below top_p of the surviving mass.  Mass is
-//     fixed point (weight * 2^40 in uint64), so sums are exact and the cut is
-//     deterministic whatever the atomic order;
-//   * ties at the cut are ranked in index order with one block scan.
-// The draw is an inverse CDF in index order over the kept weights with a
-// caller-supplied uniform u in [0, 1): the first token whose inclusive
-// cumulative weight exceeds u * total.
-// Histograms, the seen-token bitmap and the count hash live in LDS; the row
-// itself is re-read from L2 on each pass.
+//   * top_k: radix select (11/11/10-bit digits of the order-preserving key)
+//     on element counts finds the k-th element, and a radix select on the
+//     indices of its ties finds how far into them the cut goes;
+//   * top_p: the same on probability mass finds the last element whose
+//     preceding mass is below top_p of the surviving mass.  Mass is fixed
+//     point (weight * 2^40 in uint64), so sums are exact and the cut is
+//     deterministic whatever the atomic order.
+// The draw takes the element whose interval of the kept mass, accumulated in
+// the same total order, holds u * total, for a caller-supplied uniform u in
+// [0, 1): one more mass select and one index select.
+// Nothing depends on the order elements are visited in, so every pass over
+// the row is a coalesced sweep.  With a top-k cut, one sweep gathers the
+// elements at or above a sample-estimated threshold into LDS (a few hundred at
+// top-k 50) and every later pass runs over those; histograms, the seen-token
+// bitmap and the count hash live in LDS too.
 #include "common.hpp"
 #include "lif_math.hpp"
 
@@ -73,8 +77,8 @@ __device__ __forceinline__ int hash_slot(int tok) {
 
 // Penalised logit (sampler.py:98-119): repetition first, then presence and
 // frequency, for tokens generated so far.
-__device__ __forceinline__ float penalise(const Params &P, const Shared &sh, int i, float v) {
-  if (!((sh.seen[i >> 5] >> (i & 31)) & 1u)) return v;
+// Penalty of a token known to be in the history.
+__device__ __forceinline__ float penalise_seen(const Params &P, const Shared &sh, int i, float v) {
   if (P.rep != 1.f) v = v > 0.f ? v / P.rep : v * P.rep;
   if (P.presence != 0.f || P.frequency != 0.f) {
     float cnt = 1.f;
@@ -86,6 +90,11 @@ __device__ __forceinline__ float penalise(const Params &P, const Shared &sh, int
     v = v - (P.presence + P.frequency * cnt);
   }
   return v;
+}
+
+__device__ __forceinline__ float penalise(const Params &P, const Shared &sh, int i, float v) {
+  if (!((sh.seen[i >> 5] >> (i & 31)) & 1u)) return v;
+  return penalise_seen(P, sh, i, v);
 }
 
 __device__ __forceinline__ unsigned long long shfl_up_u64(unsigned long long v, int d) {
@@ -182,14 +191,15 @@ __device__ __forceinline__ void zero_hist(Shared &sh) {
 }
 
 // ---- element sources ----------------------------------------------------------------
-// each(f): every element once, f(index, x), any order; chunk(f): this thread's
-// contiguous range, in index order (ranges ascend with the thread id).
+// each(f) visits every element once, f(index, x), in no particular order.
 
-// The logits row in global memory; x = penalise(raw) / temperature.
+// The logits row in global memory; x = penalise(raw) / temperature.  Coalesced
+// 16-byte loads, eight in flight per thread.
 template <int DT, bool VEC>
 struct GlobalSrc {
   typedef typename Elem<DT>::T E;
-  static constexpr int W = VEC ? Elem<DT>::kVec : 1;  // 16 bytes per load
+  static constexpr int W = VEC ? Elem<DT>::kVec : 1;
+  static constexpr int kInFlight = 8;
   typedef E Vec __attribute__((ext_vector_type(W)));
   const E *p;
   int V;
@@ -203,17 +213,14 @@ struct GlobalSrc {
     const int nv = V / W;
     const Vec *pv = reinterpret_cast<const Vec *>(p);
     int v = threadIdx.x;
-    for (; v + 3 * kThreads < nv; v += 4 * kThreads) {
-      const Vec a0 = pv[v], a1 = pv[v + kThreads], a2 = pv[v + 2 * kThreads],
-                a3 = pv[v + 3 * kThreads];
+    for (; v + (kInFlight - 1) * kThreads < nv; v += kInFlight * kThreads) {
+      Vec a[kInFlight];
 #pragma unroll
-      for (int j = 0; j < W; ++j) f(v * W + j, a0[j]);
+      for (int u = 0; u < kInFlight; ++u) a[u] = pv[v + u * kThreads];
 #pragma unroll
-      for (int j = 0; j < W; ++j) f((v + kThreads) * W + j, a1[j]);
+      for (int u = 0; u < kInFlight; ++u)
 #pragma unroll
-      for (int j = 0; j < W; ++j) f((v + 2 * kThreads) * W + j, a2[j]);
-#pragma unroll
-      for (int j = 0; j < W; ++j) f((v + 3 * kThreads) * W + j, a3[j]);
+        for (int j = 0; j < W; ++j) f((v + u * kThreads) * W + j, a[u][j]);
     }
     for (; v < nv; v += kThreads) {
       const Vec a = pv[v];
@@ -225,194 +232,238 @@ struct GlobalSrc {
   template <class F> __device__ __forceinline__ void each(F f) const {
     each_raw([&](int i, E raw) { f(i, x(i, raw)); });
   }
-  template <class F> __device__ __forceinline__ void chunk(F f) const {
-    const int per = ((V + kThreads - 1) / kThreads + W - 1) / W * W;
-    const int lo = min(V, static_cast<int>(threadIdx.x) * per), hi = min(V, lo + per);
-    int i = lo;
-    // Four 16-byte loads in flight per iteration.
-    for (; i + 4 * W <= hi; i += 4 * W) {
-      const Vec *q = reinterpret_cast<const Vec *>(p + i);
-      const Vec a0 = q[0], a1 = q[1], a2 = q[2], a3 = q[3];
+  // f(i, v) with v the penalised logit, not divided by the temperature (an
+  // order-preserving map of x): one bitmap word per vector, none without
+  // history.
+  template <class F> __device__ __forceinline__ void each_pen(F f, bool has_hist) const {
+    const int nv = V / W;
+    const Vec *pv = reinterpret_cast<const Vec *>(p);
+    auto one = [&](int b, const Vec &a) {
+      const uint32_t bits = has_hist ? (sh->seen[b >> 5] >> (b & 31)) : 0u;
 #pragma unroll
-      for (int j = 0; j < W; ++j) f(i + j, x(i + j, a0[j]));
+      for (int j = 0; j < W; ++j) {
+        float v = elem_to_f32<DT>(a[j]);
+        if ((bits >> j) & 1u) v = penalise_seen(P, *sh, b + j, v);
+        f(b + j, v);
+      }
+    };
+    int v = threadIdx.x;
+    for (; v + (kInFlight - 1) * kThreads < nv; v += kInFlight * kThreads) {
+      Vec a[kInFlight];
 #pragma unroll
-      for (int j = 0; j < W; ++j) f(i + W + j, x(i + W + j, a1[j]));
+      for (int u = 0; u < kInFlight; ++u) a[u] = pv[v + u * kThreads];
 #pragma unroll
-      for (int j = 0; j < W; ++j) f(i + 2 * W + j, x(i + 2 * W + j, a2[j]));
-#pragma unroll
-      for (int j = 0; j < W; ++j) f(i + 3 * W + j, x(i + 3 * W + j, a3[j]));
+      for (int u = 0; u < kInFlight; ++u) one((v + u * kThreads) * W, a[u]);
     }
-    for (; i + W <= hi; i += W) {
-      const Vec a = *reinterpret_cast<const Vec *>(p + i);
-#pragma unroll
-      for (int j = 0; j < W; ++j) f(i + j, x(i + j, a[j]));
+    for (; v < nv; v += kThreads) one(v * W, pv[v]);
+    for (int i = nv * W + threadIdx.x; i < V; i += kThreads) {
+      const float raw = elem_to_f32<DT>(p[i]);
+      f(i, has_hist ? penalise(P, *sh, i, raw) : raw);
     }
-    for (; i < hi; ++i) f(i, x(i, p[i]));
   }
 };
 
-// The candidates gathered into LDS (index order).
+// Candidates gathered into LDS (any order).
 struct CandSrc {
   const Shared *sh;
   int n;
   template <class F> __device__ __forceinline__ void each(F f) const {
     for (int j = threadIdx.x; j < n; j += kThreads) f(sh->ci[j], sh->cx[j]);
   }
-  template <class F> __device__ __forceinline__ void chunk(F f) const {
-    const int per = (n + kThreads - 1) / kThreads;
-    const int lo = min(n, static_cast<int>(threadIdx.x) * per), hi = min(n, lo + per);
-    for (int j = lo; j < hi; ++j) f(sh->ci[j], sh->cx[j]);
+};
+
+// Every kSampleStride-th element of the row, gathered into the candidate value
+// array before the candidates themselves are.
+constexpr int kSampleStride = 32;
+struct SampleSrc {
+  const Shared *sh;
+  int n;
+  template <class F> __device__ __forceinline__ void each(F f) const {
+    for (int j = threadIdx.x; j < n; j += kThreads) f(j, sh->cx[j]);
   }
 };
 
-// min_p -> top_k -> top_p -> draw over a source; returns the token.  `Z_all`
-// (when have_Z) is the alive mass of the whole row, needed when the source is
-// a candidate subset and no top-k cut bounds the survivors inside it.
-template <class Src>
-__device__ __forceinline__ int64_t filter_and_draw(const Src src, Shared &sh, const Params P, float m,
-                                   long long k_req, bool have_Z, unsigned long long Z_all,
-                                   float u) {
-  auto alive = [&](float x) { return P.min_p <= 0.f || expf(x - m) >= P.min_p; };
+// ---- order statistics over a source ---------------------------------------------------
+// All cuts below are prefixes of one total order: key descending, then index
+// ascending.  They are found with radix selects (11/11/10-bit digits of the
+// key, 10/10-bit digits of the index), so no pass depends on visiting order.
 
-  // top-k: cut (Kk, tk) on element counts.
-  uint32_t Kk = 0;                // elements with key > Kk are kept
-  unsigned long long tk = ~0ull;  // ties at Kk kept, in index order (~0: all)
+// Key of the k-th largest element (k >= 1) among those where pred(i, x) holds;
+// `above` gets how many have a larger key.
+template <class Src, class Pred>
+__device__ __forceinline__ uint32_t radix_rank(const Src &src, Shared &sh, unsigned long long k,
+                                               Pred pred, unsigned long long &above) {
+  uint32_t prefix = 0;
+  above = 0;
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
+    const int hi_shift = shift + (pass == 2 ? 10 : 11);
+    zero_hist(sh);
+    src.each([&](int i, float x) {
+      if (!pred(i, x)) return;
+      const uint32_t key = fkey(x);
+      if (pass > 0 && (key >> hi_shift) != (prefix >> hi_shift)) return;
+      atomicAdd(&sh.hist[(key >> shift) & dmask], 1ull);
+    });
+    __syncthreads();
+    select_bin(sh, above, static_cast<double>(k));
+    prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
+    above = sh.bcast[1];
+  }
+  return prefix;
+}
+
+// Key K where the fixed-point mass of the pred elements, accumulated from the
+// largest key down, reaches `target`: mass(keys > K) < target <=
+// mass(keys >= K).  `extra` is mass to count at key Kx besides the visited
+// elements (ties whose membership is decided by index).  Returns false if
+// the total is below target.
+template <class Src, class Pred>
+__device__ __forceinline__ bool mass_select(const Src &src, Shared &sh, Pred pred, float m,
+                                            double target, uint32_t Kx, unsigned long long extra,
+                                            uint32_t &K, unsigned long long &above) {
+  uint32_t prefix = 0;
+  above = 0;
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
+    const int hi_shift = shift + (pass == 2 ? 10 : 11);
+    zero_hist(sh);
+    src.each([&](int i, float x) {
+      if (!pred(i, x)) return;
+      const uint32_t key = fkey(x);
+      if (pass > 0 && (key >> hi_shift) != (prefix >> hi_shift)) return;
+      atomicAdd(&sh.hist[(key >> shift) & dmask], mass_of(x, m));
+    });
+    __syncthreads();
+    if (threadIdx.x == 0 && extra && (pass == 0 || (Kx >> hi_shift) == (prefix >> hi_shift)))
+      sh.hist[(Kx >> shift) & dmask] += extra;
+    __syncthreads();
+    select_bin(sh, above, target);
+    if (!sh.bcast[2]) return false;
+    prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
+    above = sh.bcast[1];
+  }
+  K = prefix;
+  return true;
+}
+
+// Index of the j-th smallest index (j >= 1) among the pred elements (indices
+// below 2^20; the vocabulary limit is 2^18).
+template <class Src, class Pred>
+__device__ __forceinline__ int index_rank(const Src &src, Shared &sh, unsigned long long j,
+                                          Pred pred) {
+  // Ascending index = descending (2^20 - 1 - index).
+  uint32_t prefix = 0;
+  unsigned long long above = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int shift = pass == 0 ? 10 : 0;
+    zero_hist(sh);
+    src.each([&](int i, float x) {
+      if (!pred(i, x)) return;
+      const uint32_t r = 0xfffffu - static_cast<uint32_t>(i);
+      if (pass > 0 && (r >> 10) != (prefix >> 10)) return;
+      atomicAdd(&sh.hist[(r >> shift) & 0x3ffu], 1ull);
+    });
+    __syncthreads();
+    select_bin(sh, above, static_cast<double>(j));
+    prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
+    above = sh.bcast[1];
+  }
+  return static_cast<int>(0xfffffu - prefix);
+}
+
+template <class Src, class Pred>
+__device__ __forceinline__ unsigned long long count_if(const Src &src, Shared &sh, Pred pred) {
+  unsigned long long c = 0, total;
+  src.each([&](int i, float x) { c += pred(i, x) ? 1 : 0; });
+  block_exclusive_scan(c, sh, &total);
+  return total;
+}
+
+template <class Src, class Pred>
+__device__ __forceinline__ unsigned long long mass_if(const Src &src, Shared &sh, float m, Pred pred) {
+  unsigned long long z = 0, total;
+  src.each([&](int i, float x) {
+    if (pred(i, x)) z += mass_of(x, m);
+  });
+  block_exclusive_scan(z, sh, &total);
+  return total;
+}
+
+// min_p -> top_k -> top_p -> draw over a source; returns the token.  `Z_all`
+// (when have_Z) is the alive mass of the whole row, used when the source is a
+// candidate subset and no top-k cut bounds the survivors inside it.
+template <class Src>
+__device__ __forceinline__ int64_t filter_and_draw(const Src src, Shared &sh, const Params P,
+                                                   float m, long long k_req, bool have_Z,
+                                                   unsigned long long Z_all, float u) {
+  auto alive = [&](float x) { return P.min_p <= 0.f || expf(x - m) >= P.min_p; };
+  constexpr int kAll = 0x7fffffff;
+
+  // top-k: kept = key > Kk, or key == Kk and index <= Ik.
+  uint32_t Kk = 0;
+  int Ik = kAll;
+  bool k_cut = false;
   if (k_req > 0) {
-    unsigned long long c = 0;
-    src.each([&](int, float x) { c += alive(x) ? 1 : 0; });
-    unsigned long long alive_cnt;
-    block_exclusive_scan(c, sh, &alive_cnt);
+    const unsigned long long alive_cnt = count_if(src, sh, [&](int, float x) { return alive(x); });
     if (static_cast<unsigned long long>(k_req) < alive_cnt) {
-      uint32_t prefix = 0;
-      unsigned long long above = 0;
-      for (int pass = 0; pass < 3; ++pass) {
-        const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-        const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
-        const int hi_shift = shift + (pass == 2 ? 10 : 11);
-        zero_hist(sh);
-        src.each([&](int, float x) {
-          if (!alive(x)) return;
-          const uint32_t k = fkey(x);
-          if (pass > 0 && (k >> hi_shift) != (prefix >> hi_shift)) return;
-          atomicAdd(&sh.hist[(k >> shift) & dmask], 1ull);
-        });
-        __syncthreads();
-        select_bin(sh, above, static_cast<double>(k_req));
-        prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
-        above = sh.bcast[1];
-      }
-      Kk = prefix;
-      tk = static_cast<unsigned long long>(k_req) - above;
+      unsigned long long above;
+      Kk = radix_rank(src, sh, static_cast<unsigned long long>(k_req),
+                      [&](int, float x) { return alive(x); }, above);
+      Ik = index_rank(src, sh, static_cast<unsigned long long>(k_req) - above,
+                      [&](int, float x) { return alive(x) && fkey(x) == Kk; });
+      k_cut = true;
     }
   }
-  const bool k_partial = tk != ~0ull;
-  auto in_s_nontie = [&](float x, uint32_t k) {
-    return alive(x) && (k > Kk || (k == Kk && !k_partial));
+  auto in_s = [&](int i, float x) {
+    const uint32_t k = fkey(x);
+    return alive(x) && (k > Kk || (k == Kk && i <= Ik));
   };
-  const unsigned long long wK = k_partial ? mass_of(unkey(Kk), m) : 0;
 
-  // top-p: cut (Kf, tf) on the survivors' probability mass.
+  // top-p over the survivors: kept = in_s and (key > Kf, or key == Kf and
+  // index <= If), the shortest prefix whose mass reaches top_p of theirs.
   uint32_t Kf = Kk;
-  unsigned long long tf = tk;
+  int If = Ik;
   if (P.top_p < 1.f) {
-    unsigned long long Z;
-    if (have_Z && !k_partial) {
-      Z = Z_all;
-    } else {
-      unsigned long long z = 0;
-      src.each([&](int, float x) {
-        if (in_s_nontie(x, fkey(x))) z += mass_of(x, m);
-      });
-      block_exclusive_scan(z, sh, &Z);
-      if (k_partial) Z += tk * wK;
-    }
+    const unsigned long long Z = (have_Z && !k_cut) ? Z_all : mass_if(src, sh, m, in_s);
     const double target = static_cast<double>(P.top_p) * static_cast<double>(Z);
-    uint32_t prefix = 0;
-    unsigned long long above = 0;
-    bool found = true;
-    for (int pass = 0; pass < 3 && found; ++pass) {
-      const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-      const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
-      const int hi_shift = shift + (pass == 2 ? 10 : 11);
-      zero_hist(sh);
-      src.each([&](int, float x) {
-        const uint32_t k = fkey(x);
-        if (!in_s_nontie(x, k)) return;
-        if (pass > 0 && (k >> hi_shift) != (prefix >> hi_shift)) return;
-        atomicAdd(&sh.hist[(k >> shift) & dmask], mass_of(x, m));
-      });
-      __syncthreads();
-      // The kept ties of the top-k cut all weigh wK: add them analytically.
-      if (threadIdx.x == 0 && k_partial && (pass == 0 || (Kk >> hi_shift) == (prefix >> hi_shift)))
-        sh.hist[(Kk >> shift) & dmask] += tk * wK;
-      __syncthreads();
-      select_bin(sh, above, target);
-      found = sh.bcast[2] != 0;
-      prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
-      above = sh.bcast[1];
-    }
-    if (found) {
-      Kf = prefix;
-      const unsigned long long w = mass_of(unkey(Kf), m);
-      // Ties at Kf kept: the first j with above + (j - 1) * w < target.
+    uint32_t K;
+    unsigned long long above;
+    if (mass_select(src, sh, in_s, m, target, 0u, 0ull, K, above)) {
+      const unsigned long long w = mass_of(unkey(K), m);
+      // Ties at K kept: the first j (by index) with above + (j - 1) * w < target.
       unsigned long long j =
           w ? static_cast<unsigned long long>(ceil((target - static_cast<double>(above)) / static_cast<double>(w)))
             : 1;
       if (j < 1) j = 1;
-      if (Kf == Kk && k_partial && j > tk) j = tk;
-      tf = j;
+      auto tie = [&](int i, float x) { return in_s(i, x) && fkey(x) == K; };
+      const unsigned long long c = count_if(src, sh, tie);
+      Kf = K;
+      If = j >= c ? kAll : index_rank(src, sh, j, tie);
     }
   }
-
-  // Draw: inverse CDF in index order over the kept weights.  Ties at Kf are
-  // ranked by a scan of per-thread tie counts.
-  const bool f_partial = tf != ~0ull;
-  unsigned long long wsum = 0, ties = 0;
-  src.chunk([&](int, float x) {
+  auto kept = [&](int i, float x) {
     const uint32_t k = fkey(x);
-    if (!alive(x) || k < Kf) return;
-    if (k == Kf && f_partial) {
-      ++ties;
-      return;
-    }
-    wsum += mass_of(x, m);
-  });
-  unsigned long long tot_ties;
-  const unsigned long long rank0 = block_exclusive_scan(ties, sh, &tot_ties);
-  unsigned long long kept_ties = 0;
-  if (f_partial) kept_ties = rank0 >= tf ? 0 : (tf - rank0 < ties ? tf - rank0 : ties);
-  const unsigned long long wf = f_partial ? mass_of(unkey(Kf), m) : 0;
-  const unsigned long long mine = wsum + kept_ties * wf;
-  unsigned long long Wtot;
-  const unsigned long long before = block_exclusive_scan(mine, sh, &Wtot);
-  unsigned long long target =
-      static_cast<unsigned long long>(static_cast<double>(u) * static_cast<double>(Wtot));
-  if (target >= Wtot) target = Wtot ? Wtot - 1 : 0;
-  if (threadIdx.x == 0) sh.bcast[3] = 0;  // unreachable fallback: the top element always weighs 2^40
-  __syncthreads();
-  if (mine > 0 && before <= target && target < before + mine) {
-    unsigned long long acc = before, seen_ties = 0;
-    bool done = false;
-    src.chunk([&](int i, float x) {
-      if (done) return;
-      const uint32_t k = fkey(x);
-      if (!alive(x) || k < Kf) return;
-      unsigned long long w;
-      if (k == Kf && f_partial) {
-        if (seen_ties++ >= kept_ties) return;
-        w = wf;
-      } else {
-        w = mass_of(x, m);
-      }
-      acc += w;
-      if (acc > target) {
-        sh.bcast[3] = static_cast<unsigned long long>(i);
-        done = true;
-      }
-    });
+    return in_s(i, x) && (k > Kf || (k == Kf && i <= If));
+  };
+
+  // Draw: the element whose interval of the kept mass, accumulated in the same
+  // order (key descending, index ascending), holds u * total.
+  const unsigned long long Wtot = mass_if(src, sh, m, kept);
+  unsigned long long T = static_cast<unsigned long long>(static_cast<double>(u) * static_cast<double>(Wtot));
+  if (T >= Wtot) T = Wtot ? Wtot - 1 : 0;
+  uint32_t K;
+  unsigned long long above;
+  if (!mass_select(src, sh, kept, m, static_cast<double>(T) + 1.0, 0u, 0ull, K, above)) {
+    // Unreachable: the largest kept element always weighs 2^40.
+    return static_cast<int64_t>(index_rank(src, sh, 1, kept));
   }
-  __syncthreads();
-  return static_cast<int64_t>(sh.bcast[3]);
+  const unsigned long long w = mass_of(unkey(K), m);
+  const unsigned long long jt = w ? (T - above) / w : 0;
+  return static_cast<int64_t>(
+      index_rank(src, sh, jt + 1, [&](int i, float x) { return kept(i, x) && fkey(x) == K; }));
 }
 
 template <int DT, bool VEC>
@@ -442,8 +493,9 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
   if (P.use_hash)
     for (int s = tid; s < kHashSlots; s += kThreads) sh.hkey[s] = 0, sh.hcnt[s] = 0;
   __syncthreads();
+  int nh = 0;
   if (history && hist_len) {
-    int nh = hist_len[row * hist_len_stride];
+    nh = hist_len[row * hist_len_stride];
     // At most one row of history (the row stride) and kMaxHist tokens.
     const int64_t cap = hist_stride < kMaxHist ? hist_stride : kMaxHist;
     nh = nh < 0 ? 0 : (nh > cap ? static_cast<int>(cap) : nh);
@@ -488,67 +540,57 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
   const long long k_req = (P.top_k < 0 || P.top_k >= V) ? -1 : P.top_k;
   const float u = uniforms ? uniforms[row] : 0.f;
 
-  // ---- pass A: max, and the top-digit count histogram for a top-k cut ----------
-  zero_hist(sh);
-  float m = -INFINITY;
-  g.each([&](int, float x) {
-    m = fmaxf(m, x);
-    if (k_req > 0) atomicAdd(&sh.hist[fkey(x) >> 21], 1ull);
-  });
-  m = block_max(m, sh);
-  auto alive = [&](float x) { return P.min_p <= 0.f || expf(x - m) >= P.min_p; };
+  // ---- pass A (on the penalised logits v; x = v / temperature preserves
+  // their order): max, and (for a top-k cut) every 32nd value as a sample ----
+  const bool has_hist = nh > 0;
+  float mv = -INFINITY;
+  const bool sample = k_req > 0;
+  g.each_pen([&](int i, float v) {
+    mv = fmaxf(mv, v);
+    if (sample && (i % kSampleStride) == 0) sh.cx[i / kSampleStride] = v;
+  }, has_hist);
+  mv = block_max(mv, sh);
+  const float m = mv / P.temp;  // the largest x
 
-  // ---- candidate bound: every kept element has key >= L --------------------------
-  // With top-k: the first-digit bin of the k-th largest element (alive or not:
-  // the k largest alive are the k largest when k are alive, and otherwise all
-  // alive elements are above that bin anyway).  With top-p only: the
-  // first-digit bin where the alive mass, from the top, reaches top_p of the
-  // whole.
-  bool fast = false, have_Z = false;
-  uint32_t L = 0;
-  unsigned long long Z_all = 0;
+  // ---- candidates: with a top-k cut, the elements at or above the r-th
+  // largest sample, r a margin above k / kSampleStride.  If they number at
+  // least k and fit in LDS, the k largest (alive or not) are among them, and
+  // so is everything any later cut keeps.  Otherwise, and without a top-k
+  // cut, the row itself is the source.  The bound is taken 64 key steps low:
+  // an element just under it in v may round to the same x as one above it.
+  int64_t tok = -1;
   if (k_req > 0) {
-    select_bin(sh, 0, static_cast<double>(k_req));
-    L = static_cast<uint32_t>(sh.bcast[0]) << 21;
-    fast = sh.bcast[1] + sh.hist[sh.bcast[0]] <= static_cast<unsigned long long>(kCand);
-  } else if (P.top_p < 1.f) {
-    zero_hist(sh);
-    g.each([&](int, float x) {
-      if (alive(x)) atomicAdd(&sh.hist[fkey(x) >> 21], mass_of(x, m));
-    });
+    SampleSrc smp_src;
+    smp_src.sh = &sh;
+    smp_src.n = (V + kSampleStride - 1) / kSampleStride;
+    const long long kk = (k_req + kSampleStride - 1) / kSampleStride;
+    const long long r = min<long long>(smp_src.n, kk + (kk + 1) / 2 + 8);
+    unsigned long long above;
+    const uint32_t Ls =
+        radix_rank(smp_src, sh, static_cast<unsigned long long>(r), [](int, float) { return true; }, above);
+    const uint32_t L = Ls > 64u ? Ls - 64u : 0u;
+    // Unordered append; the counter keeps counting past the capacity.
     __syncthreads();
-    unsigned long long mine = 0;
-    for (int b = tid; b < kBins; b += kThreads) mine += sh.hist[b];
-    block_exclusive_scan(mine, sh, &Z_all);
-    select_bin(sh, 0, static_cast<double>(P.top_p) * static_cast<double>(Z_all));
-    L = static_cast<uint32_t>(sh.bcast[0]) << 21;
-    have_Z = fast = sh.bcast[2] != 0;
-  }
-  int64_t tok;
-  if (fast) {
-    // Ordered compaction of the elements with key >= L into LDS.
-    unsigned long long c = 0;
-    g.chunk([&](int, float x) { c += fkey(x) >= L ? 1 : 0; });
-    unsigned long long n_c;
-    const unsigned long long off = block_exclusive_scan(c, sh, &n_c);
-    fast = n_c <= static_cast<unsigned long long>(kCand);
-    if (fast) {
-      int o = static_cast<int>(off);
-      g.chunk([&](int i, float x) {
-        if (fkey(x) >= L) {
-          sh.cx[o] = x;
-          sh.ci[o] = i;
-          ++o;
-        }
-      });
-      __syncthreads();
+    if (tid == 0) sh.bcast[3] = 0;
+    __syncthreads();
+    g.each_pen([&](int i, float v) {
+      if (fkey(v) < L) return;
+      const unsigned long long o = atomicAdd(&sh.bcast[3], 1ull);
+      if (o < static_cast<unsigned long long>(kCand)) {
+        sh.cx[o] = v / P.temp;
+        sh.ci[o] = i;
+      }
+    }, has_hist);
+    __syncthreads();
+    const unsigned long long n_c = sh.bcast[3];
+    if (n_c <= static_cast<unsigned long long>(kCand) && n_c >= static_cast<unsigned long long>(k_req)) {
       CandSrc cs;
       cs.sh = &sh;
       cs.n = static_cast<int>(n_c);
-      tok = filter_and_draw(cs, sh, P, m, k_req, have_Z, Z_all, u);
+      tok = filter_and_draw(cs, sh, P, m, k_req, false, 0, u);
     }
   }
-  if (!fast) tok = filter_and_draw(g, sh, P, m, k_req, false, 0, u);
+  if (tok < 0) tok = filter_and_draw(g, sh, P, m, k_req, false, 0, u);
   if (tid == 0) out[row] = tok;
 }
 

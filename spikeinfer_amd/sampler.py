@@ -9,10 +9,11 @@ Differences from the reference that a caller can observe:
   * equal logits are ordered by index (the reference leaves that to
     ``torch.topk``), so which of two tied tokens a top-k/top-p cut keeps is
     fixed;
-  * the draw is the inverse CDF, in index order, of the kept weights at a
-    uniform ``u`` that the caller supplies (``torch.rand`` by default, a
-    per-request ``torch.Generator`` for seeded requests), where the reference
-    calls ``torch.multinomial``: the same distribution, a different stream.
+  * the draw is the inverse CDF of the kept weights, tokens taken by value
+    descending (index ascending on ties), at a uniform ``u`` that the caller
+    supplies (``torch.rand`` by default, a per-request ``torch.Generator`` for
+    seeded requests), where the reference calls ``torch.multinomial``: the
+    same distribution, a different stream.
 """
 from __future__ import annotations
 

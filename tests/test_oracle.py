@@ -291,13 +291,14 @@ def test_prefill_zero_query_is_running_mean():
 
 # ---- sampler oracle (spikeinfer/engine/sampler.py semantics) ----------------
 def test_sample_closed_form_distribution():
-    """logits ln(1..4): probabilities k/10, CDF boundaries at .1, .3, .6."""
+    """logits ln(1..4): probabilities k/10, drawn largest first, so the draw's
+    boundaries are at .4, .7, .9."""
     lg = np.log(np.arange(1, 5, dtype=np.float64)).astype(np.float32)
-    _, kept, probs, _ = orc.sample_row(lg)
-    assert kept.all()
+    _, kept, probs, _, order = orc.sample_row(lg)
+    assert kept.all() and order.tolist() == [3, 2, 1, 0]
     np.testing.assert_allclose(probs, [0.1, 0.2, 0.3, 0.4], atol=1e-7)
-    toks = [orc.sample_row(lg, u=u)[0] for u in (0.05, 0.15, 0.29, 0.31, 0.59, 0.61, 0.99)]
-    assert toks == [0, 1, 1, 2, 2, 3, 3]
+    toks = [orc.sample_row(lg, u=u)[0] for u in (0.05, 0.39, 0.41, 0.69, 0.71, 0.89, 0.91, 0.99)]
+    assert toks == [3, 3, 2, 2, 1, 1, 0, 0]
 
 
 def test_sample_top_k_top_p_min_p_known_answers():

@@ -1,9 +1,10 @@
 """The HIP sampler against the sampler oracle (oracle.sample_row, a numpy
 restatement of spikeinfer/engine/sampler.py:48-177) on identical logits and
 uniforms.  The kernel's token must be in the oracle's kept set and its
-interval of the oracle's index-order CDF must contain u (widened by 1e-6, the
-float32 weights' rounding); where u is farther than that from every boundary
-this is the same token as the oracle's.  Rows whose filter cut lies within
+interval of the oracle's CDF (kept tokens by value descending, index
+ascending) must contain u (widened by 1e-6, the float32 weights' rounding);
+where u is farther than that from every boundary this is the same token as
+the oracle's.  Rows whose filter cut lies within
 rounding of its boundary (oracle margin < 1e-6) only need a kept token, and
 must stay rare."""
 from __future__ import annotations
@@ -66,7 +67,7 @@ def test_sampler_matches_oracle(gpu, case, dtype):
     skipped = 0
     for i in range(rows):
         p = params[i]
-        tok, kept, _probs, margin = orc.sample_row(
+        tok, kept, _probs, margin, order = orc.sample_row(
             used[i], temperature=p.get("temperature", 1.0), top_k=p.get("top_k", -1),
             top_p=p.get("top_p", 1.0), min_p=p.get("min_p", 0.0), rep=p.get("rep", 1.0),
             presence=p.get("presence", 0.0), frequency=p.get("frequency", 0.0),
@@ -76,8 +77,9 @@ def test_sampler_matches_oracle(gpu, case, dtype):
             continue
         t = got[i]
         assert kept[t], f"row {i}: token {t} not kept (oracle {tok})"
-        cdf = np.cumsum(_probs)
-        lo, hi = cdf[t] - _probs[t], cdf[t]
+        cdf = np.cumsum(_probs[order])
+        pos = int(np.nonzero(order == t)[0][0])
+        lo, hi = cdf[pos] - _probs[t], cdf[pos]
         assert lo - 1e-6 <= us[i] <= hi + 1e-6, f"row {i}: u={us[i]} outside [{lo}, {hi}] of {t}"
         if lo + 1e-6 < us[i] < hi - 1e-6:
             assert t == tok
@@ -94,11 +96,11 @@ def test_sampler_ties_and_tiny_vocab(gpu):
 
 
 def test_sampler_uniform_sweep_follows_closed_form(gpu):
-    """logits ln(1..4): CDF boundaries at 0.1, 0.3, 0.6 (index order)."""
+    """logits ln(1..4): drawn largest first, boundaries at 0.4, 0.7, 0.9."""
     lg = np.log(np.arange(1, 5, dtype=np.float64)).astype(np.float32)
-    us = [0.05, 0.15, 0.29, 0.31, 0.59, 0.61, 0.99]
+    us = [0.05, 0.39, 0.41, 0.69, 0.71, 0.89, 0.91, 0.99]
     got, _ = _run(gpu, np.stack([lg] * len(us)), [dict()] * len(us), [[]] * len(us), us)
-    assert got == [0, 1, 1, 2, 2, 3, 3]
+    assert got == [3, 3, 2, 2, 1, 1, 0, 0]
 
 
 def test_sampler_history_len_shared_count(gpu):
