@@ -277,6 +277,7 @@ int spk_sample(const void *logits, int logits_dtype, int64_t row_stride, int row
 size_t spk_sample_shared_bytes(void);
 
 
+
 #ifdef __cplusplus
 }
 #endif
