@@ -246,7 +246,8 @@ extern "C" size_t spk_decode_attn_workspace_bytes(int T, int N, int Hq, int Hkv,
   const int64_t nparts = (ctx_max + part - 1) / part;
   // Partial sums of split contexts, then the launch order of long contexts.
   const size_t partials = nparts <= 1 ? 0 : (size_t)nparts * T * N * Hq * (head_dim + 1) * sizeof(float);
-  const size_t order = plan_launch(ctx_max) ? ((size_t)nparts * N * T * Hkv + 1) * sizeof(int32_t) : 0;
+  const int64_t items = nparts * N;
+  const size_t order = plan_in_workspace(ctx_max, items) ? ((size_t)items * T * Hkv + 1) * sizeof(int32_t) : 0;
   return partials + order;
 }
 
@@ -299,8 +300,10 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
   if (!force_general && mfma_path_supported(p)) {
     build_digit_table(scale, p.digits);
     const size_t partial_floats = p.num_parts > 1 ? (size_t)p.num_parts * T * N * Hq * (head_dim + 1) : 0;
-    int32_t *order = plan_launch(ctx_max) ? reinterpret_cast<int32_t *>(p.ws + partial_floats) : nullptr;
-    launch_decode_mfma(p, order, s);
+    const bool plan = plan_launch(ctx_max);
+    int32_t *order = plan_in_workspace(ctx_max, (int64_t)p.num_parts * N)
+                         ? reinterpret_cast<int32_t *>(p.ws + partial_floats) : nullptr;
+    launch_decode_mfma(p, plan, order, s);
   } else switch (W) {
     case 1: launch_general<1>(p, grid, s); break;
     case 2: launch_general<2>(p, grid, s); break;

@@ -35,6 +35,9 @@ struct AttnParams {
   // work item (part * units + unit) of block b, longest first; order[items]
   // holds the number of items.  nullptr: block (unit, part) = (x, y).
   const int32_t *order;
+  // Matrix-core path: the main kernel computes the longest-first order itself
+  // (N * num_parts <= kInlinePlanItems) instead of reading `order`.
+  int plan_inline;
   // Matrix-core path: for d = popc(q & ~k) in 0..64, the four e4m3 digits of
   // exp(-d*scale) * 2^8 (byte s weighs 2^-(4s)), built on the host once per
   // scale (build_digit_table) and copied into LDS by every workgroup.
@@ -59,10 +62,17 @@ inline int choose_part_len(int64_t units, int64_t ctx_max, int block_size) {
 // Matrix-core path for head_dim 64, n_rep <= 8 (decode_attn_mfma.hip).
 // Returns false when the shape or alignment does not qualify.
 bool mfma_path_supported(const AttnParams &p);
-// Launches the matrix-core kernel, preceded, for long contexts
-// (plan_launch), by the planner that fills `order` (units * num_parts + 1
-// ints of scratch).
+// Long contexts (plan_launch) are launched longest first.  Up to
+// kInlinePlanItems (sequence, partition) items the main kernel orders them
+// itself; beyond, a planner kernel first writes the order into `order`
+// (items + 1 ints of workspace, plan_in_workspace).
 inline bool plan_launch(int64_t ctx_max) { return ctx_max >= 8192; }
-void launch_decode_mfma(AttnParams p, int32_t *order, hipStream_t s);
+constexpr int kInlinePlanItems = 4096;
+inline bool plan_in_workspace(int64_t ctx_max, int64_t items) {
+  return plan_launch(ctx_max) && items > kInlinePlanItems;
+}
+// Launches the matrix-core kernel; `plan` orders it longest first, from
+// `order` when not null (after the planner kernel fills it), else in-kernel.
+void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s);
 
 }  // namespace spk

@@ -163,6 +163,88 @@ __device__ __forceinline__ void contract_half(const WaveStage &st, int lane, int
   accl = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, Bl, accl, 0, 4, 0, 127, 0, 127);
 }
 
+// Longest-processing-time-first order of the (sequence, partition) items,
+// computed by every workgroup for itself: slot q of the order is the item of
+// the q-th largest size bucket (256 tokens wide), ties in item order (item i =
+// part * N + sequence).  Items are counted into an LDS histogram, the buckets
+// scanned largest first, and the slot's item found by a block-wide prefix
+// count of that bucket's members.  Returns -1 past the last existing item
+// (uniform over the block).  Needs N * num_parts <= kInlinePlanItems; `sh`
+// holds kMaxBuckets + 8 ints and is free again after the call.
+constexpr int kMaxBuckets = 130;  // part_len <= 32768 tokens, 256 per bucket
+__device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh) {
+  constexpr int kThreads = kWaves * 64;
+  int *count = sh, *wsum = sh + kMaxBuckets, *res = wsum + kWaves;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int M = p.N * p.num_parts;
+  const int nb = (p.part_len >> 8) + 2;
+  // Bucket of item i, -1 when the sequence has no such partition.
+  auto key = [&](int i) {
+    const int n = i % p.N, part = i / p.N;
+    const int len = p.lens[n];
+    const int nparts = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
+    if (part >= nparts) return -1;
+    const int size = min(p.part_len, len - part * p.part_len);
+    return size <= 0 ? 0 : ((size + 255) >> 8) + 1;
+  };
+  for (int b = tid; b < nb; b += kThreads) count[b] = 0;
+  __syncthreads();
+  const int per = (M + kThreads - 1) / kThreads;
+  const int i0 = min(M, tid * per), i1 = min(M, i0 + per);
+  for (int i = i0; i < i1; ++i) {
+    const int k = key(i);
+    if (k >= 0) atomicAdd(&count[k], 1);
+  }
+  __syncthreads();
+  if (wave == 0) {  // largest bucket first: lane holds list positions 3*lane..3*lane+2
+    int c[3], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const int pos = 3 * lane + k;
+      c[k] = pos < nb ? count[nb - 1 - pos] : 0;
+      sum += c[k];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      if (run <= q && q < run + c[k]) {
+        res[0] = nb - 1 - (3 * lane + k);
+        res[1] = q - run;
+      }
+      run += c[k];
+    }
+    if (lane == 63 && q >= incl) res[0] = -1;
+  }
+  __syncthreads();
+  const int sel = res[0], j = res[1];
+  if (sel < 0) return -1;
+  int mine = 0;
+  for (int i = i0; i < i1; ++i) mine += key(i) == sel;
+  int incl = mine;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int before = incl - mine;
+  for (int w = 0; w < wave; ++w) before += wsum[w];
+  if (before <= j && j < before + mine) {
+    int r = j - before;
+    for (int i = i0; i < i1; ++i)
+      if (key(i) == sel && r-- == 0) res[2] = i;
+  }
+  __syncthreads();
+  return res[2];
+}
+
 // One workgroup = 4 waves = one (partition, t, kv head, sequence); waves take
 // the partition's 128-token steps round-robin (two steps of loads in flight
 // per wave) and reduce at the end in a fixed order.
@@ -173,7 +255,14 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6))
   // sibling units of equal length.
   const int units = p.N * p.T * p.Hkv;
   int unit = blockIdx.x, part = blockIdx.y;
-  if (p.order) {  // planned launch: longest work items first
+  __shared__ __align__(16) char smem[kSmemBytes];
+  if (p.plan_inline) {  // planned launch: longest work items first
+    const int ups = p.T * p.Hkv;
+    const int i = plan_slot(p, (int)blockIdx.x / ups, reinterpret_cast<int *>(smem));
+    if (i < 0) return;
+    unit = (i % p.N) * ups + (int)blockIdx.x % ups;
+    part = i / p.N;
+  } else if (p.order) {
     const int items = units * p.num_parts;
     if ((int)blockIdx.x >= p.order[items]) return;
     const int item = p.order[blockIdx.x];
@@ -195,7 +284,6 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6))
 
   __shared__ uint32_t tab[65];                // per d: 4 e4m3 digits of exp(-d*scale)
   __shared__ int32_t blocks[kMaxPartBlocks];  // this partition's physical blocks
-  __shared__ __align__(16) char smem[kSmemBytes];
   WaveStage &st = reinterpret_cast<WaveStage *>(smem)[wave];
 
   if (tid <= 64) tab[tid] = p.digits[tid];
@@ -422,7 +510,6 @@ namespace mfma {
 __global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, int N, int UPS,
                                                         int part_len, int num_parts,
                                                         int32_t *order) {
-  constexpr int kMaxBuckets = 130;  // part_len <= 32768 tokens, 256 per bucket
   __shared__ int count[kMaxBuckets];
   __shared__ int offset[kMaxBuckets];
   const int tid = threadIdx.x;
@@ -463,12 +550,16 @@ __global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, in
 
 }  // namespace mfma
 
-void launch_decode_mfma(AttnParams p, int32_t *order, hipStream_t s) {
+void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s) {
   const int threads = mfma::kWaves * 64;
   const int units = p.N * p.T * p.Hkv;
   dim3 grid(units, p.num_parts);
   p.order = nullptr;
-  if (order) {
+  p.plan_inline = 0;
+  if (plan && !order) {
+    p.plan_inline = 1;
+    grid = dim3(units * p.num_parts);
+  } else if (plan) {
     mfma::decode_attn_plan<<<1, 1024, 0, s>>>(p.lens, p.N, p.T * p.Hkv, p.part_len, p.num_parts,
                                               order);
     p.order = order;

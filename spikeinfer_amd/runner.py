@@ -7,7 +7,10 @@ holds the whole step -- forward, lm_head, sampling, and the advance of every
 row to its next position -- so consecutive replays need no host work at all.
 Static buffers follow the reference's capture conventions
 (model_runner.py:189-287): rows past the live batch point at the cache's pad
-block with ``seq_len = 1`` and never advance.
+block with ``seq_len = 1`` and never advance.  As there, one graph is captured
+per batch bucket (config.py:117-126: 1, 2, 4, ..., 64) and a batch runs in the
+smallest bucket that holds it; every bucket's graph works on a row prefix of
+the same static buffers, and all of them share one graph memory pool.
 """
 from __future__ import annotations
 
@@ -22,9 +25,13 @@ from .sampler import BatchSampler, SamplingParams, sample_tokens
 from .spike_cache import PagedSpikeCache, slot_mapping
 
 
+DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64)
+
+
 class DecodeRunner:
     def __init__(self, model: SpikingDecoder, cache: PagedSpikeCache, batch_size: int,
-                 max_model_len: int, max_new_tokens: int = 2048) -> None:
+                 max_model_len: int, max_new_tokens: int = 2048,
+                 buckets: tuple[int, ...] = DEFAULT_BUCKETS) -> None:
         self.model = model
         self.cache = cache
         self.B = batch_size
@@ -38,32 +45,53 @@ class DecodeRunner:
         self.block_tables = torch.full((batch_size, self.max_blocks), cache.pad_block,
                                        dtype=torch.int32, device=dev)
         self.seq_lens = torch.ones(batch_size, dtype=torch.int32, device=dev)
-        self.meta = AttentionMetadata(slot_mapping=self.slot_mapping, block_size=self.bs,
-                                      num_decode_tokens=batch_size, block_tables=self.block_tables,
-                                      seq_lens=self.seq_lens)
-        self.bufs = {
-            "q_packed": torch.empty((model.T, batch_size, model.Hq, model.W), dtype=torch.int32, device=dev),
-            "attn": torch.empty((model.T, batch_size, model.Hq, model.D), dtype=model.dtype, device=dev),
-        }
+        self.meta = self._meta(batch_size)
+        # Buckets up to the batch size; the batch size itself is always one, so
+        # every live count up to it has a graph.
+        self.buckets = tuple(sorted({b for b in buckets if 0 < b < batch_size} | {batch_size}))
+        self._bufs: dict[int, dict[str, torch.Tensor]] = {}
         self.logits = torch.empty((batch_size, c.vocab_size), dtype=model.dtype, device=dev)
         self.sampler = BatchSampler(batch_size, dev)
         self.history = torch.zeros((batch_size, max_new_tokens), dtype=torch.int64, device=dev)
         self.step_count = torch.zeros(1, dtype=torch.int32, device=dev)
         self.live = torch.zeros(1, dtype=torch.int32, device=dev)  # rows that advance
-        self.graph: torch.cuda.CUDAGraph | None = None
+        self.n_live = 0
+        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self._free_blocks = list(range(cache.num_allocatable_blocks))
 
+    def _meta(self, b: int) -> AttentionMetadata:
+        return AttentionMetadata(slot_mapping=self.slot_mapping[:b], block_size=self.bs,
+                                 num_decode_tokens=b, block_tables=self.block_tables[:b],
+                                 seq_lens=self.seq_lens[:b])
+
+    def bucket_for(self, n: int) -> int:
+        """Smallest bucket holding ``n`` rows (model_runner.py:180-184)."""
+        for b in self.buckets:
+            if b >= n:
+                return b
+        raise ValueError(f"batch of {n} exceeds the runner's {self.B} rows")
+
     # -- one decode step (the captured body) ------------------------------------
-    def _step(self) -> None:
+    def _step(self, b: int | None = None) -> None:
+        """One decode step over rows ``[0, b)`` (default: the whole batch)."""
+        b = self.B if b is None else b
         m, s = self.model, self.sampler
-        hidden = m.forward_paged(self.input_ids, self.positions, self.cache.layers, self.meta, self.bufs)
-        m.compute_logits(hidden, out=self.logits)
-        s.uniforms.uniform_()
-        sample_tokens(self.logits, s.temperature, s.top_k, s.top_p, s.min_p, s.repetition_penalty,
-                      s.presence_penalty, s.frequency_penalty, self.history, self.step_count,
-                      s.uniforms, s.tokens)
+        if b not in self._bufs:
+            self._bufs[b] = {
+                "q_packed": torch.empty((m.T, b, m.Hq, m.W), dtype=torch.int32, device=self.device),
+                "attn": torch.empty((m.T, b, m.Hq, m.D), dtype=m.dtype, device=self.device),
+            }
+        meta = self.meta if b == self.B else self._meta(b)
+        hidden = m.forward_paged(self.input_ids[:b], self.positions[:b], self.cache.layers, meta,
+                                 self._bufs[b])
+        logits = self.logits[:b]
+        m.compute_logits(hidden, out=logits)
+        s.uniforms[:b].uniform_()
+        sample_tokens(logits, s.temperature[:b], s.top_k[:b], s.top_p[:b], s.min_p[:b],
+                      s.repetition_penalty[:b], s.presence_penalty[:b], s.frequency_penalty[:b],
+                      self.history, self.step_count, s.uniforms[:b], s.tokens[:b])
         decode_advance(s.tokens, self.input_ids, self.positions, self.seq_lens, self.slot_mapping,
-                       self.block_tables, self.bs, self.B, self.live, self.history, self.step_count)
+                       self.block_tables, self.bs, b, self.live, self.history, self.step_count)
 
     # -- prefill -------------------------------------------------------------
     @torch.no_grad()
@@ -104,6 +132,7 @@ class DecodeRunner:
         logits = self.model.compute_logits(hidden, last)
 
         self.live.fill_(n)
+        self.n_live = n
         self.sampler.set_params(params)
         self.block_tables.fill_(self.cache.pad_block)
         self.block_tables[:n] = torch.tensor(tables, dtype=torch.int32, device=dev)
@@ -124,9 +153,15 @@ class DecodeRunner:
 
     # -- capture and replay --------------------------------------------------------
     @torch.no_grad()
-    def capture(self) -> None:
-        """Captures one decode step.  Warm-up runs on the pad block only (the
-        live rows are parked and restored), so capture changes no sequence."""
+    def capture(self, buckets: tuple[int, ...] | None = None) -> list[int]:
+        """Captures one decode step per bucket (default: all of them), largest
+        first into one shared memory pool.  Warm-up runs on the pad block only
+        (the live rows are parked and restored), so capture changes no
+        sequence.  Returns the buckets captured."""
+        todo = sorted(self.buckets if buckets is None else buckets, reverse=True)
+        for b in todo:
+            if b not in self.buckets:
+                raise ValueError(f"{b} is not one of the buckets {self.buckets}")
         parked = (self.input_ids, self.positions, self.seq_lens, self.slot_mapping,
                   self.step_count, self.history, self.live, self.sampler.tokens)
         saved = [t.clone() for t in parked]
@@ -139,20 +174,34 @@ class DecodeRunner:
         stream = torch.cuda.Stream(self.device)
         stream.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(stream):
-            for _ in range(2):
-                self._step()
+            for b in todo:
+                for _ in range(2):
+                    self._step(b)
         torch.cuda.current_stream(self.device).wait_stream(stream)
         torch.cuda.synchronize(self.device)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self._step()
+        pool = None
+        for b in todo:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=pool):
+                self._step(b)
+            pool = g.pool()
+            self.graphs[b] = g
         self.block_tables.copy_(bt)
         for t, v in zip(parked, saved):
             t.copy_(v)
+        return todo
+
+    @property
+    def graph(self) -> torch.cuda.CUDAGraph | None:
+        """The graph the live batch replays (None before its bucket is captured)."""
+        return self.graphs.get(self.bucket_for(max(self.n_live, 1)))
 
     def replay(self, steps: int = 1) -> None:
+        g = self.graph
+        if g is None:
+            raise RuntimeError(f"no graph captured for a batch of {self.n_live}")
         for _ in range(steps):
-            self.graph.replay()
+            g.replay()
 
     @torch.no_grad()
     def generate(self, prompts: list[list[int]], params: list[SamplingParams],
@@ -160,6 +209,6 @@ class DecodeRunner:
         """``[n, max_new_tokens]`` generated token ids (first from prefill)."""
         self.start(prompts, params, shuffle_blocks)
         if self.graph is None:
-            self.capture()
+            self.capture((self.bucket_for(len(prompts)),))
         self.replay(max_new_tokens - 1)
         return self.history[: len(prompts), :max_new_tokens].clone()

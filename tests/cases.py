@@ -16,12 +16,16 @@ def random_bits(rng, shape, density):
 
 
 def attn_case(seq_lens, block_size=16, T=4, q_heads=14, kv_heads=2, head_dim=64,
-              density=0.4, q_density=0.4, seed=0, extra_blocks=3):
-    """Packed q/k/v, a scrambled block table padded with the pad block, lens."""
+              density=0.4, q_density=0.4, seed=0, extra_blocks=3, compact=False):
+    """Packed q/k/v, a scrambled block table padded with the pad block, lens.
+
+    ``compact`` sizes the cache to the blocks the sequences use (many short
+    sequences beside one long one) instead of n * max_blocks."""
     rng = np.random.default_rng(seed)
     n = len(seq_lens)
     max_blocks = max(1, max((s + block_size - 1) // block_size for s in seq_lens))
-    num_blocks = n * max_blocks + extra_blocks
+    used = sum((s + block_size - 1) // block_size for s in seq_lens)
+    num_blocks = (used if compact else n * max_blocks) + extra_blocks
     slots = num_blocks * block_size
     k = orc.pack(random_bits(rng, (T, kv_heads, slots, head_dim), density))
     v = orc.pack(random_bits(rng, (T, kv_heads, slots, head_dim), density))

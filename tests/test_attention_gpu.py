@@ -117,6 +117,20 @@ def test_long_context_split_partitions(lens, gpu):
     _check(_run(case, gpu), oracle_attn(case), f"long lens={lens}")
 
 
+@pytest.mark.parametrize("n", [300, 4100])
+def test_long_context_launch_order_over_ragged_batches(n, gpu):
+    """Long contexts are launched longest first: ordered inside the main
+    kernel up to 4096 (sequence, partition) items, by a separate planner
+    beyond.  Ragged batches with empty sequences must cover every item once."""
+    rng = np.random.default_rng(n)
+    lens = rng.integers(0, 200, n)
+    lens[rng.choice(n, 20, replace=False)] = 0
+    lens[rng.choice(n, 3, replace=False)] = [8200, 12000, 8193]
+    case = attn_case(lens.tolist(), block_size=16, T=1, density=0.2, q_density=0.2, seed=n,
+                     compact=True)
+    _check(_run(case, gpu), oracle_attn(case), f"ragged n={n}")
+
+
 def test_bf16_output_within_bf16_rounding(gpu):
     case = attn_case([1, 5, 40, 97, 300], block_size=16, seed=13)
     got = _run(case, gpu, dtype=torch.bfloat16)

@@ -49,9 +49,9 @@ def test_host_side_validation_without_a_gpu():
     rc = lib.spk_decode_attn(None, s4, None, s4, None, s4, 0, None, 0, 0, None, None, 0, s4,
                              4, 1, 14, 2, 64, 16, 8, 5.0, None, 0, None)
     assert rc == _lib.SPK_EINVAL and b"scale" in lib.spk_last_error()
-    # long contexts need a workspace; a missing one is rejected, not faulted
+    # split contexts need a workspace; a missing one is rejected, not faulted
     rc = lib.spk_decode_attn(None, s4, None, s4, None, s4, 0, None, 0, 0, None, None, 0, s4,
-                             4, 256, 14, 2, 64, 16, 2048, 0.125, None, 0, None)
+                             4, 8, 14, 2, 64, 16, 2048, 0.125, None, 0, None)
     assert rc == _lib.SPK_EINVAL and b"workspace" in lib.spk_last_error()
     assert lib.spk_lif_multistep(None, 2, _i64(0, 0, 1), None, None, 0, None, None, 0, None,
                                  0, 4, 4, None) == _lib.SPK_EINVAL
@@ -64,13 +64,17 @@ def test_workspace_sizing():
     lib = _lib.load()
     # config 3 shape: one partition, no workspace
     assert lib.spk_decode_attn_workspace_bytes(4, 64, 14, 2, 64, 16, 12) == 0
-    # config 4 shape: whole-sequence partitions, longest-first launch order
+    # config 4 shape: whole-sequence partitions, ordered longest first inside
+    # the kernel, no workspace
+    assert lib.spk_decode_attn_workspace_bytes(4, 256, 14, 2, 64, 16, 2048) == 0
+    # past 4096 (sequence, partition) items a planner writes the launch order
     # (one int per work item + the item count)
-    ws = lib.spk_decode_attn_workspace_bytes(4, 256, 14, 2, 64, 16, 2048)
-    assert ws == (256 * 4 * 2 + 1) * 4
-    # a small batch of long contexts splits them: partial sums + order
+    ws = lib.spk_decode_attn_workspace_bytes(1, 4100, 14, 2, 64, 16, 750)
+    assert ws == (4100 * 1 * 2 + 1) * 4
+    # a small batch of long contexts splits them: partial sums, no order
     ws = lib.spk_decode_attn_workspace_bytes(4, 8, 14, 2, 64, 16, 2048)
-    assert ws > 8 * 4 * 14 * 65 * 4
+    nparts = ws // (4 * 8 * 14 * 65 * 4)
+    assert nparts > 1 and ws == nparts * 4 * 8 * 14 * 65 * 4
 
 
 def test_python_api_refuses_cpu_tensors():

@@ -245,6 +245,36 @@ def test_runner_graph_greedy_matches_eager_steps(gpu):
     assert runner.positions[:n].tolist() == [plen + new - 1] * n
 
 
+def test_runner_buckets_match_eager_batches(gpu):
+    """One runner captures every bucket up to 8 into one pool; a batch of 3
+    replays the bucket-4 graph and a batch of 6 the bucket-8 graph, each giving
+    the tokens of eager steps over a batch of that bucket's size."""
+    m = _small_model(gpu, seed=13)
+    bs, plen, new = 16, 9, 7
+    g = torch.Generator().manual_seed(17)
+    prompts = [torch.randint(0, 1024, (plen,), generator=g).tolist() for _ in range(6)]
+    runner = DecodeRunner(m, PagedSpikeCache(2, m.T, m.Hkv, m.D, 64, bs, device=gpu), batch_size=8,
+                          max_model_len=plen + new + 1, max_new_tokens=16)
+    assert runner.buckets == (1, 2, 4, 8)
+    assert runner.bucket_for(3) == 4 and runner.bucket_for(8) == 8
+    with pytest.raises(ValueError):
+        runner.bucket_for(9)
+    assert runner.capture() == [8, 4, 2, 1]
+    for n, bucket in ((3, 4), (6, 8), (1, 1)):
+        params = [SamplingParams(temperature=0.0) for _ in range(n)]
+        toks = runner.generate(prompts[:n], params, new, shuffle_blocks=n)
+        assert runner.graph is runner.graphs[bucket]
+        eager = DecodeRunner(m, PagedSpikeCache(2, m.T, m.Hkv, m.D, 64, bs, device=gpu),
+                             batch_size=bucket, max_model_len=plen + new + 1, max_new_tokens=16)
+        eager.start(prompts[:n], params, shuffle_blocks=n)
+        for _ in range(new - 1):
+            eager._step()
+        torch.cuda.synchronize()
+        assert torch.equal(toks, eager.history[:n, :new]), f"batch {n} in bucket {bucket}"
+        # Rows past the live batch stay parked on the pad block.
+        assert (runner.seq_lens[n:] == 1).all() and (runner.slot_mapping[n:] == runner.cache.pad_slot).all()
+
+
 def test_runner_sampling_in_graph_stays_in_top_k(gpu):
     """Sampling inside the graph: every token is one of the row's top-k of the
     eager logits at that step (checked on the first decode step)."""
