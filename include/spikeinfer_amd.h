@@ -184,6 +184,19 @@ int spk_add_rmsnorm(void *h, const void *delta, const void *weight, void *out,
                     int dtype, int64_t rows, int hidden, float eps, void *stream);
 
 /*
+ * Embedding lookup + the first layer's RMSNorm, broadcast over T: for token
+ * i, e = embed[clamp(ids[i], 0, vocab - 1)] (a row of `hidden`); for every
+ * t < T, h[t, i] = e and out[t, i] = round(weight * round(e * rsqrt(mean(e^2)
+ * + eps))).  h and out are [T, n, hidden] contiguous.  Replaces
+ * `embed_tokens(ids)` broadcast to T steps and the first input_layernorm
+ * (spikeinfer/modeling_fast.py:300, :311, :206).  Out-of-range ids read the
+ * nearest row (torch raises instead).
+ */
+int spk_embed_rmsnorm(const int64_t *ids, const void *embed, int64_t vocab, const void *weight,
+                      void *h, void *out, int dtype, int T, int64_t n, int hidden, float eps,
+                      void *stream);
+
+/*
  * Final residual add, RMSNorm and rate-coded readout: h [T, rows, hidden]
  * contiguous (plus delta of the same shape when not NULL, rounded to dtype; h
  * is only read) -> out [rows, hidden] = round(sum_t RMSNorm(h_t) * (1/T)),
@@ -202,7 +215,10 @@ int spk_rmsnorm_mean_t(const void *h, const void *delta, const void *weight, voi
  *   x        x_dtype (BF16/F16) [T, n_tok, (Hq + 2*Hkv) * D], channel stride 1,
  *            strides {t, token} in elements: q heads, then k, then v heads
  *            (the concatenated q/k/v projection output)
- *   cos, sin x_dtype [n_tok, D] contiguous (rotary tables of each token)
+ *   cos, sin x_dtype [n_tok, D] contiguous (rotary tables of each token), or,
+ *            when positions != NULL, [table_rows, D] tables whose row
+ *            positions[i] serves token i (out-of-range positions read the
+ *            nearest row)
  *   beta, threshold  param_dtype [3, D] contiguous: q, k and v sites
  *   q_packed int32 [T, n_q, Hq, W] at q_strides: tokens [0, n_q) (the decode
  *            prefix) are packed here
@@ -214,7 +230,8 @@ int spk_rmsnorm_mean_t(const void *h, const void *delta, const void *weight, voi
  * round(rotate_half(x)*sin)).  D is a power of two in [64, 512].
  */
 int spk_qkv_rope_lif_pack(const void *x, int x_dtype, const int64_t x_strides[2],
-                          const void *cos, const void *sin, const void *beta,
+                          const void *cos, const void *sin, const int64_t *positions,
+                          int64_t table_rows, const void *beta,
                           const void *threshold, int param_dtype, int32_t *q_packed,
                           const int64_t q_strides[3], int64_t n_q, int32_t *k_cache,
                           int32_t *v_cache, const int64_t cache_strides[3],

@@ -54,8 +54,9 @@ _SIGNATURES = {
     "spk_unpack": (_i32, [_vp, _i64, _i32, _vp, _i32, _vp]),
     "spk_add_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _f32, _vp]),
     "spk_rmsnorm_mean_t": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i64, _i32, _f32, _vp]),
+    "spk_embed_rmsnorm": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i64, _i32, _f32, _vp]),
     "spk_qkv_rope_lif_pack": (_i32, [
-        _vp, _i32, _i64p, _vp, _vp, _vp, _vp, _i32, _vp, _i64p, _i64, _vp, _vp, _i64p, _vp,
+        _vp, _i32, _i64p, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _i64p, _i64, _vp, _vp, _i64p, _vp,
         _i64, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _vp]),
     "spk_lif_gate_mul": (_i32, [_vp, _i32, _i64p, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _vp]),
     "spk_decode_advance": (_i32, [

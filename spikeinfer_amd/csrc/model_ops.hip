@@ -61,8 +61,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(typename Elem<DT>::T *
     }
     return ss;
   };
-  auto norm = [&](const Vec &x, int v, float r) {
-    const Vec w = wr[v];
+  auto norm = [&](const Vec &x, const Vec &w, int v, float r) {
     Vec y;
 #pragma unroll
     for (int i = 0; i < V; ++i) {
@@ -73,8 +72,14 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(typename Elem<DT>::T *
   };
   float ss = 0.f;
   if (nv <= 64 * kNormRegVecs) {
-    // The row stays in registers between the two halves.
-    Vec xs[kNormRegVecs];
+    // The row stays in registers between the two halves; the weights are
+    // loaded with it, ahead of the reduction.
+    Vec xs[kNormRegVecs], ws[kNormRegVecs];
+#pragma unroll
+    for (int k = 0; k < kNormRegVecs; ++k) {
+      const int v = lane + 64 * k;
+      if (v < nv) ws[k] = wr[v];
+    }
 #pragma unroll
     for (int k = 0; k < kNormRegVecs; ++k) {
       const int v = lane + 64 * k;
@@ -89,7 +94,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(typename Elem<DT>::T *
 #pragma unroll
     for (int k = 0; k < kNormRegVecs; ++k) {
       const int v = lane + 64 * k;
-      if (v < nv) norm(xs[k], v, r);
+      if (v < nv) norm(xs[k], ws[k], v, r);
     }
     return;
   }
@@ -97,7 +102,84 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(typename Elem<DT>::T *
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
   const float r = rsqrtf(ss * (1.f / static_cast<float>(hidden)) + eps);
-  for (int v = lane; v < nv; v += 64) norm(hr[v], v, r);
+  for (int v = lane; v < nv; v += 64) norm(hr[v], wr[v], v, r);
+}
+
+// ---- embedding + first RMSNorm ------------------------------------------------
+// One wave per token: e = embed[clamp(ids[i], 0, vocab - 1)], then for every
+// timestep t: h[t, i] = e and out[t, i] = round(weight * round(e * r)) with
+// r = rsqrt(mean(e^2) + eps) (the input is the same at every timestep, so the
+// norm is computed once).
+template <int DT>
+__global__ __launch_bounds__(256) void embed_rmsnorm_kernel(const int64_t *ids,
+                                                            const typename Elem<DT>::T *embed,
+                                                            int64_t vocab,
+                                                            const typename Elem<DT>::T *weight,
+                                                            typename Elem<DT>::T *h,
+                                                            typename Elem<DT>::T *out, int T,
+                                                            int64_t n, int hidden, float eps) {
+  typedef typename Elem<DT>::T E;
+  constexpr int V = Elem<DT>::kVec;
+  typedef E Vec __attribute__((ext_vector_type(V)));
+  const int lane = threadIdx.x & 63;
+  const int64_t tok = blockIdx.x * (int64_t)(blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (tok >= n) return;
+  int64_t id = ids[tok];
+  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+  const Vec *er = reinterpret_cast<const Vec *>(embed + id * hidden);
+  const Vec *wr = reinterpret_cast<const Vec *>(weight);
+  const int nv = hidden / V;
+  const int64_t tstep = n * hidden / V;  // Vecs per timestep
+  Vec *hr = reinterpret_cast<Vec *>(h + tok * hidden);
+  Vec *orow = reinterpret_cast<Vec *>(out + tok * hidden);
+  auto emit = [&](const Vec &e, const Vec &w, int v, float r) {
+    Vec y;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float nrm = round_to<DT>(elem_to_f32<DT>(e[i]) * r);
+      y[i] = f32_to_elem<DT>(elem_to_f32<DT>(w[i]) * nrm);
+    }
+    for (int t = 0; t < T; ++t) {
+      hr[t * tstep + v] = e;
+      orow[t * tstep + v] = y;
+    }
+  };
+  auto sumsq = [&](const Vec &x) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float f = elem_to_f32<DT>(x[i]);
+      ss += f * f;
+    }
+    return ss;
+  };
+  float ss = 0.f;
+  if (nv <= 64 * kNormRegVecs) {
+    Vec es[kNormRegVecs], ws[kNormRegVecs];
+#pragma unroll
+    for (int k = 0; k < kNormRegVecs; ++k) {
+      const int v = lane + 64 * k;
+      if (v < nv) {
+        es[k] = er[v];
+        ws[k] = wr[v];
+        ss += sumsq(es[k]);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    const float r = rsqrtf(ss * (1.f / static_cast<float>(hidden)) + eps);
+#pragma unroll
+    for (int k = 0; k < kNormRegVecs; ++k) {
+      const int v = lane + 64 * k;
+      if (v < nv) emit(es[k], ws[k], v, r);
+    }
+    return;
+  }
+  for (int v = lane; v < nv; v += 64) ss += sumsq(er[v]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  const float r = rsqrtf(ss * (1.f / static_cast<float>(hidden)) + eps);
+  for (int v = lane; v < nv; v += 64) emit(er[v], wr[v], v, r);
 }
 
 // ---- final RMSNorm + mean over the T timesteps --------------------------------
@@ -172,7 +254,9 @@ __global__ __launch_bounds__(256) void rmsnorm_mean_t_kernel(const typename Elem
 struct QkvParams {
   const void *x;           // [T, n_tok, (Hq + 2 Hkv) * D], channel stride 1
   int64_t xs0, xs1;
-  const void *cos, *sin;   // [n_tok, D] contiguous
+  const void *cos, *sin;   // [n_tok, D], or [table_rows, D] indexed by pos[token]
+  const int64_t *pos;      // nullptr: row = token
+  int64_t table_rows;
   const void *beta, *th;   // [3, D] contiguous: q, k, v sites
   int param_dtype;
   uint64_t *q_packed;      // [T, n_q, Hq, W] (strides in int32 words)
@@ -187,42 +271,61 @@ struct QkvParams {
   int Hq, Hkv, D;
 };
 
-// D/8 lanes per (token, head) row, 8 channels (16 bytes) per lane.  The
-// rotate-half partner of channel c < D/2 is c + D/2, held by lane sub ^ (D/16)
-// of the same row; rows never straddle a wave (64 % (D/8) == 0).
+// R = min(D/2, 64) lanes per (token, head) row; lane `sub` owns the channel
+// pairs (c, c + D/2) for c = sub + R*j, j < D/(2R), so the rotate-half
+// partner of each channel is in the same lane.  Rows never straddle a wave
+// (64 % R == 0), and the packed words come from wave ballots: bit `lane` of
+// ballot(spike of c) is channel c of the lane's row.
 template <int DT>
 __global__ __launch_bounds__(256) void qkv_rope_lif_pack_kernel(QkvParams p) {
   typedef typename Elem<DT>::T E;
-  typedef E Vec __attribute__((ext_vector_type(8)));
-  const int L = p.D >> 3;
+  constexpr int kMaxPairs = 4;                 // D <= 512
+  const int half = p.D >> 1;
+  const int R = half < 64 ? half : 64;
+  const int P = half / R;
   const int Htot = p.Hq + 2 * p.Hkv;
   const int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t row = g / L;
-  const int sub = static_cast<int>(g - row * L);
+  const int64_t row = g / R;
+  const int sub = static_cast<int>(g - row * R);
+  const int lane = threadIdx.x & 63;
   const bool active = row < p.n_tok * Htot;
   const int64_t tok = active ? row / Htot : 0;
   const int hh = active ? static_cast<int>(row - tok * Htot) : 0;
   const int site = hh < p.Hq ? 0 : (hh < p.Hq + p.Hkv ? 1 : 2);
   const int h = site == 0 ? hh : (site == 1 ? hh - p.Hq : hh - p.Hq - p.Hkv);
-  const int cl = sub * 8;                      // channel within the head
-  const int half = L >> 1;
-  const bool low = sub < half;                 // channels below D/2
   const bool rope = site != 2;
 
-  float beta[8], th[8], u[8], cs[8], sn[8];
-  const Vec cv = active ? reinterpret_cast<const Vec *>(static_cast<const E *>(p.cos) + tok * p.D)[sub] : Vec{};
-  const Vec sv = active ? reinterpret_cast<const Vec *>(static_cast<const E *>(p.sin) + tok * p.D)[sub] : Vec{};
-  load_params(p.beta, p.param_dtype, site * p.D + cl, beta);
-  load_params(p.th, p.param_dtype, site * p.D + cl, th);
+  float blo[kMaxPairs], bhi[kMaxPairs], tlo[kMaxPairs], thi[kMaxPairs];
+  float clo[kMaxPairs], chi[kMaxPairs], slo[kMaxPairs], shi[kMaxPairs];
+  float ulo[kMaxPairs], uhi[kMaxPairs];
+  int64_t crow = tok;
+  if (p.pos && active) {  // positions outside the table read its nearest row
+    const int64_t q = p.pos[tok];
+    crow = q < 0 ? 0 : (q >= p.table_rows ? p.table_rows - 1 : q);
+  }
+  const E *cosr = static_cast<const E *>(p.cos) + crow * p.D;
+  const E *sinr = static_cast<const E *>(p.sin) + crow * p.D;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    beta[i] = clamp01(beta[i]);
-    u[i] = 0.f;
-    cs[i] = elem_to_f32<DT>(cv[i]);
-    sn[i] = elem_to_f32<DT>(sv[i]);
+  for (int j = 0; j < kMaxPairs; ++j) {
+    if (j >= P) break;
+    const int c = sub + R * j;
+    float b1[1], t1[1];
+    load_params(p.beta, p.param_dtype, site * p.D + c, b1);
+    blo[j] = clamp01(b1[0]);
+    load_params(p.th, p.param_dtype, site * p.D + c, t1);
+    tlo[j] = t1[0];
+    load_params(p.beta, p.param_dtype, site * p.D + c + half, b1);
+    bhi[j] = clamp01(b1[0]);
+    load_params(p.th, p.param_dtype, site * p.D + c + half, t1);
+    thi[j] = t1[0];
+    clo[j] = active ? elem_to_f32<DT>(cosr[c]) : 0.f;
+    chi[j] = active ? elem_to_f32<DT>(cosr[c + half]) : 0.f;
+    slo[j] = active ? elem_to_f32<DT>(sinr[c]) : 0.f;
+    shi[j] = active ? elem_to_f32<DT>(sinr[c + half]) : 0.f;
+    ulo[j] = uhi[j] = 0.f;
   }
 
-  // Destination of this row's packed words.
+  // Destination of this row's packed words (D/64 per timestep).
   uint64_t *dst = nullptr;
   int64_t dstep = 0;  // per timestep, in uint64 words
   if (active) {
@@ -241,56 +344,51 @@ __global__ __launch_bounds__(256) void qkv_rope_lif_pack_kernel(QkvParams p) {
   }
   E *dense = active ? static_cast<E *>(p.dense[site]) : nullptr;
   const int Hs = site == 0 ? p.Hq : p.Hkv;
-  const int64_t dense_row = (static_cast<int64_t>(h) * p.n_tok + tok) * p.D + cl;
+  const int64_t dense_row = (static_cast<int64_t>(h) * p.n_tok + tok) * p.D;
   const int64_t dense_tstep = static_cast<int64_t>(Hs) * p.n_tok * p.D;
+  const int rshift = R == 32 ? 32 * ((lane >> 5) & 1) : 0;  // this row's bits of a ballot
 
-  const E *xrow = static_cast<const E *>(p.x) + tok * p.xs1 + hh * p.D + cl;
+  const E *xrow = static_cast<const E *>(p.x) + tok * p.xs1 + hh * p.D;
   for (int t0 = 0; t0 < p.T; t0 += kTBatchQkv) {
-    Vec xv[kTBatchQkv];
+    E xl[kTBatchQkv][kMaxPairs], xh[kTBatchQkv][kMaxPairs];
 #pragma unroll
     for (int k = 0; k < kTBatchQkv; ++k)
-      xv[k] = (active && t0 + k < p.T)
-                  ? __builtin_nontemporal_load(reinterpret_cast<const Vec *>(xrow + (t0 + k) * p.xs0))
-                  : Vec{};
+#pragma unroll
+      for (int j = 0; j < kMaxPairs; ++j) {
+        const bool ld = active && t0 + k < p.T && j < P;
+        xl[k][j] = ld ? xrow[(t0 + k) * p.xs0 + sub + R * j] : E{};
+        xh[k][j] = ld ? xrow[(t0 + k) * p.xs0 + sub + R * j + half] : E{};
+      }
 #pragma unroll
     for (int k = 0; k < kTBatchQkv; ++k) {
       if (t0 + k >= p.T) break;
       const int t = t0 + k;
-      const Vec x = xv[k];
-      // Partner half of the head (all lanes take part in the exchange).
-      Vec xp;
-      {
-        typedef uint32_t U4 __attribute__((ext_vector_type(4)));
-        U4 w = __builtin_bit_cast(U4, x);
-        U4 r;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) r[j] = __shfl_xor(w[j], half);
-        xp = __builtin_bit_cast(Vec, r);
-      }
-      uint32_t byte = 0;
-      Vec spk;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float cur = elem_to_f32<DT>(x[i]);
+      for (int j = 0; j < kMaxPairs; ++j) {
+        if (j >= P) break;
+        float lo = elem_to_f32<DT>(xl[k][j]), hi = elem_to_f32<DT>(xh[k][j]);
         if (rope) {
-          const float xr = low ? -elem_to_f32<DT>(xp[i]) : elem_to_f32<DT>(xp[i]);
-          cur = round_to<DT>(round_to<DT>(cur * cs[i]) + round_to<DT>(xr * sn[i]));
+          const float rl = round_to<DT>(round_to<DT>(lo * clo[j]) + round_to<DT>(-hi * slo[j]));
+          const float rh = round_to<DT>(round_to<DT>(hi * chi[j]) + round_to<DT>(lo * shi[j]));
+          lo = rl;
+          hi = rh;
         }
-        const bool s = lif_step(u[i], cur, beta[i], th[i]);
-        byte |= s ? (1u << i) : 0u;
-        spk[i] = spike_elem<DT>(s);
+        const bool sl = lif_step(ulo[j], lo, blo[j], tlo[j]);
+        const bool sh = lif_step(uhi[j], hi, bhi[j], thi[j]);
+        const uint64_t ml = __ballot(sl), mh = __ballot(sh);
+        if (dst && sub == 0) {
+          if (R == 32) {
+            dst[t * dstep] = ((ml >> rshift) & 0xffffffffull) | (((mh >> rshift) & 0xffffffffull) << 32);
+          } else {
+            dst[t * dstep + j] = ml;
+            dst[t * dstep + P + j] = mh;
+          }
+        }
+        if (dense) {
+          dense[t * dense_tstep + dense_row + sub + R * j] = spike_elem<DT>(sl);
+          dense[t * dense_tstep + dense_row + sub + R * j + half] = spike_elem<DT>(sh);
+        }
       }
-      // OR the 8 spike bytes of each aligned 8-lane group into a 64-bit word.
-      const int s8 = sub & 7;
-      uint32_t lo = s8 < 4 ? byte << (8 * s8) : 0u;
-      uint32_t hi = s8 < 4 ? 0u : byte << (8 * (s8 - 4));
-#pragma unroll
-      for (int off = 1; off < 8; off <<= 1) {
-        lo |= __shfl_xor(lo, off);
-        hi |= __shfl_xor(hi, off);
-      }
-      if (dst && s8 == 0) dst[t * dstep + (sub >> 3)] = (static_cast<uint64_t>(hi) << 32) | lo;
-      if (dense) *reinterpret_cast<Vec *>(dense + t * dense_tstep + dense_row) = spk;
     }
   }
 }
@@ -409,6 +507,34 @@ extern "C" int spk_add_rmsnorm(void *h, const void *delta, const void *weight, v
   return check_launch("add_rmsnorm");
 }
 
+extern "C" int spk_embed_rmsnorm(const int64_t *ids, const void *embed, int64_t vocab,
+                                 const void *weight, void *h, void *out, int dtype, int T,
+                                 int64_t n, int hidden, float eps, void *stream) {
+  if (!valid_float_dtype(dtype)) return fail(SPK_EINVAL, "embed_rmsnorm: dtype %d", dtype);
+  if (T < 1 || n < 0 || vocab < 1 || hidden <= 0 || hidden % vec_of(dtype))
+    return fail(SPK_EINVAL, "embed_rmsnorm: bad shape T=%d n=%lld vocab=%lld hidden=%d", T,
+                (long long)n, (long long)vocab, hidden);
+  if (n > 0 && (!ids || !embed || !weight || !h || !out))
+    return fail(SPK_EINVAL, "embed_rmsnorm: null pointer");
+  if (!aligned16(embed) || !aligned16(weight) || !aligned16(h) || !aligned16(out))
+    return fail(SPK_EINVAL, "embed_rmsnorm: buffers must be 16-byte aligned");
+  if (n == 0) return SPK_OK;
+  const dim3 grid(static_cast<unsigned>((n + 3) / 4));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+#define SPK_CASE(DT)                                                                          \
+  case DT:                                                                                    \
+    embed_rmsnorm_kernel<DT><<<grid, 256, 0, s>>>(                                            \
+        ids, static_cast<const Elem<DT>::T *>(embed), vocab,                                  \
+        static_cast<const Elem<DT>::T *>(weight), static_cast<Elem<DT>::T *>(h),              \
+        static_cast<Elem<DT>::T *>(out), T, n, hidden, eps);                                  \
+    break;
+    SPK_CASE(SPK_F32) SPK_CASE(SPK_F16) SPK_CASE(SPK_BF16)
+#undef SPK_CASE
+  }
+  return check_launch("embed_rmsnorm");
+}
+
 extern "C" int spk_rmsnorm_mean_t(const void *h, const void *delta, const void *weight, void *out,
                                   int dtype, int T, int64_t rows, int hidden, float eps,
                                   void *stream) {
@@ -439,6 +565,7 @@ extern "C" int spk_rmsnorm_mean_t(const void *h, const void *delta, const void *
 
 extern "C" int spk_qkv_rope_lif_pack(
     const void *x, int x_dtype, const int64_t x_strides[2], const void *cos, const void *sin,
+    const int64_t *positions, int64_t table_rows,
     const void *beta, const void *threshold, int param_dtype, int32_t *q_packed,
     const int64_t q_strides[3], int64_t n_q, int32_t *k_cache, int32_t *v_cache,
     const int64_t cache_strides[3], const int64_t *slot_mapping, int64_t num_slots,
@@ -468,6 +595,8 @@ extern "C" int spk_qkv_rope_lif_pack(
   void *dense[3] = {dense_q, dense_k, dense_v};
   for (void *d : dense)
     if (d && !aligned16(d)) return fail(SPK_EINVAL, "qkv_rope_lif_pack: dense outputs must be 16-byte aligned");
+  if (positions && table_rows < 1)
+    return fail(SPK_EINVAL, "qkv_rope_lif_pack: positions need a table of at least one row");
   if (n_tok == 0) return SPK_OK;
   QkvParams p;
   p.x = x;
@@ -475,6 +604,8 @@ extern "C" int spk_qkv_rope_lif_pack(
   p.xs1 = x_strides[1];
   p.cos = cos;
   p.sin = sin;
+  p.pos = positions;
+  p.table_rows = table_rows;
   p.beta = beta;
   p.th = threshold;
   p.param_dtype = param_dtype;
@@ -496,7 +627,7 @@ extern "C" int spk_qkv_rope_lif_pack(
   p.Hq = Hq;
   p.Hkv = Hkv;
   p.D = D;
-  const int64_t threads = n_tok * (Hq + 2 * Hkv) * (D / 8);
+  const int64_t threads = n_tok * (Hq + 2 * Hkv) * (D / 2 < 64 ? D / 2 : 64);
   const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (x_dtype == SPK_BF16)

@@ -50,6 +50,39 @@ def add_rmsnorm(h: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tenso
     return out
 
 
+def embed_rmsnorm(ids: torch.Tensor, embed: torch.Tensor, weight: torch.Tensor, eps: float,
+                  T: int, h: torch.Tensor | None = None,
+                  out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Embedding rows of ``ids`` broadcast over ``T`` steps, and their RMSNorm.
+
+    Returns ``(h, x)``, both ``[T, n, hidden]``: ``h[t] = embed[ids]`` and
+    ``x[t] = Qwen2RMSNorm(h[t])``.
+    """
+    dev = _lib.require_gpu(ids, embed, weight, h, out)
+    if ids.dtype != torch.int64 or ids.ndim != 1 or not ids.is_contiguous():
+        raise ValueError("embed_rmsnorm: ids must be a contiguous int64 vector")
+    if embed.ndim != 2 or not embed.is_contiguous() or embed.dtype not in _VEC_DTYPES:
+        raise ValueError("embed_rmsnorm: embed must be a contiguous [vocab, hidden] float matrix")
+    vocab, hidden = embed.shape
+    if weight.numel() != hidden or weight.dtype != embed.dtype or not weight.is_contiguous():
+        raise ValueError(f"embed_rmsnorm: weight must be {hidden} contiguous {embed.dtype} entries")
+    n = ids.numel()
+    shape = (T, n, hidden)
+    h = torch.empty(shape, dtype=embed.dtype, device=dev) if h is None else h
+    out = torch.empty(shape, dtype=embed.dtype, device=dev) if out is None else out
+    for name, t in (("h", h), ("out", out)):
+        if tuple(t.shape) != shape or t.dtype != embed.dtype or not t.is_contiguous():
+            raise ValueError(f"embed_rmsnorm: {name} must be contiguous {shape} {embed.dtype}")
+    _lib.check(
+        _lib.load().spk_embed_rmsnorm(
+            ids.data_ptr(), embed.data_ptr(), vocab, weight.data_ptr(), h.data_ptr(), out.data_ptr(),
+            _lib.dtype_code(embed.dtype), T, n, hidden, float(eps), _lib.stream_of(dev),
+        ),
+        "embed_rmsnorm",
+    )
+    return h, out
+
+
 def rmsnorm_mean_t(h: torch.Tensor, weight: torch.Tensor, eps: float,
                    out: torch.Tensor | None = None, delta: torch.Tensor | None = None) -> torch.Tensor:
     """``RMSNorm(h + delta).mean(dim=0)`` for ``h [T, rows, hidden]``
@@ -90,13 +123,16 @@ def qkv_rope_lif_pack(
     q_packed: torch.Tensor | None = None,
     n_q: int = 0,
     dense: tuple[torch.Tensor | None, torch.Tensor | None, torch.Tensor | None] | None = None,
+    positions: torch.Tensor | None = None,
 ) -> torch.Tensor | None:
     """RoPE -> LIF -> pack for the q/k/v site of one layer.
 
     Args:
         qkv: ``[T, n_tok, (Hq + 2 Hkv) * D]`` concatenated projection output
             (channel stride 1).
-        cos, sin: ``[n_tok, D]`` rotary tables in qkv's dtype.
+        cos, sin: ``[n_tok, D]`` rotary tables in qkv's dtype, or, with
+            ``positions`` (int64 ``[n_tok]``), ``[rows, D]`` tables indexed by
+            each token's position.
         beta, threshold: ``[3, D]`` (q, k, v sites).
         k_cache, v_cache: the layer's ``int32 [T, Hkv, slots, W]`` caches;
             token ``i`` is written at ``slot_mapping[i]``.
@@ -104,15 +140,22 @@ def qkv_rope_lif_pack(
         dense: optional ``[T, H, n_tok, D]`` outputs of the 0/1 spikes per site.
     Returns ``q_packed``.
     """
-    dev = _lib.require_gpu(qkv, cos, sin, beta, threshold, k_cache, v_cache, slot_mapping, q_packed)
+    dev = _lib.require_gpu(qkv, cos, sin, beta, threshold, k_cache, v_cache, slot_mapping, q_packed,
+                           positions)
     if qkv.ndim != 3 or qkv.stride(-1) != 1:
         raise ValueError("qkv must be [T, n_tok, C] with a contiguous channel axis")
     T, n_tok, C = qkv.shape
     if C != (num_q_heads + 2 * num_kv_heads) * head_dim:
         raise ValueError(f"qkv has {C} channels, expected {(num_q_heads + 2 * num_kv_heads) * head_dim}")
+    rows = cos.shape[0] if positions is not None else n_tok
+    if positions is not None:
+        if positions.dtype != torch.int64 or not positions.is_contiguous() or positions.numel() < n_tok:
+            raise ValueError(f"positions must be a contiguous int64 vector of >= {n_tok} entries")
+        if rows < 1:
+            raise ValueError("rotary tables need at least one row")
     for name, t in (("cos", cos), ("sin", sin)):
-        if tuple(t.shape) != (n_tok, head_dim) or not t.is_contiguous() or t.dtype != qkv.dtype:
-            raise ValueError(f"{name} must be a contiguous [{n_tok}, {head_dim}] {qkv.dtype} tensor")
+        if t.ndim != 2 or tuple(t.shape) != (rows, head_dim) or not t.is_contiguous() or t.dtype != qkv.dtype:
+            raise ValueError(f"{name} must be a contiguous [{rows}, {head_dim}] {qkv.dtype} tensor")
     beta = beta.reshape(3, head_dim).contiguous()
     threshold = threshold.reshape(3, head_dim).to(beta.dtype).contiguous()
     if slot_mapping.dtype != torch.int64:
@@ -138,7 +181,8 @@ def qkv_rope_lif_pack(
     _lib.check(
         _lib.load().spk_qkv_rope_lif_pack(
             qkv.data_ptr(), _lib.dtype_code(qkv.dtype), (_lib.ctypes.c_int64 * 2)(*qkv.stride()[:2]),
-            cos.data_ptr(), sin.data_ptr(), beta.data_ptr(), threshold.data_ptr(),
+            cos.data_ptr(), sin.data_ptr(), _lib.ptr(positions), rows if positions is not None else 0,
+            beta.data_ptr(), threshold.data_ptr(),
             _lib.dtype_code(beta.dtype), _lib.ptr(q_packed), qs, n_q,
             k_cache.data_ptr(), v_cache.data_ptr(), (_lib.ctypes.c_int64 * 3)(*k_cache.stride()[:3]),
             slot_mapping.data_ptr(), k_cache.shape[2], _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),

@@ -27,7 +27,8 @@ import torch
 import torch.nn.functional as F
 
 from .attention import AttentionMetadata
-from .kernels.decoder_ops import add_rmsnorm, lif_gate_mul, qkv_rope_lif_pack, rmsnorm_mean_t
+from .kernels.decoder_ops import (add_rmsnorm, embed_rmsnorm, lif_gate_mul, qkv_rope_lif_pack,
+                                  rmsnorm_mean_t)
 from .kernels.packing import packed_width
 from .kernels.spike_attention import gather_kv_unpacked, paged_spike_attn_decode
 
@@ -47,6 +48,7 @@ class SpikingQwenConfig:
     rms_norm_eps: float = 1e-6
     rope_theta: float = 1000000.0
     tie_word_embeddings: bool = True
+    max_position_embeddings: int = 32768
     T: int = 4
     beta_init: float = 0.9
     threshold_init: float = 1.0
@@ -99,6 +101,12 @@ class SpikingDecoder:
         # Rotary inverse frequencies as Qwen2RotaryEmbedding builds them (fp32, host).
         exps = torch.arange(0, self.D, 2, dtype=torch.int64).float() / self.D
         self.inv_freq = (1.0 / (c.rope_theta ** exps)).to(self.device)
+        # cos/sin of every position, computed once by the same ops as
+        # rope_tables (so a table row equals the per-step value bit for bit);
+        # the q/k/v kernel reads row positions[i] for token i.
+        with torch.no_grad():
+            self.rope_cos, self.rope_sin = self.rope_tables(
+                torch.arange(c.max_position_embeddings, device=self.device))
 
     # -- weights -----------------------------------------------------------
     def load_reference_state_dict(self, sd: dict[str, torch.Tensor]) -> None:
@@ -155,8 +163,8 @@ class SpikingDecoder:
         H, D, Hq, Hkv = c.hidden_size, self.D, self.Hq, self.Hkv
         n_dec = meta.num_decode_tokens
         bufs = bufs or {}
-        cos, sin = self.rope_tables(positions)
-        h = F.embedding(input_ids, self.embed).unsqueeze(0).expand(T, n, H).contiguous()
+        positions = positions.to(torch.int64).contiguous()
+        h, x = embed_rmsnorm(input_ids, self.embed, self.layers[0].input_norm, c.rms_norm_eps, T)
         q_packed = bufs.get("q_packed")
         if n_dec and q_packed is None:
             q_packed = torch.empty((T, n_dec, Hq, self.W), dtype=torch.int32, device=h.device)
@@ -168,15 +176,15 @@ class SpikingDecoder:
             dense = (torch.empty((T, Hq, n, D), dtype=self.dtype, device=h.device),
                      torch.empty((T, Hkv, n, D), dtype=self.dtype, device=h.device),
                      torch.empty((T, Hkv, n, D), dtype=self.dtype, device=h.device))
-        x = add_rmsnorm(h, None, self.layers[0].input_norm, c.rms_norm_eps)
         delta = None
         for i, L in enumerate(self.layers):
             if i:
                 x = add_rmsnorm(h, delta, L.input_norm, c.rms_norm_eps, out=x)
             k_cache, v_cache = kv_caches[i]
             qkv = F.linear(x, L.w_qkv, L.b_qkv)
-            qkv_rope_lif_pack(qkv, cos, sin, L.lif_qkv_beta, L.lif_qkv_th, k_cache, v_cache,
-                              meta.slot_mapping, Hq, Hkv, D, q_packed=q_packed, n_q=n_dec, dense=dense)
+            qkv_rope_lif_pack(qkv, self.rope_cos, self.rope_sin, L.lif_qkv_beta, L.lif_qkv_th, k_cache,
+                              v_cache, meta.slot_mapping, Hq, Hkv, D, q_packed=q_packed, n_q=n_dec,
+                              dense=dense, positions=positions)
             if n_dec:
                 paged_spike_attn_decode(q_packed, k_cache, v_cache, meta.block_tables, meta.seq_lens,
                                         head_dim=D, block_size=meta.block_size, num_q_heads=Hq,

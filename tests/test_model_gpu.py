@@ -17,7 +17,7 @@ import torch
 
 from model_ref import forward_paged_ref, lif_ref, pack_ref, rms_norm, rotate_half
 from spikeinfer_amd.attention import AttentionMetadata
-from spikeinfer_amd.kernels.decoder_ops import (add_rmsnorm, decode_advance, lif_gate_mul,
+from spikeinfer_amd.kernels.decoder_ops import (add_rmsnorm, decode_advance, embed_rmsnorm, lif_gate_mul,
                                                 qkv_rope_lif_pack, rmsnorm_mean_t)
 from spikeinfer_amd.model import SpikingDecoder, SpikingQwenConfig
 from spikeinfer_amd.runner import DecodeRunner
@@ -50,6 +50,28 @@ def test_add_rmsnorm_matches_qwen2_rmsnorm(gpu, with_delta):
     assert (got != want).float().mean() < 1e-3
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_embed_rmsnorm_matches_embedding_then_norm(gpu, dtype):
+    """h = embedding rows broadcast over T (exact); x = Qwen2RMSNorm(h) to one
+    ulp, as add_rmsnorm; an out-of-range id reads the last row."""
+    g = torch.Generator(device=gpu).manual_seed(3)
+    vocab, hidden, T = 1000, 896, 4
+    emb = (torch.randn((vocab, hidden), generator=g, device=gpu) * 0.05).to(dtype)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g, device=gpu)).to(dtype)
+    ids = torch.randint(0, vocab, (37,), generator=g, device=gpu)
+    ids[5] = vocab + 7
+    h, x = embed_rmsnorm(ids, emb, w, 1e-6, T)
+    rows = emb[ids.clamp(max=vocab - 1)]
+    assert torch.equal(h, rows.unsqueeze(0).expand(T, -1, -1))
+    want = rms_norm(h, w, 1e-6)
+    if dtype == torch.bfloat16:
+        assert _ulps(x, want) <= 1
+        assert (x != want).float().mean() < 1e-3
+    else:
+        torch.testing.assert_close(x, want, rtol=1e-6, atol=1e-6)
+    assert torch.equal(x[0], x[T - 1])
+
+
 @pytest.mark.parametrize("with_delta", [False, True])
 def test_rmsnorm_mean_t_matches_norm_then_mean(gpu, with_delta):
     g = torch.Generator(device=gpu).manual_seed(2)
@@ -70,9 +92,12 @@ def _rope_tables(positions, D, dtype, theta=1e6):
     return e.cos().to(dtype).to(positions.device), e.sin().to(dtype).to(positions.device)
 
 
-@pytest.mark.parametrize("D,Hq,Hkv", [(64, 14, 2), (128, 4, 4), (64, 2, 1)])
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 14, 2), (128, 4, 4), (64, 2, 1), (256, 2, 1)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_qkv_rope_lif_pack_bit_exact(gpu, D, Hq, Hkv, dtype):
+@pytest.mark.parametrize("tables", [False, True])
+def test_qkv_rope_lif_pack_bit_exact(gpu, D, Hq, Hkv, dtype, tables):
+    """Against the torch composition; with ``tables`` the kernel reads
+    cos/sin rows by position from tables of positions 0..4999."""
     T, n, n_q = 4, 23, 9
     g = torch.Generator(device=gpu).manual_seed(D + Hq)
     qkv = (torch.randn((T, n, (Hq + 2 * Hkv) * D), generator=g, device=gpu) * 1.5 + 0.3).to(dtype)
@@ -88,8 +113,14 @@ def test_qkv_rope_lif_pack_bit_exact(gpu, D, Hq, Hkv, dtype):
     vc = torch.zeros_like(kc)
     qp = torch.zeros((T, n_q, Hq, W), dtype=torch.int32, device=gpu)
     dense = tuple(torch.empty((T, H, n, D), dtype=dtype, device=gpu) for H in (Hq, Hkv, Hkv))
-    qkv_rope_lif_pack(qkv, cos, sin, beta, th, kc, vc, slots, Hq, Hkv, D, q_packed=qp, n_q=n_q,
-                      dense=dense)
+    if tables:
+        tc, ts = _rope_tables(torch.arange(5000, device=gpu), D, dtype)
+        assert torch.equal(tc[pos], cos) and torch.equal(ts[pos], sin)
+        qkv_rope_lif_pack(qkv, tc, ts, beta, th, kc, vc, slots, Hq, Hkv, D, q_packed=qp, n_q=n_q,
+                          dense=dense, positions=pos)
+    else:
+        qkv_rope_lif_pack(qkv, cos, sin, beta, th, kc, vc, slots, Hq, Hkv, D, q_packed=qp, n_q=n_q,
+                          dense=dense)
 
     q = qkv[..., :Hq * D].view(T, n, Hq, D)
     k = qkv[..., Hq * D:(Hq + Hkv) * D].view(T, n, Hkv, D)
