@@ -6,30 +6,36 @@
 // Why MFMA: per 16-byte K+V token unit the value side needs n_rep*64 = 448
 // multiply-adds (GQA 7:1).  At 8 TB/s that is ~224 T MAC/s, far above what
 // the fp32 VALU issues, so a lane-per-channel loop cannot approach the HBM
-// roofline.  Here each 64-token step of a wave is one K=64 contraction:
+// roofline.  Here each 128-token step of a wave is one K=128 contraction per
+// output tile:
 //
-//   D[32 x 32] += A[32 x 64] * B[64 x 32]     (v_mfma_scale_f32_32x32x64_f8f6f4)
+//   D[16 x 16] += A[16 x 128] * B[128 x 16]   (v_mfma_scale_f32_16x16x128_f8f6f4)
 //
-//   A rows  = (head h < 8, digit s < 4): row 4h+s holds, per token, digit s of
-//             the weight w(d) = exp(-d*scale), d = popc(q_h & ~k).  The weight
-//             is split into four e4m3 digits, w = sum_s q_s * 2^-(8+4s)
-//             (relative error <= ~1e-6), looked up in a 65-entry LDS table
-//             (built once per scale on the host, passed in the arguments).
-//   B cols  = 32 of the 64 channels; element = fp4 e2m1 0b0001 (= 0.5) where
-//             the v bit is set.  Two MFMAs cover the 64 channels.
+//   A rows  = (head h, digit s < 4) of one row tile (heads 4rt..4rt+3): row
+//             4(h-4rt)+s holds, per token, digit s of the weight
+//             w(d) = exp(-d*scale), d = popc(q_h & ~k).  The weight is split
+//             into four e4m3 digits, w = sum_s q_s * 2^-(8+4s) (relative error
+//             <= ~1e-6), looked up in a 65-entry LDS table (built once per
+//             scale on the host, passed in the arguments).
+//   B cols  = 16 channels 4c+ts (c < 16) of channel tile ts; element = fp4
+//             with the v bit in place (0.5, 1.0 or 2.0 per set bit); a fifth,
+//             all-ones tile accumulates the softmax denominators.
+//   Two row tiles x five column tiles = 10 MFMAs per step (each about half
+//   the issue time of a 32x32x64 one, measured).
 //
 // Bits become MFMA operands through LDS transpose reads:
 //   * v words are staged token-major (8 B per token).  ds_read_b64_tr_b4 on 16
-//     token rows hands lane i the nibble i (channels 4i..4i+3) of all 16 rows,
-//     so `(w >> s) & 0x11111111` is directly eight fp4 elements of channel
-//     4i+s over eight tokens;
+//     token rows hands lane i of each 16-lane group nibble i (channels
+//     4i..4i+3) of all 16 rows, so `w & (0x11111111 << s)` is eight fp4
+//     elements of channel 4i+s over eight tokens (bit 3, the fp4 sign, is
+//     first shifted down to bit 2);
 //   * the 8 digit words of a token (32 bytes, byte 4h+s) are staged
 //     token-major; ds_read_b64_tr_b8 transposes 8x16-byte blocks so lane m
 //     receives byte column m (= A row m) for 8 tokens.
-// Operand layouts (measured on gfx950): A lane l holds row l%32, byte k is
-// K = 32*(l/32)+k; B (fp4) lane l holds column l%32, nibble k is
-// K = 32*(k/16) + 16*(l/32) + k%16; D lane l, acc j is row
-// 8*(j/4) + 4*(l/32) + j%4, column l%32.
+// Operand layouts of the 16x16x128 f8 x f4 MFMA (measured on gfx950 with
+// one-hot probes): A lane l holds row l%16, byte k is
+// K = 16*(l/16) + k%16 + 64*(k/16); B (fp4) lane l holds column l%16, nibble
+// n is K = 32*(l/16) + n; D lane l, acc j is row 4*(l/16) + j, column l%16.
 #include "decode_attn.hpp"
 
 #include <cmath>
@@ -39,6 +45,7 @@ namespace spk {
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 #define SPK_LDS __attribute__((address_space(3)))
 
 namespace mfma {
@@ -57,7 +64,7 @@ struct alignas(16) WaveStage {
   uint4 a[2][kStepTokens];            // digit rows, window-major            (4 KB)
 };
 
-constexpr int kReduceFloats = (kWaves - 1) * 64 * 12;  // 8 values + 4 l per lane
+constexpr int kReduceFloats = (kWaves - 1) * 64 * 10;  // 8 values + 2 l per lane
 constexpr int kSmemBytes =
     (kWaves * (int)sizeof(WaveStage) > kReduceFloats * 4) ? kWaves * (int)sizeof(WaveStage)
                                                             : kReduceFloats * 4;
@@ -122,45 +129,55 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Contracts staged rows [64u, 64u+64) of the step (its even tokens for u = 0,
-// odd for u = 1): two channel tiles and
-// the all-ones tile that accumulates the softmax denominators.
-//   tile 0 column n: channel 4*(n%16) + n/16      (fp4 0001 = 0.5 per set bit)
-//   tile 1 column n: channel 4*(n%16) + 2 + n/16  (fp4 0100 = 2.0 per set bit)
-// Lanes 16..31 of each half shift their transposed v words right by one, so
-// one AND per register selects their channel for both tiles.
-__device__ __forceinline__ void contract_half(const WaveStage &st, int lane, int u, v16f &acc0,
-                                              v16f &acc1, v16f &accl) {
-  const int g = lane >> 5;          // K group of the MFMA operands
-  const int i16 = lane & 15;        // lane within its 16-lane transpose group
-  const int win = (lane >> 4) & 1;  // 16-byte window of a digit row / odd channels
-  const SPK_LDS char *lds_v = (const SPK_LDS char *)st.v + 64 * u * 8;
-  const SPK_LDS char *lds_a = (const SPK_LDS char *)&st.a[win][64 * u];
-  v8i A;
+// Contracts the 128 staged rows of a step with 16x16x128 MFMAs: K index k
+// reads stage row srow(k) = (k%32 < 16 ? 0 : 64) + 16*(k/32) + k%16 (any
+// order shared by A and B gives the same sums; this one lets every 16-lane
+// transpose group read its own contiguous rows).
+//   A, row tile rt (heads 4rt..4rt+3): lane l holds row l%16 = (head, digit),
+//     bytes 0..15 -> K 16q..16q+15 and bytes 16..31 -> K 64+16q.. (q = l/16),
+//     read as four 8-row tr_b8 transposes of the tile's 16-byte window;
+//   B, channel tile s (0..3): lane l holds column l%16 = channel 4*(l%16)+s,
+//     nibble n -> K 32p + n (p = l/16), from two tr_b4 transposes (rows
+//     16p.. and 64+16p..); bit s of each nibble is kept in place for s < 3
+//     (fp4 0.5, 1.0, 2.0) and shifted to bit 2 for s = 3 (2.0);
+//   the all-ones B tile accumulates the softmax denominators.
+__device__ __forceinline__ void contract_step(const WaveStage &st, int lane, v4f (&acc)[2][4],
+                                              v4f (&accl)[2]) {
+  const int q = lane >> 4;
+  const int i16 = lane & 15;
+  const SPK_LDS char *lds_v = (const SPK_LDS char *)st.v;
+  const v2i w0 = tr_b4(lds_v + (16 * q + i16) * 8);
+  const v2i w1 = tr_b4(lds_v + (64 + 16 * q + i16) * 8);
+  const uint32_t w[4] = {static_cast<uint32_t>(w0.x), static_cast<uint32_t>(w0.y),
+                         static_cast<uint32_t>(w1.x), static_cast<uint32_t>(w1.y)};
+  const int r0 = ((q & 1) ? 64 : 0) + 16 * (q >> 1);  // rows of A bytes 0..15; +32 for 16..31
+  const int sub = (i16 >> 1) & 7, hb = (i16 & 1) * 8;
+  v8i A[2];
 #pragma unroll
-  for (int qd = 0; qd < 4; ++qd) {
-    const int row = 32 * g + 8 * qd + ((i16 >> 1) & 7);
-    const v2i r = tr_b8(lds_a + row * 16 + (i16 & 1) * 8);
-    A[2 * qd] = r.x;
-    A[2 * qd + 1] = r.y;
-  }
-  const v2i w0 = tr_b4(lds_v + (16 * g + i16) * 8);
-  const v2i w1 = tr_b4(lds_v + (32 + 16 * g + i16) * 8);
-  // Lanes of the second 16-lane group take the odd channel of each pair:
-  // shifted right by one, bit 0 / bit 2 of every nibble are channels 4i+1 /
-  // 4i+3 (bit 3 takes the next nibble's bit 0 and is masked off below).
-  const uint32_t wv[4] = {static_cast<uint32_t>(w0.x) >> win, static_cast<uint32_t>(w0.y) >> win,
-                          static_cast<uint32_t>(w1.x) >> win, static_cast<uint32_t>(w1.y) >> win};
-  v8i B0 = {}, B1 = {}, Bl = {};
+  for (int rt = 0; rt < 2; ++rt) {
+    const SPK_LDS char *lds_a = (const SPK_LDS char *)&st.a[rt][0];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    B0[i] = static_cast<int>(wv[i] & 0x11111111u);
-    B1[i] = static_cast<int>(wv[i] & 0x44444444u);
-    Bl[i] = 0x11111111;
+    for (int c = 0; c < 4; ++c) {
+      const int row = r0 + 32 * (c >> 1) + 8 * (c & 1) + sub;
+      const v2i r = tr_b8(lds_a + row * 16 + hb);
+      A[rt][2 * c] = r.x;
+      A[rt][2 * c + 1] = r.y;
+    }
   }
-  acc0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B0, acc0, 0, 4, 0, 127, 0, 127);
-  acc1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B1, acc1, 0, 4, 0, 127, 0, 127);
-  accl = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, Bl, accl, 0, 4, 0, 127, 0, 127);
+  constexpr uint32_t kMask[4] = {0x11111111u, 0x22222222u, 0x44444444u, 0x44444444u};
+#pragma unroll
+  for (int ts = 0; ts < 4; ++ts) {
+    v8i B = {};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) B[i] = static_cast<int>((ts == 3 ? w[i] >> 1 : w[i]) & kMask[ts]);
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+      acc[rt][ts] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[rt], B, acc[rt][ts], 0, 4, 0, 127, 0, 127);
+  }
+  const v8i Bl = {0x11111111, 0x11111111, 0x11111111, 0x11111111, 0, 0, 0, 0};
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+    accl[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[rt], Bl, accl[rt], 0, 4, 0, 127, 0, 127);
 }
 
 // Longest-processing-time-first order of the (sequence, partition) items,
@@ -249,7 +266,7 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh) {
 // the partition's 128-token steps round-robin (two steps of loads in flight
 // per wave) and reduce at the end in a fixed order.
 template <int NREP>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6))) void decode_attn_mfma_kernel(AttnParams p) {
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void decode_attn_mfma_kernel(AttnParams p) {
   // Unplanned launch: x = (sequence, timestep, kv head) unit, y = partition.
   // Either way consecutive block ids (dealt round-robin to the 8 XCDs) are
   // sibling units of equal length.
@@ -325,7 +342,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6))
     vw[0] = v2.x; vw[1] = v2.y;
   };
 
-  v16f acc0 = {}, acc1 = {}, accl = {};
+  v4f acc[2][4] = {}, accl[2] = {};
 
   constexpr int kStride = kWaves * kStepTokens;
   const int first = start + wave * kStepTokens;
@@ -346,8 +363,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6))
       stage_step<NREP, true>(st, lane, kw, vw, valid, q0, q1, tab);
     }
     wave_sync();
-    contract_half(st, lane, 0, acc0, acc1, accl);
-    if (!masked || j0 + 1 < end) contract_half(st, lane, 1, acc0, acc1, accl);  // odd tokens
+    contract_step(st, lane, acc, accl);
     wave_sync();
   };
 
@@ -383,63 +399,64 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6))
     else step(k2, v2, true, j0);
   }
 
-  // Per lane: column n = lane%32 of the tiles; rows 4h+s with
-  // h = 2*qd + lane/32, s = j%4, for acc index j = 4*qd + s.  Digit s carries
-  // 2^-(8+4s); a set bit is 0.5 (tile 0, ones tile) or 2.0 (tile 1).
-  float val[8], lh[4];
+  // Per lane: row tile rt holds head 4rt + lane/16 with its four digits in
+  // acc[rt][ts][d] (digit d carries 2^-(8+4d)); column lane%16 of channel
+  // tile ts is channel 4*(lane%16) + ts, whose set bits were 0.5, 1.0, 2.0,
+  // 2.0 for ts = 0..3 (the ones tile: 0.5).
+  float val[8], lh[2];
 #pragma unroll
-  for (int qd = 0; qd < 4; ++qd) {
-    float a0 = 0.f, a1 = 0.f, al = 0.f;
+  for (int rt = 0; rt < 2; ++rt) {
+    float l = 0.f;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float f = ldexpf(1.f, -(7 + 4 * s));
-      a0 += acc0[4 * qd + s] * f;
-      a1 += acc1[4 * qd + s] * (0.25f * f);
-      al += accl[4 * qd + s] * f;
+    for (int d = 0; d < 4; ++d) l += accl[rt][d] * ldexpf(1.f, -(7 + 4 * d));
+    lh[rt] = l;
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts) {
+      const float m = ts == 0 ? 1.f : (ts == 1 ? 0.5f : 0.25f);
+      float a = 0.f;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) a += acc[rt][ts][d] * (m * ldexpf(1.f, -(7 + 4 * d)));
+      val[4 * rt + ts] = a;
     }
-    val[2 * qd] = a0;
-    val[2 * qd + 1] = a1;
-    lh[qd] = al;
   }
 
   // Cross-wave reduction (fixed order) through LDS, reusing the stage area.
   __syncthreads();
   float *red = reinterpret_cast<float *>(smem);
   if (wave > 0) {
-    float *dst = red + ((wave - 1) * 64 + lane) * 12;
+    float *dst = red + ((wave - 1) * 64 + lane) * 10;
 #pragma unroll
     for (int k = 0; k < 8; ++k) dst[k] = val[k];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) dst[8 + k] = lh[k];
+    for (int k = 0; k < 2; ++k) dst[8 + k] = lh[k];
   }
   __syncthreads();
   if (wave != 0) return;
   for (int w = 1; w < kWaves; ++w) {
-    const float *src = red + ((w - 1) * 64 + lane) * 12;
+    const float *src = red + ((w - 1) * 64 + lane) * 10;
 #pragma unroll
     for (int k = 0; k < 8; ++k) val[k] += src[k];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) lh[k] += src[8 + k];
+    for (int k = 0; k < 2; ++k) lh[k] += src[8 + k];
   }
 
-  const int col = lane & 31;
   const bool single = nparts_seq == 1;
 #pragma unroll
-  for (int qd = 0; qd < 4; ++qd) {
-    const int h = 2 * qd + (lane >> 5);
+  for (int rt = 0; rt < 2; ++rt) {
+    const int h = 4 * rt + (lane >> 4);
     if (h >= NREP) continue;
     const int hq = kvh * NREP + h;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int ch = 4 * (col & 15) + 2 * u + (col >> 4);
-      const float a = val[2 * qd + u];
+    for (int ts = 0; ts < 4; ++ts) {
+      const int ch = 4 * (lane & 15) + ts;
+      const float a = val[4 * rt + ts];
       if (single) {
-        const float o = len <= 0 ? 0.f : a / lh[qd];
+        const float o = len <= 0 ? 0.f : a / lh[rt];
         store_f32_as(p.out, t * p.os0 + n * p.os1 + hq * p.os2 + ch * p.os3, p.out_dtype, o);
       } else {
         float *dst = p.ws + ((((int64_t)part * p.T + t) * p.N + n) * p.Hq + hq) * 65;
         dst[ch] = a;
-        if (ch == 0) dst[64] = lh[qd];
+        if (ch == 0) dst[64] = lh[rt];
       }
     }
   }
