@@ -115,7 +115,7 @@ __device__ __forceinline__ void stage_step(WaveStage &st, int lane, const uint64
     token_digits<NREP, MASKED>(kw[e], valid[e], q0, q1, tab, dig);
     const int row = lane + 64 * e;
     st.a[0][row] = make_uint4(dig[0], dig[1], dig[2], dig[3]);
-    st.a[1][row] = make_uint4(dig[4], dig[5], dig[6], dig[7]);
+    if (NREP > 4) st.a[1][row] = make_uint4(dig[4], dig[5], dig[6], dig[7]);
     const uint64_t v = (!MASKED || valid[e]) ? vw[e] : 0ull;
     st.v[row] = v;
   }
@@ -141,6 +141,7 @@ __device__ __forceinline__ void wave_sync() {
 //     16p.. and 64+16p..); bit s of each nibble is kept in place for s < 3
 //     (fp4 0.5, 1.0, 2.0) and shifted to bit 2 for s = 3 (2.0);
 //   the all-ones B tile accumulates the softmax denominators.
+template <int RT>  // row tiles: heads 4rt..4rt+3 for rt < RT
 __device__ __forceinline__ void contract_step(const WaveStage &st, int lane, v4f (&acc)[2][4],
                                               v4f (&accl)[2]) {
   const int q = lane >> 4;
@@ -154,7 +155,7 @@ __device__ __forceinline__ void contract_step(const WaveStage &st, int lane, v4f
   const int sub = (i16 >> 1) & 7, hb = (i16 & 1) * 8;
   v8i A[2];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
     const SPK_LDS char *lds_a = (const SPK_LDS char *)&st.a[rt][0];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -171,12 +172,12 @@ __device__ __forceinline__ void contract_step(const WaveStage &st, int lane, v4f
 #pragma unroll
     for (int i = 0; i < 4; ++i) B[i] = static_cast<int>((ts == 3 ? w[i] >> 1 : w[i]) & kMask[ts]);
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
       acc[rt][ts] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[rt], B, acc[rt][ts], 0, 4, 0, 127, 0, 127);
   }
   const v8i Bl = {0x11111111, 0x11111111, 0x11111111, 0x11111111, 0, 0, 0, 0};
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int rt = 0; rt < RT; ++rt)
     accl[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[rt], Bl, accl[rt], 0, 4, 0, 127, 0, 127);
 }
 
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
       stage_step<NREP, true>(st, lane, kw, vw, valid, q0, q1, tab);
     }
     wave_sync();
-    contract_step(st, lane, acc, accl);
+    contract_step<(NREP > 4 ? 2 : 1)>(st, lane, acc, accl);
     wave_sync();
   };
 

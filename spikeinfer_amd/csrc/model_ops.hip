@@ -20,6 +20,9 @@
 namespace spk {
 
 constexpr int kTBatchQkv = 4;  // timesteps whose loads are issued together
+// q/k/v launches with at least this many 8-channel lanes (prefill) take the
+// vector kernel; smaller ones (decode) the channel-pair kernel.
+constexpr int64_t kQkvWideThreads = 256 * 256;
 constexpr int kMaxMeanT = 8;   // timesteps rmsnorm_mean_t keeps in registers
 constexpr int kNormRegVecs = 4;  // 16-byte vectors per lane add_rmsnorm keeps in registers
 
@@ -270,6 +273,120 @@ struct QkvParams {
   int64_t n_tok;
   int Hq, Hkv, D;
 };
+
+// Wide launches (prefill): D/8 lanes per (token, head) row, 8 channels (16
+// bytes) per lane, fewer and wider memory accesses than the pair layout.  The
+// rotate-half partner of channel c < D/2 is c + D/2, held by lane sub ^ (D/16)
+// of the same row; rows never straddle a wave (64 % (D/8) == 0).
+template <int DT>
+__global__ __launch_bounds__(256) void qkv_rope_lif_pack_vec_kernel(QkvParams p) {
+  typedef typename Elem<DT>::T E;
+  typedef E Vec __attribute__((ext_vector_type(8)));
+  const int L = p.D >> 3;
+  const int Htot = p.Hq + 2 * p.Hkv;
+  const int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t row = g / L;
+  const int sub = static_cast<int>(g - row * L);
+  const bool active = row < p.n_tok * Htot;
+  const int64_t tok = active ? row / Htot : 0;
+  const int hh = active ? static_cast<int>(row - tok * Htot) : 0;
+  const int site = hh < p.Hq ? 0 : (hh < p.Hq + p.Hkv ? 1 : 2);
+  const int h = site == 0 ? hh : (site == 1 ? hh - p.Hq : hh - p.Hq - p.Hkv);
+  const int cl = sub * 8;                      // channel within the head
+  const int half = L >> 1;
+  const bool low = sub < half;                 // channels below D/2
+  const bool rope = site != 2;
+
+  float beta[8], th[8], u[8], cs[8], sn[8];
+  int64_t crow = tok;
+  if (p.pos && active) {  // positions outside the table read its nearest row
+    const int64_t q = p.pos[tok];
+    crow = q < 0 ? 0 : (q >= p.table_rows ? p.table_rows - 1 : q);
+  }
+  const Vec cv = active ? reinterpret_cast<const Vec *>(static_cast<const E *>(p.cos) + crow * p.D)[sub] : Vec{};
+  const Vec sv = active ? reinterpret_cast<const Vec *>(static_cast<const E *>(p.sin) + crow * p.D)[sub] : Vec{};
+  load_params(p.beta, p.param_dtype, site * p.D + cl, beta);
+  load_params(p.th, p.param_dtype, site * p.D + cl, th);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    beta[i] = clamp01(beta[i]);
+    u[i] = 0.f;
+    cs[i] = elem_to_f32<DT>(cv[i]);
+    sn[i] = elem_to_f32<DT>(sv[i]);
+  }
+
+  // Destination of this row's packed words.
+  uint64_t *dst = nullptr;
+  int64_t dstep = 0;  // per timestep, in uint64 words
+  if (active) {
+    if (site == 0) {
+      if (tok < p.n_q) {
+        dst = p.q_packed + (tok * p.qs1 + h * p.qs2) / 2;
+        dstep = p.qs0 / 2;
+      }
+    } else {
+      const int64_t slot = p.slots[tok];
+      if (slot >= 0 && slot < p.num_slots) {
+        dst = (site == 1 ? p.k_cache : p.v_cache) + (h * p.cs1 + slot * p.cs2) / 2;
+        dstep = p.cs0 / 2;
+      }
+    }
+  }
+  E *dense = active ? static_cast<E *>(p.dense[site]) : nullptr;
+  const int Hs = site == 0 ? p.Hq : p.Hkv;
+  const int64_t dense_row = (static_cast<int64_t>(h) * p.n_tok + tok) * p.D + cl;
+  const int64_t dense_tstep = static_cast<int64_t>(Hs) * p.n_tok * p.D;
+
+  const E *xrow = static_cast<const E *>(p.x) + tok * p.xs1 + hh * p.D + cl;
+  for (int t0 = 0; t0 < p.T; t0 += kTBatchQkv) {
+    Vec xv[kTBatchQkv];
+#pragma unroll
+    for (int k = 0; k < kTBatchQkv; ++k)
+      xv[k] = (active && t0 + k < p.T)
+                  ? __builtin_nontemporal_load(reinterpret_cast<const Vec *>(xrow + (t0 + k) * p.xs0))
+                  : Vec{};
+#pragma unroll
+    for (int k = 0; k < kTBatchQkv; ++k) {
+      if (t0 + k >= p.T) break;
+      const int t = t0 + k;
+      const Vec x = xv[k];
+      // Partner half of the head (all lanes take part in the exchange).
+      Vec xp;
+      {
+        typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+        U4 w = __builtin_bit_cast(U4, x);
+        U4 r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = __shfl_xor(w[j], half);
+        xp = __builtin_bit_cast(Vec, r);
+      }
+      uint32_t byte = 0;
+      Vec spk;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float cur = elem_to_f32<DT>(x[i]);
+        if (rope) {
+          const float xr = low ? -elem_to_f32<DT>(xp[i]) : elem_to_f32<DT>(xp[i]);
+          cur = round_to<DT>(round_to<DT>(cur * cs[i]) + round_to<DT>(xr * sn[i]));
+        }
+        const bool s = lif_step(u[i], cur, beta[i], th[i]);
+        byte |= s ? (1u << i) : 0u;
+        spk[i] = spike_elem<DT>(s);
+      }
+      // OR the 8 spike bytes of each aligned 8-lane group into a 64-bit word.
+      const int s8 = sub & 7;
+      uint32_t lo = s8 < 4 ? byte << (8 * s8) : 0u;
+      uint32_t hi = s8 < 4 ? 0u : byte << (8 * (s8 - 4));
+#pragma unroll
+      for (int off = 1; off < 8; off <<= 1) {
+        lo |= __shfl_xor(lo, off);
+        hi |= __shfl_xor(hi, off);
+      }
+      if (dst && s8 == 0) dst[t * dstep + (sub >> 3)] = (static_cast<uint64_t>(hi) << 32) | lo;
+      if (dense) *reinterpret_cast<Vec *>(dense + t * dense_tstep + dense_row) = spk;
+    }
+  }
+}
 
 // R = min(D/2, 64) lanes per (token, head) row; lane `sub` owns the channel
 // pairs (c, c + D/2) for c = sub + R*j, j < D/(2R), so the rotate-half
@@ -627,13 +744,22 @@ extern "C" int spk_qkv_rope_lif_pack(
   p.Hq = Hq;
   p.Hkv = Hkv;
   p.D = D;
-  const int64_t threads = n_tok * (Hq + 2 * Hkv) * (D / 2 < 64 ? D / 2 : 64);
-  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (x_dtype == SPK_BF16)
-    qkv_rope_lif_pack_kernel<SPK_BF16><<<grid, 256, 0, s>>>(p);
-  else
-    qkv_rope_lif_pack_kernel<SPK_F16><<<grid, 256, 0, s>>>(p);
+  const int64_t rows = n_tok * (Hq + 2 * Hkv);
+  if (rows * (D / 8) >= kQkvWideThreads) {  // enough work for 8 channels per lane
+    const dim3 grid(static_cast<unsigned>((rows * (D / 8) + 255) / 256));
+    if (x_dtype == SPK_BF16)
+      qkv_rope_lif_pack_vec_kernel<SPK_BF16><<<grid, 256, 0, s>>>(p);
+    else
+      qkv_rope_lif_pack_vec_kernel<SPK_F16><<<grid, 256, 0, s>>>(p);
+  } else {
+    const int64_t threads = rows * (D / 2 < 64 ? D / 2 : 64);
+    const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+    if (x_dtype == SPK_BF16)
+      qkv_rope_lif_pack_kernel<SPK_BF16><<<grid, 256, 0, s>>>(p);
+    else
+      qkv_rope_lif_pack_kernel<SPK_F16><<<grid, 256, 0, s>>>(p);
+  }
   return check_launch("qkv_rope_lif_pack");
 }
 

@@ -92,20 +92,22 @@ def _rope_tables(positions, D, dtype, theta=1e6):
     return e.cos().to(dtype).to(positions.device), e.sin().to(dtype).to(positions.device)
 
 
-@pytest.mark.parametrize("D,Hq,Hkv", [(64, 14, 2), (128, 4, 4), (64, 2, 1), (256, 2, 1)])
+@pytest.mark.parametrize("D,Hq,Hkv,n", [(64, 14, 2, 23), (128, 4, 4, 23), (64, 2, 1, 23), (256, 2, 1, 23),
+                                         (64, 14, 2, 512)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("tables", [False, True])
-def test_qkv_rope_lif_pack_bit_exact(gpu, D, Hq, Hkv, dtype, tables):
+def test_qkv_rope_lif_pack_bit_exact(gpu, D, Hq, Hkv, n, dtype, tables):
     """Against the torch composition; with ``tables`` the kernel reads
-    cos/sin rows by position from tables of positions 0..4999."""
-    T, n, n_q = 4, 23, 9
+    cos/sin rows by position from tables of positions 0..4999.  512 tokens
+    take the wide (8 channels per lane) kernel, 23 the channel-pair one."""
+    T, n_q = 4, 9
     g = torch.Generator(device=gpu).manual_seed(D + Hq)
     qkv = (torch.randn((T, n, (Hq + 2 * Hkv) * D), generator=g, device=gpu) * 1.5 + 0.3).to(dtype)
     beta = (0.6 + 0.4 * torch.rand((3, D), generator=g, device=gpu)).to(dtype)
     th = (0.5 + torch.rand((3, D), generator=g, device=gpu)).to(dtype)
     pos = torch.randint(0, 5000, (n,), generator=g, device=gpu)
     cos, sin = _rope_tables(pos, D, dtype)
-    slots_n = 200
+    slots_n = max(200, 2 * n)
     slots = torch.randperm(slots_n, generator=g, device=gpu)[:n]
     slots[3] = -1  # skipped token
     W = D // 32
