@@ -307,7 +307,13 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
   if (tid <= 64) tab[tid] = p.digits[tid];
   const int nblk = end > start ? ((end - start - 1) >> p.bs_log2) + 1 : 0;
   const int blk0 = start >> p.bs_log2;
-  for (int b = tid; b < nblk; b += kWaves * 64) blocks[b] = p.bt[n * p.bts0 + (blk0 + b) * p.bts1];
+  // Physical blocks outside the cache are replaced by block 0 here, once, so
+  // the loads below never leave [0, num_slots) (a pair never straddles a block).
+  const uint32_t num_blocks = static_cast<uint32_t>(min<int64_t>(p.num_slots >> p.bs_log2, 0xffffffffll));
+  for (int b = tid; b < nblk; b += kWaves * 64) {
+    const uint32_t phys = static_cast<uint32_t>(p.bt[n * p.bts0 + (blk0 + b) * p.bts1]);
+    blocks[b] = static_cast<int32_t>(phys < num_blocks ? phys : 0u);
+  }
 
   uint32_t q0[8], q1[8];
 #pragma unroll
@@ -324,18 +330,16 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
   const uint64_t *kbase = reinterpret_cast<const uint64_t *>(p.k + t * p.ks0 + kvh * p.ks1);
   const uint64_t *vbase = reinterpret_cast<const uint64_t *>(p.v + t * p.vs0 + kvh * p.vs1);
   const int bs_mask = (1 << p.bs_log2) - 1;
-  const uint64_t num_slots = static_cast<uint64_t>(p.num_slots);
 
   // Tokens j, j+1 of this partition (j even, same block as block_size >= 2)
   // -> their K/V words, one 16-byte load each.  Pairs past the partition
-  // re-read its last pair (clamped) so the loads stay unconditional; slots
-  // outside the cache are never dereferenced.
+  // re-read its last pair (clamped) so the loads stay unconditional; the
+  // staged block ids are inside the cache, so every slot is.
+  const int last_pair = (end - 1) & ~1;
   auto load = [&](int j, uint64_t (&kw)[2], uint64_t (&vw)[2]) {
-    const int jj = min(j, (end - 1) & ~1);
-    const int phys = blocks[(jj - start) >> p.bs_log2];
-    uint64_t slot = (static_cast<uint64_t>(static_cast<uint32_t>(phys)) << p.bs_log2) |
-                    static_cast<uint64_t>(jj & bs_mask);
-    slot = slot + 1 < num_slots ? slot : 0;
+    const int jj = min(j, last_pair);
+    const uint32_t phys = static_cast<uint32_t>(blocks[(jj - start) >> p.bs_log2]);
+    const uint64_t slot = (static_cast<uint64_t>(phys) << p.bs_log2) | static_cast<uint64_t>(jj & bs_mask);
     typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
     const v2u64 k2 = __builtin_nontemporal_load(reinterpret_cast<const v2u64 *>(kbase + slot));
     const v2u64 v2 = __builtin_nontemporal_load(reinterpret_cast<const v2u64 *>(vbase + slot));
@@ -372,8 +376,12 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
   // flight is never copied (a copy would wait for it).
   uint64_t k0[2], v0[2], k1[2], v1[2], k2[2], v2[2];
   const int lo = 2 * lane;
-  load(first + lo, k0, v0);
-  load(first + kStride + lo, k1, v1);
+  // A wave with no tokens (short or empty partition) issues no loads: only
+  // then is every pair index inside the staged block range [0, nblk).
+  if (ntotal > 0) {
+    load(first + lo, k0, v0);
+    load(first + kStride + lo, k1, v1);
+  }
   int i = 0;
   for (; i + 3 <= nfull; i += 3) {
     load(first + (i + 2) * kStride + lo, k2, v2);
