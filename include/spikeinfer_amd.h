@@ -174,6 +174,37 @@ int spk_unpack(const int32_t *words, int64_t rows, int C, void *out,
  * ------------------------------------------------------------------------ */
 
 /*
+ * Decode attention that derives its own spikes: for the N decode tokens,
+ * RoPE -> LIF -> pack of each unit's q heads and current k/v head (exactly as
+ * spk_qkv_rope_lif_pack computes them), the current k/v words written to the
+ * token's cache slot, then the same attention as spk_decode_attn over
+ * seq_lens[i] tokens (the current one included).  One launch replaces
+ * spk_qkv_rope_lif_pack + spk_decode_attn on a decode-only batch
+ * (spikeinfer/modeling_fast.py:121-135 + attention.py:138-149 + the Triton
+ * launch in spike_attention.py:204-220).
+ *
+ *   x        x_dtype (BF16/F16) [T, N, (Hq + 2*Hkv) * 64], channel stride 1,
+ *            strides {t, token} in elements (the q/k/v projection output)
+ *   cos, sin x_dtype [table_rows, 64] tables; token i uses row positions[i]
+ *   beta, threshold  param_dtype [3, 64]: q, k and v sites
+ *   slot_mapping int64 [N]: cache slot of each token's k/v words (outside
+ *            [0, num_slots): not written)
+ *   k_cache, v_cache int32 [T, Hkv, num_slots, 2] at cache_strides
+ *   block_tables, seq_lens, out, workspace: as spk_decode_attn.
+ * head_dim must be 64, Hq/Hkv <= 8 and T <= 8 (SPK_EUNSUPPORTED otherwise).
+ */
+int spk_qkv_decode_attn(const void *x, int x_dtype, const int64_t x_strides[2], const void *cos,
+                        const void *sin, const int64_t *positions, int64_t table_rows,
+                        const void *beta, const void *threshold, int param_dtype,
+                        const int64_t *slot_mapping, int32_t *k_cache, int32_t *v_cache,
+                        const int64_t cache_strides[4], int64_t num_slots,
+                        const int32_t *block_tables, int64_t bt_stride0, int64_t bt_stride1,
+                        const int32_t *seq_lens, void *out, int out_dtype,
+                        const int64_t out_strides[4], int T, int N, int Hq, int Hkv, int head_dim,
+                        int block_size, int max_blocks, float scale, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/*
  * Residual add + RMSNorm over rows of `hidden` contiguous elements, dtype in
  * {F32, F16, BF16}.  When delta != NULL, h <- round(h + delta) in place; then
  * out = round(weight * round(x * rsqrt(mean(x^2) + eps))), x = float(h).

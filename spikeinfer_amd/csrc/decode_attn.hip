@@ -251,18 +251,22 @@ extern "C" size_t spk_decode_attn_workspace_bytes(int T, int N, int Hq, int Hkv,
   return partials + order;
 }
 
-extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], const int32_t *k_cache,
-                               const int64_t k_strides[4], const int32_t *v_cache,
-                               const int64_t v_strides[4], int64_t num_slots,
-                               const int32_t *block_tables, int64_t bt_stride0, int64_t bt_stride1,
-                               const int32_t *seq_lens, void *out, int out_dtype,
-                               const int64_t out_strides[4], int T, int N, int Hq, int Hkv,
-                               int head_dim, int block_size, int max_blocks, float scale,
-                               void *workspace, size_t workspace_bytes, void *stream) {
+// Shared by spk_decode_attn and spk_qkv_decode_attn: validation, parameters,
+// path choice and launches.  fz != nullptr selects the fused q/k/v path
+// (matrix-core kernel only; its x dtype in fused_dtype).
+static int decode_attn_impl(const int32_t *q, const int64_t q_strides[4], const int32_t *k_cache,
+                            const int64_t k_strides[4], const int32_t *v_cache,
+                            const int64_t v_strides[4], int64_t num_slots,
+                            const int32_t *block_tables, int64_t bt_stride0, int64_t bt_stride1,
+                            const int32_t *seq_lens, void *out, int out_dtype,
+                            const int64_t out_strides[4], int T, int N, int Hq, int Hkv,
+                            int head_dim, int block_size, int max_blocks, float scale,
+                            void *workspace, size_t workspace_bytes, void *stream,
+                            const FusedParams *fz, int fused_dtype) {
   int rc = check_common(T, N, Hq, Hkv, head_dim, block_size);
   if (rc) return rc;
   if (!valid_float_dtype(out_dtype)) return fail(SPK_EINVAL, "out dtype %d not a float type", out_dtype);
-  if (q_strides[3] != 1 || k_strides[3] != 1 || v_strides[3] != 1)
+  if ((!fz && q_strides[3] != 1) || k_strides[3] != 1 || v_strides[3] != 1)
     return fail(SPK_EINVAL, "packed word axis must be contiguous");
   if (!(scale > 0.f) || scale * head_dim > 80.f)
     return fail(SPK_EINVAL, "scale=%g outside (0, 80/head_dim]", (double)scale);
@@ -273,8 +277,10 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
     return fail(SPK_EINVAL, "workspace of %zu bytes, need %zu", workspace_bytes, need);
 
   AttnParams p{};
-  p.q = reinterpret_cast<const uint32_t *>(q);
-  p.qs0 = q_strides[0]; p.qs1 = q_strides[1]; p.qs2 = q_strides[2];
+  if (!fz) {
+    p.q = reinterpret_cast<const uint32_t *>(q);
+    p.qs0 = q_strides[0]; p.qs1 = q_strides[1]; p.qs2 = q_strides[2];
+  }
   p.k = reinterpret_cast<const uint32_t *>(k_cache);
   p.ks0 = k_strides[0]; p.ks1 = k_strides[1]; p.ks2 = k_strides[2];
   p.v = reinterpret_cast<const uint32_t *>(v_cache);
@@ -291,19 +297,22 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
   p.num_parts = (int)((ctx_max + p.part_len - 1) / p.part_len);
   p.ws = static_cast<float *>(workspace);
   if (p.ws == nullptr && need > 0) return fail(SPK_EINVAL, "workspace required");
+  if (fz) p.fz = *fz;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   dim3 grid(N * T * Hkv, p.num_parts);
   const int W = (head_dim + 31) / 32;
   const char *path = getenv("SPIKEINFER_AMD_ATTN_PATH");
-  const bool force_general = path && strcmp(path, "general") == 0;
+  const bool force_general = !fz && path && strcmp(path, "general") == 0;
   if (!force_general && mfma_path_supported(p)) {
     build_digit_table(scale, p.digits);
     const size_t partial_floats = p.num_parts > 1 ? (size_t)p.num_parts * T * N * Hq * (head_dim + 1) : 0;
     const bool plan = plan_launch(ctx_max);
     int32_t *order = plan_in_workspace(ctx_max, (int64_t)p.num_parts * N)
                          ? reinterpret_cast<int32_t *>(p.ws + partial_floats) : nullptr;
-    launch_decode_mfma(p, plan, order, s);
+    launch_decode_mfma(p, plan, order, s, fz ? fused_dtype : 0);
+  } else if (fz) {
+    return fail(SPK_EUNSUPPORTED, "qkv_decode_attn: needs head_dim 64, Hq/Hkv <= 8, aligned caches");
   } else switch (W) {
     case 1: launch_general<1>(p, grid, s); break;
     case 2: launch_general<2>(p, grid, s); break;
@@ -317,6 +326,65 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
     if ((rc = check_launch("decode_attn_combine"))) return rc;
   }
   return SPK_OK;
+}
+
+extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], const int32_t *k_cache,
+                               const int64_t k_strides[4], const int32_t *v_cache,
+                               const int64_t v_strides[4], int64_t num_slots,
+                               const int32_t *block_tables, int64_t bt_stride0, int64_t bt_stride1,
+                               const int32_t *seq_lens, void *out, int out_dtype,
+                               const int64_t out_strides[4], int T, int N, int Hq, int Hkv,
+                               int head_dim, int block_size, int max_blocks, float scale,
+                               void *workspace, size_t workspace_bytes, void *stream) {
+  return decode_attn_impl(q, q_strides, k_cache, k_strides, v_cache, v_strides, num_slots,
+                          block_tables, bt_stride0, bt_stride1, seq_lens, out, out_dtype,
+                          out_strides, T, N, Hq, Hkv, head_dim, block_size, max_blocks, scale,
+                          workspace, workspace_bytes, stream, nullptr, 0);
+}
+
+extern "C" int spk_qkv_decode_attn(const void *x, int x_dtype, const int64_t x_strides[2],
+                                   const void *cos, const void *sin, const int64_t *positions,
+                                   int64_t table_rows, const void *beta, const void *threshold,
+                                   int param_dtype, const int64_t *slot_mapping, int32_t *k_cache,
+                                   int32_t *v_cache, const int64_t cache_strides[4],
+                                   int64_t num_slots, const int32_t *block_tables,
+                                   int64_t bt_stride0, int64_t bt_stride1, const int32_t *seq_lens,
+                                   void *out, int out_dtype, const int64_t out_strides[4], int T,
+                                   int N, int Hq, int Hkv, int head_dim, int block_size,
+                                   int max_blocks, float scale, void *workspace,
+                                   size_t workspace_bytes, void *stream) {
+  if (x_dtype != SPK_BF16 && x_dtype != SPK_F16)
+    return fail(SPK_EUNSUPPORTED, "qkv_decode_attn: input dtype %d (bf16 or f16 only)", x_dtype);
+  if (!valid_float_dtype(param_dtype))
+    return fail(SPK_EINVAL, "qkv_decode_attn: parameter dtype %d is not a float type", param_dtype);
+  if (T < 1 || T > kMaxFusedT)
+    return fail(SPK_EUNSUPPORTED, "qkv_decode_attn: T=%d (1..%d)", T, kMaxFusedT);
+  if (head_dim != 64)
+    return fail(SPK_EUNSUPPORTED, "qkv_decode_attn: head_dim=%d (64 only)", head_dim);
+  if (N > 0 && (!x || !cos || !sin || !positions || !beta || !threshold || !slot_mapping ||
+                !k_cache || !v_cache || table_rows < 1))
+    return fail(SPK_EINVAL, "qkv_decode_attn: null pointer or empty rotary table");
+  if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 7 ||
+      (cache_strides[0] | cache_strides[1] | cache_strides[2]) & 1)
+    return fail(SPK_EINVAL, "qkv_decode_attn: caches must be 8-byte aligned with even strides");
+  FusedParams fz{};
+  fz.x = x;
+  fz.xs0 = x_strides[0];
+  fz.xs1 = x_strides[1];
+  fz.cos = cos;
+  fz.sin = sin;
+  fz.pos = positions;
+  fz.table_rows = table_rows;
+  fz.beta = beta;
+  fz.th = threshold;
+  fz.param_dtype = param_dtype;
+  fz.slots = slot_mapping;
+  fz.k_out = reinterpret_cast<uint32_t *>(k_cache);
+  fz.v_out = reinterpret_cast<uint32_t *>(v_cache);
+  return decode_attn_impl(nullptr, nullptr, k_cache, cache_strides, v_cache, cache_strides,
+                          num_slots, block_tables, bt_stride0, bt_stride1, seq_lens, out,
+                          out_dtype, out_strides, T, N, Hq, Hkv, head_dim, block_size, max_blocks,
+                          scale, workspace, workspace_bytes, stream, &fz, x_dtype);
 }
 
 extern "C" int spk_decode_scores(const int32_t *q, const int64_t q_strides[4],

@@ -11,6 +11,23 @@ constexpr int kAttnThreads = 256;   // 4 waves
 // kernel; choose_part_len never makes a partition span more blocks.
 constexpr int kMaxStagedBlocks = 2048;
 constexpr int kMaxRep = 16;
+constexpr int kMaxFusedT = 8;  // timesteps the fused q/k/v path keeps in registers
+
+// Inputs of the fused q/k/v-spike path (spk_qkv_decode_attn): the q/k/v
+// projection currents of the decode tokens, from which each workgroup derives
+// its own heads' spikes (RoPE -> LIF), writing the current token's k/v words
+// to the cache.
+struct FusedParams {
+  const void *x;            // [T, n_tok, (Hq + 2 Hkv) * 64] currents (bf16 or f16)
+  int64_t xs0, xs1;         // timestep and token strides, in elements
+  const void *cos, *sin;    // [table_rows, 64] rotary tables of x's dtype
+  const int64_t *pos;       // [n_tok] positions (rows of the tables)
+  int64_t table_rows;
+  const void *beta, *th;    // [3, 64]: q, k and v sites
+  int param_dtype;
+  const int64_t *slots;     // [n_tok] cache slot of each token's k/v words
+  uint32_t *k_out, *v_out;  // the caches (same layout as AttnParams::k / v)
+};
 
 struct AttnParams {
   const uint32_t *q;
@@ -42,6 +59,7 @@ struct AttnParams {
   // exp(-d*scale) * 2^8 (byte s weighs 2^-(4s)), built on the host once per
   // scale (build_digit_table) and copied into LDS by every workgroup.
   uint32_t digits[65];
+  FusedParams fz;  // used by the fused instantiations only
 };
 
 // Fills digits[] for `scale` (host; reuses the last table when unchanged).
@@ -73,6 +91,7 @@ inline bool plan_in_workspace(int64_t ctx_max, int64_t items) {
 }
 // Launches the matrix-core kernel; `plan` orders it longest first, from
 // `order` when not null (after the planner kernel fills it), else in-kernel.
-void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s);
+// fused_dtype: 0 for q from p.q, else the dtype (SPK_BF16 / SPK_F16) of p.fz.x.
+void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s, int fused_dtype = 0);
 
 }  // namespace spk

@@ -37,6 +37,7 @@
 // K = 16*(l/16) + k%16 + 64*(k/16); B (fp4) lane l holds column l%16, nibble
 // n is K = 32*(l/16) + n; D lane l, acc j is row 4*(l/16) + j, column l%16.
 #include "decode_attn.hpp"
+#include "lif_math.hpp"
 
 #include <cmath>
 
@@ -266,8 +267,96 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh) {
 // One workgroup = 4 waves = one (partition, t, kv head, sequence); waves take
 // the partition's 128-token steps round-robin (two steps of loads in flight
 // per wave) and reduce at the end in a fixed order.
-template <int NREP>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void decode_attn_mfma_kernel(AttnParams p) {
+// Fused path: the unit's spikes at timestep t from the q/k/v currents, as
+// spk_qkv_rope_lif_pack computes them (the same RoPE roundings and LIF
+// recurrence over timesteps 0..t).  Each wave takes two heads a round: lane
+// half lane/32 one head, lane%32 the channel pair (c, c + 32), so a ballot
+// of each half's spikes is that head's packed word.  fw[h] for the NREP q
+// heads, fw[NREP] for k, fw[NREP + 1] for v.  fused_load issues every load
+// of the unit at once (ahead of the block-table staging); fused_spikes then
+// computes, overlapping the first K/V loads.
+template <int XDT>
+struct FusedIn {
+  typedef typename Elem<XDT>::T E;
+  static constexpr int kRounds = 2;  // (NREP + 2) heads <= 10, 8 per round
+  E xl[kRounds][kMaxFusedT], xh[kRounds][kMaxFusedT];
+  float blo[kRounds], bhi[kRounds], tlo[kRounds], thi[kRounds];
+  float clo[kRounds], chi[kRounds], slo[kRounds], shi[kRounds];
+};
+
+template <int NREP, int XDT>
+__device__ __forceinline__ void fused_load(const AttnParams &p, int n, int t, int kvh, int wave,
+                                           int lane, FusedIn<XDT> &in) {
+  typedef typename Elem<XDT>::T E;
+  const FusedParams &f = p.fz;
+  const int64_t q = f.pos[n];
+  const int64_t prow = q < 0 ? 0 : (q >= f.table_rows ? f.table_rows - 1 : q);
+  const int c = lane & 31;
+  const E *cosr = static_cast<const E *>(f.cos) + prow * 64;
+  const E *sinr = static_cast<const E *>(f.sin) + prow * 64;
+  const E *xtok = static_cast<const E *>(f.x) + n * f.xs1;
+#pragma unroll
+  for (int r = 0; r < (NREP + 2 + 7) / 8; ++r) {
+    const int hi = r * 8 + wave * 2 + (lane >> 5);
+    const bool act = hi < NREP + 2;
+    const int site = hi < NREP ? 0 : (hi == NREP ? 1 : 2);
+    const int col = (hi < NREP ? kvh * NREP + hi : (hi == NREP ? p.Hq + kvh : p.Hq + p.Hkv + kvh)) * 64;
+    float v[1];
+    load_params(f.beta, f.param_dtype, site * 64 + c, v);
+    in.blo[r] = clamp01(v[0]);
+    load_params(f.beta, f.param_dtype, site * 64 + c + 32, v);
+    in.bhi[r] = clamp01(v[0]);
+    load_params(f.th, f.param_dtype, site * 64 + c, v);
+    in.tlo[r] = v[0];
+    load_params(f.th, f.param_dtype, site * 64 + c + 32, v);
+    in.thi[r] = v[0];
+    in.clo[r] = elem_to_f32<XDT>(cosr[c]);
+    in.chi[r] = elem_to_f32<XDT>(cosr[c + 32]);
+    in.slo[r] = elem_to_f32<XDT>(sinr[c]);
+    in.shi[r] = elem_to_f32<XDT>(sinr[c + 32]);
+#pragma unroll
+    for (int k = 0; k < kMaxFusedT; ++k) {
+      in.xl[r][k] = act && k <= t ? xtok[k * f.xs0 + col + c] : E{};
+      in.xh[r][k] = act && k <= t ? xtok[k * f.xs0 + col + c + 32] : E{};
+    }
+  }
+}
+
+template <int NREP, int XDT>
+__device__ __forceinline__ void fused_spikes(const FusedIn<XDT> &in, int t, int wave, int lane,
+                                             uint64_t *fw) {
+  const int c = lane & 31;
+#pragma unroll
+  for (int r = 0; r < (NREP + 2 + 7) / 8; ++r) {
+    const int hi = r * 8 + wave * 2 + (lane >> 5);
+    const bool rope = hi <= NREP;  // q and k heads; v has none
+    bool s_lo = false, s_hi = false;
+    float ulo = 0.f, uhi = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxFusedT; ++k) {
+      if (k > t) break;
+      float lo = elem_to_f32<XDT>(in.xl[r][k]), hi2 = elem_to_f32<XDT>(in.xh[r][k]);
+      if (rope) {
+        const float rl = round_to<XDT>(round_to<XDT>(lo * in.clo[r]) + round_to<XDT>(-hi2 * in.slo[r]));
+        const float rh = round_to<XDT>(round_to<XDT>(hi2 * in.chi[r]) + round_to<XDT>(lo * in.shi[r]));
+        lo = rl;
+        hi2 = rh;
+      }
+      s_lo = lif_step(ulo, lo, in.blo[r], in.tlo[r]);
+      s_hi = lif_step(uhi, hi2, in.bhi[r], in.thi[r]);
+    }
+    const uint64_t ml = __ballot(s_lo), mh = __ballot(s_hi);
+    if (hi < NREP + 2 && c == 0) {
+      const int sft = (lane >> 5) * 32;
+      fw[hi] = ((ml >> sft) & 0xffffffffull) | (((mh >> sft) & 0xffffffffull) << 32);
+    }
+  }
+}
+
+// XDT = 0: queries come packed in p.q.  XDT = SPK_BF16 / SPK_F16: the fused
+// path, which derives this unit's q and current k/v spikes from p.fz.
+template <int NREP, int XDT>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT == 0 ? 4 : 3))) void decode_attn_mfma_kernel(AttnParams p) {
   // Unplanned launch: x = (sequence, timestep, kv head) unit, y = partition.
   // Either way consecutive block ids (dealt round-robin to the 8 XCDs) are
   // sibling units of equal length.
@@ -300,6 +389,9 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
   const int start = part * p.part_len;
   const int end = min(len, start + p.part_len);
 
+  FusedIn<XDT == 0 ? SPK_BF16 : XDT> fin;
+  if constexpr (XDT != 0) fused_load<NREP, XDT>(p, n, t, kvh, wave, lane, fin);
+
   __shared__ uint32_t tab[65];                // per d: 4 e4m3 digits of exp(-d*scale)
   __shared__ int32_t blocks[kMaxPartBlocks];  // this partition's physical blocks
   WaveStage &st = reinterpret_cast<WaveStage *>(smem)[wave];
@@ -316,17 +408,21 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
   }
 
   uint32_t q0[8], q1[8];
+  __shared__ uint64_t fw[10];  // fused path: packed spikes of the unit's q heads, then k, v
+  if constexpr (XDT == 0) {
 #pragma unroll
-  for (int h = 0; h < 8; ++h) {
-    q0[h] = q1[h] = 0u;
-    if (h < NREP) {
-      const uint32_t *qp = p.q + t * p.qs0 + n * p.qs1 + (kvh * NREP + h) * p.qs2;
-      q0[h] = qp[0];
-      q1[h] = qp[1];
+    for (int h = 0; h < 8; ++h) {
+      q0[h] = q1[h] = 0u;
+      if (h < NREP) {
+        const uint32_t *qp = p.q + t * p.qs0 + n * p.qs1 + (kvh * NREP + h) * p.qs2;
+        q0[h] = qp[0];
+        q1[h] = qp[1];
+      }
     }
   }
   __syncthreads();
-
+  uint64_t kcur = 0, vcur = 0;  // fused path: the current token's k/v words
+  bool subst = false;            // ... used in place of the loaded ones
   const uint64_t *kbase = reinterpret_cast<const uint64_t *>(p.k + t * p.ks0 + kvh * p.ks1);
   const uint64_t *vbase = reinterpret_cast<const uint64_t *>(p.v + t * p.vs0 + kvh * p.vs1);
   const int bs_mask = (1 << p.bs_log2) - 1;
@@ -355,11 +451,19 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
   const int nfull = span > 0 ? (span / kStride) + ((span % kStride) >= kStepTokens ? 1 : 0) : 0;
   const int ntotal = span > 0 ? (span + kStride - 1) / kStride : 0;
 
-  auto step = [&](const uint64_t (&kw)[2], const uint64_t (&vw)[2], bool masked, int j0) {
+  const int cur_pair = (len - 1) & ~1, cur_e = (len - 1) & 1;
+  auto step = [&](const uint64_t (&kin)[2], const uint64_t (&vin)[2], bool masked, int j0) {
     // Nothing of this step moves ahead of the previous one: left free, the
     // scheduler hoists a later step's popcounts next to its just-issued loads
     // and the wait for them empties the prefetch ring (measured: -3.5 %).
     __builtin_amdgcn_sched_barrier(0);
+    uint64_t kw[2] = {kin[0], kin[1]}, vw[2] = {vin[0], vin[1]};
+    if constexpr (XDT != 0) {  // the current token's words, not yet in the cache
+      if (subst && min(j0 + 2 * lane, last_pair) == cur_pair) {
+        kw[cur_e] = kcur;
+        vw[cur_e] = vcur;
+      }
+    }
     if (!masked) {
       const bool all[2] = {true, true};
       stage_step<NREP, false>(st, lane, kw, vw, all, q0, q1, tab);
@@ -382,21 +486,50 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
     load(first + lo, k0, v0);
     load(first + kStride + lo, k1, v1);
   }
+  // Fused path: the spikes, computed while those first loads are in flight.
+  if constexpr (XDT != 0) {
+    fused_spikes<NREP, XDT>(fin, t, wave, lane, fw);
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+      q0[h] = h < NREP ? static_cast<uint32_t>(fw[h]) : 0u;
+      q1[h] = h < NREP ? static_cast<uint32_t>(fw[h] >> 32) : 0u;
+    }
+    kcur = fw[NREP];
+    vcur = fw[NREP + 1];
+    // The partition holding the current token (position len - 1) stores its
+    // words in the token's cache slot, once per (t, kv head), and uses them
+    // in registers where the block table maps that position to the same slot
+    // (elsewhere it reads the cache, as the two separate launches would).
+    const int cur = len - 1;
+    if (cur >= start && cur < end) {
+      const int64_t slot = p.fz.slots[n];
+      if (slot >= 0 && slot < p.num_slots) {
+        if (tid == 0) {
+          *reinterpret_cast<uint64_t *>(p.fz.k_out + t * p.ks0 + kvh * p.ks1 + slot * p.ks2) = kcur;
+          *reinterpret_cast<uint64_t *>(p.fz.v_out + t * p.vs0 + kvh * p.vs1 + slot * p.vs2) = vcur;
+        }
+        const uint32_t phys = static_cast<uint32_t>(blocks[(cur - start) >> p.bs_log2]);
+        const int64_t tslot = (static_cast<int64_t>(phys) << p.bs_log2) | (cur & ((1 << p.bs_log2) - 1));
+        subst = tslot == slot;
+      }
+    }
+  }
   int i = 0;
   for (; i + 3 <= nfull; i += 3) {
     load(first + (i + 2) * kStride + lo, k2, v2);
-    step(k0, v0, false, 0);
+    step(k0, v0, false, first + i * kStride);
     load(first + (i + 3) * kStride + lo, k0, v0);
-    step(k1, v1, false, 0);
+    step(k1, v1, false, first + (i + 1) * kStride);
     load(first + (i + 4) * kStride + lo, k1, v1);
-    step(k2, v2, false, 0);
+    step(k2, v2, false, first + (i + 2) * kStride);
   }
   if (i < nfull) {
     load(first + (i + 2) * kStride + lo, k2, v2);
-    step(k0, v0, false, 0);
+    step(k0, v0, false, first + i * kStride);
     ++i;
     if (i < nfull) {
-      step(k1, v1, false, 0);
+      step(k1, v1, false, first + i * kStride);
       ++i;
     }
   }
@@ -580,7 +713,7 @@ __global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, in
 
 }  // namespace mfma
 
-void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s) {
+void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s, int fused_dtype) {
   const int threads = mfma::kWaves * 64;
   const int units = p.N * p.T * p.Hkv;
   dim3 grid(units, p.num_parts);
@@ -595,16 +728,25 @@ void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s) 
     p.order = order;
     grid = dim3(units * p.num_parts);
   }
-  switch (p.nrep) {
-    case 1: mfma::decode_attn_mfma_kernel<1><<<grid, threads, 0, s>>>(p); break;
-    case 2: mfma::decode_attn_mfma_kernel<2><<<grid, threads, 0, s>>>(p); break;
-    case 3: mfma::decode_attn_mfma_kernel<3><<<grid, threads, 0, s>>>(p); break;
-    case 4: mfma::decode_attn_mfma_kernel<4><<<grid, threads, 0, s>>>(p); break;
-    case 5: mfma::decode_attn_mfma_kernel<5><<<grid, threads, 0, s>>>(p); break;
-    case 6: mfma::decode_attn_mfma_kernel<6><<<grid, threads, 0, s>>>(p); break;
-    case 7: mfma::decode_attn_mfma_kernel<7><<<grid, threads, 0, s>>>(p); break;
-    default: mfma::decode_attn_mfma_kernel<8><<<grid, threads, 0, s>>>(p); break;
+#define SPK_NREP_CASES(XDT)                                                                   \
+  switch (p.nrep) {                                                                           \
+    case 1: mfma::decode_attn_mfma_kernel<1, XDT><<<grid, threads, 0, s>>>(p); break;         \
+    case 2: mfma::decode_attn_mfma_kernel<2, XDT><<<grid, threads, 0, s>>>(p); break;         \
+    case 3: mfma::decode_attn_mfma_kernel<3, XDT><<<grid, threads, 0, s>>>(p); break;         \
+    case 4: mfma::decode_attn_mfma_kernel<4, XDT><<<grid, threads, 0, s>>>(p); break;         \
+    case 5: mfma::decode_attn_mfma_kernel<5, XDT><<<grid, threads, 0, s>>>(p); break;         \
+    case 6: mfma::decode_attn_mfma_kernel<6, XDT><<<grid, threads, 0, s>>>(p); break;         \
+    case 7: mfma::decode_attn_mfma_kernel<7, XDT><<<grid, threads, 0, s>>>(p); break;         \
+    default: mfma::decode_attn_mfma_kernel<8, XDT><<<grid, threads, 0, s>>>(p); break;        \
   }
+  if (fused_dtype == SPK_BF16) {
+    SPK_NREP_CASES(SPK_BF16)
+  } else if (fused_dtype == SPK_F16) {
+    SPK_NREP_CASES(SPK_F16)
+  } else {
+    SPK_NREP_CASES(0)
+  }
+#undef SPK_NREP_CASES
 }
 
 }  // namespace spk

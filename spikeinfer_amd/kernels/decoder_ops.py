@@ -6,6 +6,8 @@ flattened, paged form ``[T, n_tok, ...]``.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from .. import _lib
@@ -191,6 +193,65 @@ def qkv_rope_lif_pack(
         "qkv_rope_lif_pack",
     )
     return q_packed
+
+
+def qkv_decode_attention(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                         positions: torch.Tensor, beta: torch.Tensor, threshold: torch.Tensor,
+                         k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                         block_tables: torch.Tensor, seq_lens: torch.Tensor, num_q_heads: int,
+                         num_kv_heads: int, block_size: int, out: torch.Tensor,
+                         workspace: torch.Tensor | None = None) -> bool:
+    """Fused decode step of one layer's attention: the q/k/v spikes of the
+    ``N = qkv.shape[1]`` decode tokens (as :func:`qkv_rope_lif_pack`), their
+    k/v words into the cache, and attention into ``out [T, N, Hq, 64]``.
+
+    Returns False, having done nothing, when the shape is outside the fused
+    kernel (head_dim 64, Hq/Hkv <= 8, T <= 8); the caller then runs the two
+    separate operations.
+    """
+    from .spike_attention import decode_attn_workspace_bytes
+
+    dev = _lib.require_gpu(qkv, cos, sin, positions, beta, threshold, k_cache, v_cache, slot_mapping,
+                           block_tables, seq_lens, out, workspace)
+    T, n, C = qkv.shape
+    D = 64
+    if (C != (num_q_heads + 2 * num_kv_heads) * D or num_q_heads % num_kv_heads
+            or num_q_heads // num_kv_heads > 8 or T > 8 or k_cache.shape[-1] != 2):
+        return False
+    if qkv.stride(-1) != 1 or positions.dtype != torch.int64 or not positions.is_contiguous():
+        raise ValueError("qkv needs a contiguous channel axis and positions contiguous int64")
+    if (positions.numel() < n or slot_mapping.numel() < n or seq_lens.numel() < n
+            or block_tables.ndim != 2 or block_tables.shape[0] < n):
+        raise ValueError(f"positions, slot_mapping, seq_lens and block_tables need {n} rows")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.ndim != 2 or t.shape[1] != D or not t.is_contiguous() or t.dtype != qkv.dtype:
+            raise ValueError(f"{name} must be a contiguous [rows, {D}] {qkv.dtype} table")
+    if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+        raise ValueError("k and v caches must have the same shape and strides")
+    if tuple(out.shape) != (T, n, num_q_heads, D):
+        raise ValueError(f"out must be [{T}, {n}, {num_q_heads}, {D}]")
+    beta = beta.reshape(3, D).contiguous()
+    threshold = threshold.reshape(3, D).to(beta.dtype).contiguous()
+    slot_mapping = slot_mapping.to(torch.int64).contiguous()
+    block_tables = block_tables.to(torch.int32)
+    seq_lens = seq_lens.to(torch.int32).contiguous()
+    max_blocks = block_tables.shape[1]
+    need = decode_attn_workspace_bytes(T, n, num_q_heads, num_kv_heads, D, block_size, max_blocks)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    rc = _lib.load().spk_qkv_decode_attn(
+        qkv.data_ptr(), _lib.dtype_code(qkv.dtype), (_lib.ctypes.c_int64 * 2)(*qkv.stride()[:2]),
+        cos.data_ptr(), sin.data_ptr(), positions.data_ptr(), cos.shape[0], beta.data_ptr(),
+        threshold.data_ptr(), _lib.dtype_code(beta.dtype), slot_mapping.data_ptr(),
+        k_cache.data_ptr(), v_cache.data_ptr(), _lib.strides(k_cache), k_cache.shape[2],
+        block_tables.data_ptr(), block_tables.stride(0), block_tables.stride(1), seq_lens.data_ptr(),
+        out.data_ptr(), _lib.dtype_code(out.dtype), _lib.strides(out), T, n, num_q_heads,
+        num_kv_heads, D, block_size, max_blocks, 1.0 / math.sqrt(D),
+        _lib.ptr(workspace) if need else None, need, _lib.stream_of(dev))
+    if rc == _lib.SPK_EUNSUPPORTED:
+        return False
+    _lib.check(rc, "qkv_decode_attention")
+    return True
 
 
 def lif_gate_mul(gate_up: torch.Tensor, beta: torch.Tensor, threshold: torch.Tensor,

@@ -27,8 +27,8 @@ import torch
 import torch.nn.functional as F
 
 from .attention import AttentionMetadata
-from .kernels.decoder_ops import (add_rmsnorm, embed_rmsnorm, lif_gate_mul, qkv_rope_lif_pack,
-                                  rmsnorm_mean_t)
+from .kernels.decoder_ops import (add_rmsnorm, embed_rmsnorm, lif_gate_mul, qkv_decode_attention,
+                                  qkv_rope_lif_pack, rmsnorm_mean_t)
 from .kernels.packing import packed_width
 from .kernels.spike_attention import gather_kv_unpacked, paged_spike_attn_decode
 
@@ -98,6 +98,9 @@ class SpikingDecoder:
             L.lif_gate_th = const(c.threshold_init, I)
             L.w_down = normal(H, I)
             self.layers.append(L)
+        # Decode-only batches run q/k/v spikes and attention as one launch
+        # (qkv_decode_attention); False keeps the two launches (same results).
+        self.fused_attention = True
         # Rotary inverse frequencies as Qwen2RotaryEmbedding builds them (fp32, host).
         exps = torch.arange(0, self.D, 2, dtype=torch.int64).float() / self.D
         self.inv_freq = (1.0 / (c.rope_theta ** exps)).to(self.device)
@@ -182,10 +185,16 @@ class SpikingDecoder:
                 x = add_rmsnorm(h, delta, L.input_norm, c.rms_norm_eps, out=x)
             k_cache, v_cache = kv_caches[i]
             qkv = F.linear(x, L.w_qkv, L.b_qkv)
-            qkv_rope_lif_pack(qkv, self.rope_cos, self.rope_sin, L.lif_qkv_beta, L.lif_qkv_th, k_cache,
-                              v_cache, meta.slot_mapping, Hq, Hkv, D, q_packed=q_packed, n_q=n_dec,
-                              dense=dense, positions=positions)
-            if n_dec:
+            fused = (self.fused_attention and not meta.num_prefills and n_dec == n and
+                     qkv_decode_attention(qkv, self.rope_cos, self.rope_sin, positions, L.lif_qkv_beta,
+                                          L.lif_qkv_th, k_cache, v_cache, meta.slot_mapping,
+                                          meta.block_tables, meta.seq_lens, Hq, Hkv, meta.block_size,
+                                          attn))
+            if not fused:
+                qkv_rope_lif_pack(qkv, self.rope_cos, self.rope_sin, L.lif_qkv_beta, L.lif_qkv_th,
+                                  k_cache, v_cache, meta.slot_mapping, Hq, Hkv, D, q_packed=q_packed,
+                                  n_q=n_dec, dense=dense, positions=positions)
+            if n_dec and not fused:
                 paged_spike_attn_decode(q_packed, k_cache, v_cache, meta.block_tables, meta.seq_lens,
                                         head_dim=D, block_size=meta.block_size, num_q_heads=Hq,
                                         num_kv_heads=Hkv, out=attn[:, :n_dec])

@@ -140,6 +140,87 @@ def test_qkv_rope_lif_pack_bit_exact(gpu, D, Hq, Hkv, n, dtype, tables):
         assert torch.equal(got, want.transpose(1, 2))
 
 
+@pytest.mark.parametrize("Hq,Hkv,dtype", [(14, 2, torch.bfloat16), (4, 2, torch.bfloat16),
+                                          (14, 2, torch.float16)])
+def test_qkv_decode_attention_matches_two_launches(gpu, Hq, Hkv, dtype):
+    """The fused launch gives the same attention output and the same cache
+    bytes as qkv_rope_lif_pack + paged_spike_attn_decode, bit for bit: ragged
+    lengths (one long enough to split into partitions), a pad row whose slot
+    lies outside the cache, 7:1 and 2:1 GQA."""
+    from spikeinfer_amd.kernels import paged_spike_attn_decode
+    from spikeinfer_amd.kernels.decoder_ops import qkv_decode_attention
+
+    T, D, bs = 4, 64, 16
+    g = torch.Generator(device=gpu).manual_seed(Hq * 7 + (dtype == torch.float16))
+    lens = torch.randint(1, 300, (37,), generator=g, device=gpu).to(torch.int32)
+    lens[5] = 9001
+    n = lens.numel()
+    max_blocks = (int(lens.max()) + bs - 1) // bs
+    used = int(((lens + bs - 1) // bs).sum())
+    num_blocks = used + 2
+    perm = torch.randperm(num_blocks - 1, generator=g, device=gpu).to(torch.int32)
+    tables = torch.full((n, max_blocks), num_blocks - 1, dtype=torch.int32, device=gpu)
+    cur = 0
+    for i, L in enumerate(lens.tolist()):
+        nb = (L + bs - 1) // bs
+        tables[i, :nb] = perm[cur:cur + nb]
+        cur += nb
+    pos = (lens - 1).to(torch.int64)
+    slots = (tables[torch.arange(n, device=gpu), (pos // bs)].to(torch.int64) * bs + pos % bs)
+    slots[9] = num_blocks * bs + 5  # outside the cache: not written
+    words = torch.randint(-2**31, 2**31, (2, T, Hkv, num_blocks * bs, 2), generator=g, device=gpu,
+                          dtype=torch.int64).to(torch.int32)
+    qkv = (torch.randn((T, n, (Hq + 2 * Hkv) * D), generator=g, device=gpu) * 1.5 + 0.3).to(dtype)
+    beta = (0.6 + 0.4 * torch.rand((3, D), generator=g, device=gpu)).to(dtype)
+    th = (0.5 + torch.rand((3, D), generator=g, device=gpu)).to(dtype)
+    cos, sin = _rope_tables(torch.arange(10000, device=gpu), D, dtype)
+
+    ka, va = words[0].clone(), words[1].clone()
+    qp = torch.empty((T, n, Hq, 2), dtype=torch.int32, device=gpu)
+    qkv_rope_lif_pack(qkv, cos, sin, beta, th, ka, va, slots, Hq, Hkv, D, q_packed=qp, n_q=n,
+                      positions=pos)
+    out_a = paged_spike_attn_decode(qp, ka, va, tables, lens, D, bs, Hq, Hkv, dtype=dtype)
+
+    kb, vb = words[0].clone(), words[1].clone()
+    out_b = torch.empty_like(out_a)
+    assert qkv_decode_attention(qkv, cos, sin, pos, beta, th, kb, vb, slots, tables, lens, Hq, Hkv,
+                                bs, out_b)
+    torch.cuda.synchronize()
+    assert torch.equal(ka, kb) and torch.equal(va, vb)
+    assert torch.equal(out_a, out_b)
+
+
+def test_model_fused_attention_is_identical(gpu):
+    """A decode step of the model with the fused q/k/v + attention launch
+    equals the step with the two separate launches."""
+    m = _small_model(gpu, seed=21)
+    bs, n = 16, 6
+    g = torch.Generator().manual_seed(4)
+    lens = torch.randint(5, 60, (n,), generator=g)
+    tables = torch.randperm(64, generator=g)[: n * 4].view(n, 4).to(torch.int32)
+    pos = (lens - 1).to(torch.int64)
+    slots = tables[torch.arange(n), pos // bs].to(torch.int64) * bs + pos % bs
+    meta = AttentionMetadata(slot_mapping=slots.to(gpu), block_size=bs, num_decode_tokens=n,
+                             block_tables=tables.to(gpu), seq_lens=lens.to(torch.int32).to(gpu))
+    ids = torch.randint(0, 1024, (n,), generator=g).to(gpu)
+    caches = [PagedSpikeCache(2, m.T, m.Hkv, m.D, 65, bs, device=gpu) for _ in range(2)]
+    for c in caches:
+        for k, v in c.layers:
+            k.random_(-2**31, 2**31 - 1)
+        for (k0, v0), (k1, v1) in zip(caches[0].layers, caches[1].layers):
+            k1.copy_(k0)
+            v1.copy_(v0)
+    outs = []
+    for fused, c in zip((True, False), caches):
+        m.fused_attention = fused
+        outs.append(m.forward_paged(ids, pos.to(gpu), c.layers, meta))
+    m.fused_attention = True
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    for (k0, v0), (k1, v1) in zip(caches[0].layers, caches[1].layers):
+        assert torch.equal(k0, k1) and torch.equal(v0, v1)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_lif_gate_mul_bit_exact(gpu, dtype):
     """Per-channel parameters in the activation dtype (so every 16-bit lane
