@@ -43,6 +43,7 @@ constexpr float kGreedyTemp = 1e-5f;
 constexpr double kMassScale = 1099511627776.0;  // 2^40
 
 constexpr int kCand = 8192;  // LDS candidate capacity (the fast path)
+constexpr int kNoCutCand = 4096;  // without a top-k cut: about 1.5x this many candidates (the margin below)
 
 struct Params {
   float temp, min_p, top_p, rep, presence, frequency;
@@ -395,10 +396,15 @@ __device__ __forceinline__ unsigned long long mass_if(const Src &src, Shared &sh
 // min_p -> top_k -> top_p -> draw over a source; returns the token.  `Z_all`
 // (when have_Z) is the alive mass of the whole row, used when the source is a
 // candidate subset and no top-k cut bounds the survivors inside it.
+// `partial`: src holds only a prefix of the order (the candidates), no top-k
+// was requested, and Z_all is the mass of every element min_p keeps in the
+// whole row.  A top-p cut or a draw that falls beyond the prefix then returns
+// -1 (the caller takes the whole row) instead of being decided on the prefix.
 template <class Src>
 __device__ __forceinline__ int64_t filter_and_draw(const Src src, Shared &sh, const Params P,
                                                    float m, long long k_req, bool have_Z,
-                                                   unsigned long long Z_all, float u) {
+                                                   unsigned long long Z_all, float u,
+                                                   bool partial = false) {
   auto alive = [&](float x) { return P.min_p <= 0.f || expf(x - m) >= P.min_p; };
   constexpr int kAll = 0x7fffffff;
 
@@ -442,6 +448,8 @@ __device__ __forceinline__ int64_t filter_and_draw(const Src src, Shared &sh, co
       const unsigned long long c = count_if(src, sh, tie);
       Kf = K;
       If = j >= c ? kAll : index_rank(src, sh, j, tie);
+    } else if (partial) {
+      return -1;  // the cut lies past the prefix
     }
   }
   auto kept = [&](int i, float x) {
@@ -451,13 +459,17 @@ __device__ __forceinline__ int64_t filter_and_draw(const Src src, Shared &sh, co
 
   // Draw: the element whose interval of the kept mass, accumulated in the same
   // order (key descending, index ascending), holds u * total.
-  const unsigned long long Wtot = mass_if(src, sh, m, kept);
+  // Kept mass: over src, except for a prefix with nothing cut (then the whole
+  // row's min_p survivors).
+  const bool whole = partial && !(P.top_p < 1.f);
+  const unsigned long long Wtot = whole ? Z_all : mass_if(src, sh, m, kept);
   unsigned long long T = static_cast<unsigned long long>(static_cast<double>(u) * static_cast<double>(Wtot));
   if (T >= Wtot) T = Wtot ? Wtot - 1 : 0;
   uint32_t K;
   unsigned long long above;
   if (!mass_select(src, sh, kept, m, static_cast<double>(T) + 1.0, 0u, 0ull, K, above)) {
-    // Unreachable: the largest kept element always weighs 2^40.
+    if (whole) return -1;  // the draw lies past the prefix
+    // Unreachable otherwise: the largest kept element always weighs 2^40.
     return static_cast<int64_t>(index_rank(src, sh, 1, kept));
   }
   const unsigned long long w = mass_of(unkey(K), m);
@@ -541,10 +553,10 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
   const float u = uniforms ? uniforms[row] : 0.f;
 
   // ---- pass A (on the penalised logits v; x = v / temperature preserves
-  // their order): max, and (for a top-k cut) every 32nd value as a sample ----
+  // their order): max, and every 32nd value as a sample ----
   const bool has_hist = nh > 0;
   float mv = -INFINITY;
-  const bool sample = k_req > 0;
+  const bool sample = true;  // the candidate bound comes from these samples
   g.each_pen([&](int i, float v) {
     mv = fmaxf(mv, v);
     if (sample && (i % kSampleStride) == 0) sh.cx[i / kSampleStride] = v;
@@ -552,18 +564,24 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
   mv = block_max(mv, sh);
   const float m = mv / P.temp;  // the largest x
 
-  // ---- candidates: with a top-k cut, the elements at or above the r-th
-  // largest sample, r a margin above k / kSampleStride.  If they number at
-  // least k and fit in LDS, the k largest (alive or not) are among them, and
-  // so is everything any later cut keeps.  Otherwise, and without a top-k
-  // cut, the row itself is the source.  The bound is taken 64 key steps low:
-  // an element just under it in v may round to the same x as one above it.
+  // ---- candidates: the elements at or above a bound L, a prefix of the
+  // order, gathered into LDS.  L is taken from the samples: with a top-k cut,
+  // the r-th largest sample, r a margin above k / kSampleStride, so that when
+  // the candidates number at least k and fit in LDS the k largest (alive or
+  // not) are among them, and so is everything any later cut keeps.  Without a
+  // top-k cut, about kNoCutCand candidates; the same sweep then sums the mass
+  // of every min_p survivor of the row, and the candidates decide the row
+  // whenever the top-p cut and the draw fall inside them.  Otherwise the row
+  // itself is the source.  The bound is taken 64 key steps low: an element
+  // just under it in v may round to the same x as one above it.
   int64_t tok = -1;
-  if (k_req > 0) {
+  unsigned long long Z_alive = 0;
+  {
     SampleSrc smp_src;
     smp_src.sh = &sh;
     smp_src.n = (V + kSampleStride - 1) / kSampleStride;
-    const long long kk = (k_req + kSampleStride - 1) / kSampleStride;
+    const long long kk = k_req > 0 ? (k_req + kSampleStride - 1) / kSampleStride
+                                   : kNoCutCand / kSampleStride;
     const long long r = min<long long>(smp_src.n, kk + (kk + 1) / 2 + 8);
     unsigned long long above;
     const uint32_t Ls =
@@ -573,7 +591,13 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
     __syncthreads();
     if (tid == 0) sh.bcast[3] = 0;
     __syncthreads();
+    const bool sum_alive = k_req <= 0;
+    unsigned long long z = 0;
     g.each_pen([&](int i, float v) {
+      if (sum_alive) {
+        const float x = v / P.temp;
+        if (P.min_p <= 0.f || expf(x - m) >= P.min_p) z += mass_of(x, m);
+      }
       if (fkey(v) < L) return;
       const unsigned long long o = atomicAdd(&sh.bcast[3], 1ull);
       if (o < static_cast<unsigned long long>(kCand)) {
@@ -583,14 +607,17 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
     }, has_hist);
     __syncthreads();
     const unsigned long long n_c = sh.bcast[3];
-    if (n_c <= static_cast<unsigned long long>(kCand) && n_c >= static_cast<unsigned long long>(k_req)) {
+    if (sum_alive) block_exclusive_scan(z, sh, &Z_alive);
+    if (n_c <= static_cast<unsigned long long>(kCand) &&
+        n_c >= static_cast<unsigned long long>(k_req > 0 ? k_req : 1)) {
       CandSrc cs;
       cs.sh = &sh;
       cs.n = static_cast<int>(n_c);
-      tok = filter_and_draw(cs, sh, P, m, k_req, false, 0, u);
+      tok = k_req > 0 ? filter_and_draw(cs, sh, P, m, k_req, false, 0, u)
+                      : filter_and_draw(cs, sh, P, m, k_req, true, Z_alive, u, true);
     }
   }
-  if (tok < 0) tok = filter_and_draw(g, sh, P, m, k_req, false, 0, u);
+  if (tok < 0) tok = filter_and_draw(g, sh, P, m, k_req, k_req <= 0, Z_alive, u);
   if (tid == 0) out[row] = tok;
 }
 
