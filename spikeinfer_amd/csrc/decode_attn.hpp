@@ -12,6 +12,7 @@ constexpr int kAttnThreads = 256;   // 4 waves
 constexpr int kMaxStagedBlocks = 2048;
 constexpr int kMaxRep = 16;
 constexpr int kMaxFusedT = 8;  // timesteps the fused q/k/v path keeps in registers
+constexpr int kDigitEntries = 129;  // d = 0..128 (head_dim 64 or 128)
 
 // Inputs of the fused q/k/v-spike path (spk_qkv_decode_attn): the q/k/v
 // projection currents of the decode tokens, from which each workgroup derives
@@ -55,15 +56,16 @@ struct AttnParams {
   // Matrix-core path: the main kernel computes the longest-first order itself
   // (N * num_parts <= kInlinePlanItems) instead of reading `order`.
   int plan_inline;
-  // Matrix-core path: for d = popc(q & ~k) in 0..64, the four e4m3 digits of
-  // exp(-d*scale) * 2^8 (byte s weighs 2^-(4s)), built on the host once per
-  // scale (build_digit_table) and copied into LDS by every workgroup.
-  uint32_t digits[65];
+  // Matrix-core path: for d = popc(q & ~k) in 0..head_dim (<= 128), the four
+  // e4m3 digits of exp(-d*scale) * 2^8 (byte s weighs 2^-(4s)), built on the
+  // host once per scale (build_digit_table) and copied into LDS by every
+  // workgroup.
+  uint32_t digits[kDigitEntries];
   FusedParams fz;  // used by the fused instantiations only
 };
 
-// Fills digits[] for `scale` (host; reuses the last table when unchanged).
-void build_digit_table(float scale, uint32_t digits[65]);
+// Fills digits[0..128] for `scale` (host; reuses the last table when unchanged).
+void build_digit_table(float scale, uint32_t digits[kDigitEntries]);
 
 // Partition length: long contexts are split so the grid has enough
 // workgroups and no single workgroup walks a 32k-token context alone.

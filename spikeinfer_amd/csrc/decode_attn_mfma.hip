@@ -15,7 +15,7 @@
 //             4(h-4rt)+s holds, per token, digit s of the weight
 //             w(d) = exp(-d*scale), d = popc(q_h & ~k).  The weight is split
 //             into four e4m3 digits, w = sum_s q_s * 2^-(8+4s) (relative error
-//             <= ~1e-6), looked up in a 65-entry LDS table (built once per
+//             <= ~1e-6), looked up in a 129-entry LDS table (built once per
 //             scale on the host, passed in the arguments).
 //   B cols  = 16 channels 4c+ts (c < 16) of channel tile ts; element = fp4
 //             with the v bit in place (0.5, 1.0 or 2.0 per set bit); a fifth,
@@ -60,15 +60,20 @@ constexpr int kMaxPartBlocks = kMaxStagedBlocks;  // block-table entries staged 
 // staging write and transpose read touches consecutive 8/16-byte chunks (no
 // LDS bank conflicts).  Digit rows are 32 bytes (byte 4h+s = digit s of head
 // h), stored as two 16-byte windows: a[w][r] = bytes 16w..16w+15 of row r.
+// W64 = head_dim / 64 v words per token, v[w][r] = word w of row r.
+template <int W64>
 struct alignas(16) WaveStage {
-  uint64_t v[kStepTokens];            // v word of each row                  (1 KB)
+  uint64_t v[W64][kStepTokens];       // v words of each row            (1 KB each)
   uint4 a[2][kStepTokens];            // digit rows, window-major            (4 KB)
 };
 
-constexpr int kReduceFloats = (kWaves - 1) * 64 * 10;  // 8 values + 2 l per lane
-constexpr int kSmemBytes =
-    (kWaves * (int)sizeof(WaveStage) > kReduceFloats * 4) ? kWaves * (int)sizeof(WaveStage)
-                                                            : kReduceFloats * 4;
+// Cross-wave reduction: 8 * W64 values + 2 denominators per lane.
+template <int W64>
+constexpr int kReduceFloats = (kWaves - 1) * 64 * (8 * W64 + 2);
+template <int W64>
+constexpr int kSmemBytes = (kWaves * (int)sizeof(WaveStage<W64>) > kReduceFloats<W64> * 4)
+                               ? kWaves * (int)sizeof(WaveStage<W64>)
+                               : kReduceFloats<W64> * 4;
 
 __device__ __forceinline__ v2i tr_b4(const SPK_LDS char *p) {
   return __builtin_amdgcn_ds_read_tr4_b64_v2i32((SPK_LDS v2i *)p);
@@ -86,16 +91,32 @@ __device__ __forceinline__ uint32_t popc2(uint32_t a, uint32_t b) {
   return d;
 }
 
+// popc(a) + acc, the same accumulate form.
+__device__ __forceinline__ uint32_t bcnt_add(uint32_t a, uint32_t acc) {
+  uint32_t d;
+  asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(acc));
+  return d;
+}
+
 // Digit words of one token for the NREP heads; zero when masked off.
-template <int NREP, bool MASKED>
-__device__ __forceinline__ void token_digits(uint64_t kw, bool valid, const uint32_t (&q0)[8],
-                                             const uint32_t (&q1)[8], const uint32_t *tab,
+// q[w][h] = 32-bit word w of head h's packed query.
+template <int NREP, int W64, bool MASKED>
+__device__ __forceinline__ void token_digits(const uint64_t (&kw)[W64], bool valid,
+                                             const uint32_t (&q)[2 * W64][8], const uint32_t *tab,
                                              uint32_t (&dig)[8]) {
-  const uint32_t klo = static_cast<uint32_t>(kw), khi = static_cast<uint32_t>(kw >> 32);
+  uint32_t kn[2 * W64];
+#pragma unroll
+  for (int w = 0; w < W64; ++w) {
+    kn[2 * w] = ~static_cast<uint32_t>(kw[w]);
+    kn[2 * w + 1] = ~static_cast<uint32_t>(kw[w] >> 32);
+  }
 #pragma unroll
   for (int h = 0; h < 8; ++h) {
     if (h < NREP) {
-      dig[h] = (!MASKED || valid) ? tab[popc2(q0[h] & ~klo, q1[h] & ~khi)] : 0u;
+      uint32_t d = popc2(q[0][h] & kn[0], q[1][h] & kn[1]);
+#pragma unroll
+      for (int w = 2; w < 2 * W64; ++w) d = bcnt_add(q[w][h] & kn[w], d);
+      dig[h] = (!MASKED || valid) ? tab[d] : 0u;
     } else {
       dig[h] = 0u;
     }
@@ -105,20 +126,20 @@ __device__ __forceinline__ void token_digits(uint64_t kw, bool valid, const uint
 // Stages one 128-token step of a wave (lane l holds tokens 2l and 2l+1,
 // staged as rows l and l+64):
 // weight digits and v words into the wave's LDS stage.
-template <int NREP, bool MASKED>
-__device__ __forceinline__ void stage_step(WaveStage &st, int lane, const uint64_t (&kw)[2],
-                                           const uint64_t (&vw)[2], const bool (&valid)[2],
-                                           const uint32_t (&q0)[8], const uint32_t (&q1)[8],
-                                           const uint32_t *tab) {
+template <int NREP, int W64, bool MASKED>
+__device__ __forceinline__ void stage_step(WaveStage<W64> &st, int lane,
+                                           const uint64_t (&kw)[2][W64],
+                                           const uint64_t (&vw)[2][W64], const bool (&valid)[2],
+                                           const uint32_t (&q)[2 * W64][8], const uint32_t *tab) {
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     uint32_t dig[8];
-    token_digits<NREP, MASKED>(kw[e], valid[e], q0, q1, tab, dig);
+    token_digits<NREP, W64, MASKED>(kw[e], valid[e], q, tab, dig);
     const int row = lane + 64 * e;
     st.a[0][row] = make_uint4(dig[0], dig[1], dig[2], dig[3]);
     if (NREP > 4) st.a[1][row] = make_uint4(dig[4], dig[5], dig[6], dig[7]);
-    const uint64_t v = (!MASKED || valid[e]) ? vw[e] : 0ull;
-    st.v[row] = v;
+#pragma unroll
+    for (int w = 0; w < W64; ++w) st.v[w][row] = (!MASKED || valid[e]) ? vw[e][w] : 0ull;
   }
 }
 
@@ -142,16 +163,13 @@ __device__ __forceinline__ void wave_sync() {
 //     16p.. and 64+16p..); bit s of each nibble is kept in place for s < 3
 //     (fp4 0.5, 1.0, 2.0) and shifted to bit 2 for s = 3 (2.0);
 //   the all-ones B tile accumulates the softmax denominators.
-template <int RT>  // row tiles: heads 4rt..4rt+3 for rt < RT
-__device__ __forceinline__ void contract_step(const WaveStage &st, int lane, v4f (&acc)[2][4],
-                                              v4f (&accl)[2]) {
+// With W64 = 2 the channel tiles of v word hv are acc[rt][4*hv + s]
+// (channel 64*hv + 4*(l%16) + s); the A operand is shared.
+template <int RT, int W64>  // row tiles: heads 4rt..4rt+3 for rt < RT
+__device__ __forceinline__ void contract_step(const WaveStage<W64> &st, int lane,
+                                              v4f (&acc)[2][4 * W64], v4f (&accl)[2]) {
   const int q = lane >> 4;
   const int i16 = lane & 15;
-  const SPK_LDS char *lds_v = (const SPK_LDS char *)st.v;
-  const v2i w0 = tr_b4(lds_v + (16 * q + i16) * 8);
-  const v2i w1 = tr_b4(lds_v + (64 + 16 * q + i16) * 8);
-  const uint32_t w[4] = {static_cast<uint32_t>(w0.x), static_cast<uint32_t>(w0.y),
-                         static_cast<uint32_t>(w1.x), static_cast<uint32_t>(w1.y)};
   const int r0 = ((q & 1) ? 64 : 0) + 16 * (q >> 1);  // rows of A bytes 0..15; +32 for 16..31
   const int sub = (i16 >> 1) & 7, hb = (i16 & 1) * 8;
   v8i A[2];
@@ -168,13 +186,22 @@ __device__ __forceinline__ void contract_step(const WaveStage &st, int lane, v4f
   }
   constexpr uint32_t kMask[4] = {0x11111111u, 0x22222222u, 0x44444444u, 0x44444444u};
 #pragma unroll
-  for (int ts = 0; ts < 4; ++ts) {
-    v8i B = {};
+  for (int hv = 0; hv < W64; ++hv) {
+    const SPK_LDS char *lds_v = (const SPK_LDS char *)st.v[hv];
+    const v2i w0 = tr_b4(lds_v + (16 * q + i16) * 8);
+    const v2i w1 = tr_b4(lds_v + (64 + 16 * q + i16) * 8);
+    const uint32_t w[4] = {static_cast<uint32_t>(w0.x), static_cast<uint32_t>(w0.y),
+                           static_cast<uint32_t>(w1.x), static_cast<uint32_t>(w1.y)};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) B[i] = static_cast<int>((ts == 3 ? w[i] >> 1 : w[i]) & kMask[ts]);
+    for (int ts = 0; ts < 4; ++ts) {
+      v8i B = {};
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-      acc[rt][ts] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[rt], B, acc[rt][ts], 0, 4, 0, 127, 0, 127);
+      for (int i = 0; i < 4; ++i) B[i] = static_cast<int>((ts == 3 ? w[i] >> 1 : w[i]) & kMask[ts]);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+        acc[rt][4 * hv + ts] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            A[rt], B, acc[rt][4 * hv + ts], 0, 4, 0, 127, 0, 127);
+    }
   }
   const v8i Bl = {0x11111111, 0x11111111, 0x11111111, 0x11111111, 0, 0, 0, 0};
 #pragma unroll
@@ -354,15 +381,17 @@ __device__ __forceinline__ void fused_spikes(const FusedIn<XDT> &in, int t, int 
 }
 
 // XDT = 0: queries come packed in p.q.  XDT = SPK_BF16 / SPK_F16: the fused
-// path, which derives this unit's q and current k/v spikes from p.fz.
-template <int NREP, int XDT>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT == 0 ? 4 : 3))) void decode_attn_mfma_kernel(AttnParams p) {
+// path, which derives this unit's q and current k/v spikes from p.fz
+// (head_dim 64 only).  W64 = head_dim / 64 (1 or 2).
+template <int NREP, int XDT, int W64>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(W64 == 2 ? (NREP > 4 ? 2 : 3) : (XDT == 0 ? 4 : 3)))) void decode_attn_mfma_kernel(AttnParams p) {
+  static_assert(W64 == 1 || (W64 == 2 && XDT == 0), "fused path: head_dim 64 only");
   // Unplanned launch: x = (sequence, timestep, kv head) unit, y = partition.
   // Either way consecutive block ids (dealt round-robin to the 8 XCDs) are
   // sibling units of equal length.
   const int units = p.N * p.T * p.Hkv;
   int unit = blockIdx.x, part = blockIdx.y;
-  __shared__ __align__(16) char smem[kSmemBytes];
+  __shared__ __align__(16) char smem[kSmemBytes<W64>];
   if (p.plan_inline) {  // planned launch: longest work items first
     const int ups = p.T * p.Hkv;
     const int i = plan_slot(p, (int)blockIdx.x / ups, reinterpret_cast<int *>(smem));
@@ -392,11 +421,11 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT
   FusedIn<XDT == 0 ? SPK_BF16 : XDT> fin;
   if constexpr (XDT != 0) fused_load<NREP, XDT>(p, n, t, kvh, wave, lane, fin);
 
-  __shared__ uint32_t tab[65];                // per d: 4 e4m3 digits of exp(-d*scale)
+  __shared__ uint32_t tab[kDigitEntries];     // per d: 4 e4m3 digits of exp(-d*scale)
   __shared__ int32_t blocks[kMaxPartBlocks];  // this partition's physical blocks
-  WaveStage &st = reinterpret_cast<WaveStage *>(smem)[wave];
+  WaveStage<W64> &st = reinterpret_cast<WaveStage<W64> *>(smem)[wave];
 
-  if (tid <= 64) tab[tid] = p.digits[tid];
+  if (tid <= 64 * W64) tab[tid] = p.digits[tid];
   const int nblk = end > start ? ((end - start - 1) >> p.bs_log2) + 1 : 0;
   const int blk0 = start >> p.bs_log2;
   // Physical blocks outside the cache are replaced by block 0 here, once, so
@@ -407,17 +436,14 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT
     blocks[b] = static_cast<int32_t>(phys < num_blocks ? phys : 0u);
   }
 
-  uint32_t q0[8], q1[8];
+  uint32_t q[2 * W64][8];  // q[w][h]: 32-bit word w of head h's packed query
   __shared__ uint64_t fw[10];  // fused path: packed spikes of the unit's q heads, then k, v
   if constexpr (XDT == 0) {
 #pragma unroll
     for (int h = 0; h < 8; ++h) {
-      q0[h] = q1[h] = 0u;
-      if (h < NREP) {
-        const uint32_t *qp = p.q + t * p.qs0 + n * p.qs1 + (kvh * NREP + h) * p.qs2;
-        q0[h] = qp[0];
-        q1[h] = qp[1];
-      }
+      const uint32_t *qp = p.q + t * p.qs0 + n * p.qs1 + (kvh * NREP + h) * p.qs2;
+#pragma unroll
+      for (int w = 0; w < 2 * W64; ++w) q[w][h] = h < NREP ? qp[w] : 0u;
     }
   }
   __syncthreads();
@@ -428,22 +454,30 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT
   const int bs_mask = (1 << p.bs_log2) - 1;
 
   // Tokens j, j+1 of this partition (j even, same block as block_size >= 2)
-  // -> their K/V words, one 16-byte load each.  Pairs past the partition
-  // re-read its last pair (clamped) so the loads stay unconditional; the
-  // staged block ids are inside the cache, so every slot is.
+  // -> their K/V words, W64 16-byte loads each (the pair's 16 * W64 bytes are
+  // contiguous).  Pairs past the partition re-read its last pair (clamped) so
+  // the loads stay unconditional; the staged block ids are inside the cache,
+  // so every slot is.
   const int last_pair = (end - 1) & ~1;
-  auto load = [&](int j, uint64_t (&kw)[2], uint64_t (&vw)[2]) {
+  auto load = [&](int j, uint64_t (&kw)[2][W64], uint64_t (&vw)[2][W64]) {
     const int jj = min(j, last_pair);
     const uint32_t phys = static_cast<uint32_t>(blocks[(jj - start) >> p.bs_log2]);
     const uint64_t slot = (static_cast<uint64_t>(phys) << p.bs_log2) | static_cast<uint64_t>(jj & bs_mask);
     typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
-    const v2u64 k2 = __builtin_nontemporal_load(reinterpret_cast<const v2u64 *>(kbase + slot));
-    const v2u64 v2 = __builtin_nontemporal_load(reinterpret_cast<const v2u64 *>(vbase + slot));
-    kw[0] = k2.x; kw[1] = k2.y;
-    vw[0] = v2.x; vw[1] = v2.y;
+    const v2u64 *kp = reinterpret_cast<const v2u64 *>(kbase + slot * W64);
+    const v2u64 *vp = reinterpret_cast<const v2u64 *>(vbase + slot * W64);
+#pragma unroll
+    for (int i = 0; i < W64; ++i) {  // u64 2i, 2i+1 of the pair: token (2i+c)/W64, word (2i+c)%W64
+      const v2u64 k2 = __builtin_nontemporal_load(kp + i);
+      const v2u64 v2 = __builtin_nontemporal_load(vp + i);
+      kw[(2 * i) / W64][(2 * i) % W64] = k2.x;
+      kw[(2 * i + 1) / W64][(2 * i + 1) % W64] = k2.y;
+      vw[(2 * i) / W64][(2 * i) % W64] = v2.x;
+      vw[(2 * i + 1) / W64][(2 * i + 1) % W64] = v2.y;
+    }
   };
 
-  v4f acc[2][4] = {}, accl[2] = {};
+  v4f acc[2][4 * W64] = {}, accl[2] = {};
 
   constexpr int kStride = kWaves * kStepTokens;
   const int first = start + wave * kStepTokens;
@@ -452,33 +486,40 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT
   const int ntotal = span > 0 ? (span + kStride - 1) / kStride : 0;
 
   const int cur_pair = (len - 1) & ~1, cur_e = (len - 1) & 1;
-  auto step = [&](const uint64_t (&kin)[2], const uint64_t (&vin)[2], bool masked, int j0) {
+  auto step = [&](const uint64_t (&kin)[2][W64], const uint64_t (&vin)[2][W64], bool masked, int j0) {
     // Nothing of this step moves ahead of the previous one: left free, the
     // scheduler hoists a later step's popcounts next to its just-issued loads
     // and the wait for them empties the prefetch ring (measured: -3.5 %).
     __builtin_amdgcn_sched_barrier(0);
-    uint64_t kw[2] = {kin[0], kin[1]}, vw[2] = {vin[0], vin[1]};
+    uint64_t kw[2][W64], vw[2][W64];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int w = 0; w < W64; ++w) {
+        kw[e][w] = kin[e][w];
+        vw[e][w] = vin[e][w];
+      }
     if constexpr (XDT != 0) {  // the current token's words, not yet in the cache
       if (subst && min(j0 + 2 * lane, last_pair) == cur_pair) {
-        kw[cur_e] = kcur;
-        vw[cur_e] = vcur;
+        kw[cur_e][0] = kcur;
+        vw[cur_e][0] = vcur;
       }
     }
     if (!masked) {
       const bool all[2] = {true, true};
-      stage_step<NREP, false>(st, lane, kw, vw, all, q0, q1, tab);
+      stage_step<NREP, W64, false>(st, lane, kw, vw, all, q, tab);
     } else {
       const bool valid[2] = {j0 + 2 * lane < end, j0 + 2 * lane + 1 < end};
-      stage_step<NREP, true>(st, lane, kw, vw, valid, q0, q1, tab);
+      stage_step<NREP, W64, true>(st, lane, kw, vw, valid, q, tab);
     }
     wave_sync();
-    contract_step<(NREP > 4 ? 2 : 1)>(st, lane, acc, accl);
+    contract_step<(NREP > 4 ? 2 : 1), W64>(st, lane, acc, accl);
     wave_sync();
   };
 
   // Three register buffers in a fixed ring, unrolled by three, so a load in
   // flight is never copied (a copy would wait for it).
-  uint64_t k0[2], v0[2], k1[2], v1[2], k2[2], v2[2];
+  uint64_t k0[2][W64], v0[2][W64], k1[2][W64], v1[2][W64], k2[2][W64], v2[2][W64];
   const int lo = 2 * lane;
   // A wave with no tokens (short or empty partition) issues no loads: only
   // then is every pair index inside the staged block range [0, nblk).
@@ -492,8 +533,8 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT
     __syncthreads();
 #pragma unroll
     for (int h = 0; h < 8; ++h) {
-      q0[h] = h < NREP ? static_cast<uint32_t>(fw[h]) : 0u;
-      q1[h] = h < NREP ? static_cast<uint32_t>(fw[h] >> 32) : 0u;
+      q[0][h] = h < NREP ? static_cast<uint32_t>(fw[h]) : 0u;
+      q[1][h] = h < NREP ? static_cast<uint32_t>(fw[h] >> 32) : 0u;
     }
     kcur = fw[NREP];
     vcur = fw[NREP + 1];
@@ -542,10 +583,11 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT
   }
 
   // Per lane: row tile rt holds head 4rt + lane/16 with its four digits in
-  // acc[rt][ts][d] (digit d carries 2^-(8+4d)); column lane%16 of channel
-  // tile ts is channel 4*(lane%16) + ts, whose set bits were 0.5, 1.0, 2.0,
-  // 2.0 for ts = 0..3 (the ones tile: 0.5).
-  float val[8], lh[2];
+  // acc[rt][c][d] (digit d carries 2^-(8+4d)); column lane%16 of channel
+  // tile c = 4*hv + ts is channel 64*hv + 4*(lane%16) + ts, whose set bits
+  // were 0.5, 1.0, 2.0, 2.0 for ts = 0..3 (the ones tile: 0.5).
+  constexpr int kVals = 8 * W64;  // values per lane: 2 row tiles x 4 W64 channel tiles
+  float val[kVals], lh[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     float l = 0.f;
@@ -553,33 +595,35 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT
     for (int d = 0; d < 4; ++d) l += accl[rt][d] * ldexpf(1.f, -(7 + 4 * d));
     lh[rt] = l;
 #pragma unroll
-    for (int ts = 0; ts < 4; ++ts) {
+    for (int c = 0; c < 4 * W64; ++c) {
+      const int ts = c & 3;
       const float m = ts == 0 ? 1.f : (ts == 1 ? 0.5f : 0.25f);
       float a = 0.f;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) a += acc[rt][ts][d] * (m * ldexpf(1.f, -(7 + 4 * d)));
-      val[4 * rt + ts] = a;
+      for (int d = 0; d < 4; ++d) a += acc[rt][c][d] * (m * ldexpf(1.f, -(7 + 4 * d)));
+      val[4 * W64 * rt + c] = a;
     }
   }
 
   // Cross-wave reduction (fixed order) through LDS, reusing the stage area.
+  constexpr int kRed = kVals + 2;
   __syncthreads();
   float *red = reinterpret_cast<float *>(smem);
   if (wave > 0) {
-    float *dst = red + ((wave - 1) * 64 + lane) * 10;
+    float *dst = red + ((wave - 1) * 64 + lane) * kRed;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) dst[k] = val[k];
+    for (int k = 0; k < kVals; ++k) dst[k] = val[k];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) dst[8 + k] = lh[k];
+    for (int k = 0; k < 2; ++k) dst[kVals + k] = lh[k];
   }
   __syncthreads();
   if (wave != 0) return;
   for (int w = 1; w < kWaves; ++w) {
-    const float *src = red + ((w - 1) * 64 + lane) * 10;
+    const float *src = red + ((w - 1) * 64 + lane) * kRed;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) val[k] += src[k];
+    for (int k = 0; k < kVals; ++k) val[k] += src[k];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) lh[k] += src[8 + k];
+    for (int k = 0; k < 2; ++k) lh[k] += src[kVals + k];
   }
 
   const bool single = nparts_seq == 1;
@@ -589,16 +633,16 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT
     if (h >= NREP) continue;
     const int hq = kvh * NREP + h;
 #pragma unroll
-    for (int ts = 0; ts < 4; ++ts) {
-      const int ch = 4 * (lane & 15) + ts;
-      const float a = val[4 * rt + ts];
+    for (int c = 0; c < 4 * W64; ++c) {
+      const int ch = 64 * (c >> 2) + 4 * (lane & 15) + (c & 3);
+      const float a = val[4 * W64 * rt + c];
       if (single) {
         const float o = len <= 0 ? 0.f : a / lh[rt];
         store_f32_as(p.out, t * p.os0 + n * p.os1 + hq * p.os2 + ch * p.os3, p.out_dtype, o);
-      } else {
-        float *dst = p.ws + ((((int64_t)part * p.T + t) * p.N + n) * p.Hq + hq) * 65;
+      } else {  // partials: head_dim values, then the denominator
+        float *dst = p.ws + ((((int64_t)part * p.T + t) * p.N + n) * p.Hq + hq) * (64 * W64 + 1);
         dst[ch] = a;
-        if (ch == 0) dst[64] = lh[rt];
+        if (ch == 0) dst[64 * W64] = lh[rt];
       }
     }
   }
@@ -635,11 +679,11 @@ static uint32_t e4m3_encode(float x, float *val) {
   return code | (code ? sign : 0u);
 }
 
-void build_digit_table(float scale, uint32_t digits[65]) {
+void build_digit_table(float scale, uint32_t digits[kDigitEntries]) {
   static thread_local float last_scale = -1.f;
-  static thread_local uint32_t last[65];
+  static thread_local uint32_t last[kDigitEntries];
   if (scale != last_scale) {
-    for (int d = 0; d <= 64; ++d) {
+    for (int d = 0; d < kDigitEntries; ++d) {
       float x = std::exp(-static_cast<float>(d) * scale) * 256.f;
       uint32_t w = 0;
       for (int s = 0; s < 4; ++s) {
@@ -651,12 +695,14 @@ void build_digit_table(float scale, uint32_t digits[65]) {
     }
     last_scale = scale;
   }
-  for (int d = 0; d <= 64; ++d) digits[d] = last[d];
+  for (int d = 0; d < kDigitEntries; ++d) digits[d] = last[d];
 }
 
 bool mfma_path_supported(const AttnParams &p) {
   const auto al16 = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
-  return p.head_dim == 64 && p.nrep <= 8 && p.bs_log2 >= 1 && p.ks2 == 2 && p.vs2 == 2 &&
+  const int w32 = p.head_dim / 32;  // 32-bit words per token: slots must be dense
+  return (p.head_dim == 64 || p.head_dim == 128) && p.nrep <= 8 && p.bs_log2 >= 1 &&
+         p.ks2 == w32 && p.vs2 == w32 &&
          (p.ks0 % 4) == 0 && (p.ks1 % 4) == 0 && (p.vs0 % 4) == 0 && (p.vs1 % 4) == 0 &&
          al16(p.k) && al16(p.v) &&
          ((p.part_len + (1 << p.bs_log2) - 1) >> p.bs_log2) <= mfma::kMaxPartBlocks;
@@ -728,23 +774,25 @@ void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s, 
     p.order = order;
     grid = dim3(units * p.num_parts);
   }
-#define SPK_NREP_CASES(XDT)                                                                   \
+#define SPK_NREP_CASES(XDT, W64)                                                              \
   switch (p.nrep) {                                                                           \
-    case 1: mfma::decode_attn_mfma_kernel<1, XDT><<<grid, threads, 0, s>>>(p); break;         \
-    case 2: mfma::decode_attn_mfma_kernel<2, XDT><<<grid, threads, 0, s>>>(p); break;         \
-    case 3: mfma::decode_attn_mfma_kernel<3, XDT><<<grid, threads, 0, s>>>(p); break;         \
-    case 4: mfma::decode_attn_mfma_kernel<4, XDT><<<grid, threads, 0, s>>>(p); break;         \
-    case 5: mfma::decode_attn_mfma_kernel<5, XDT><<<grid, threads, 0, s>>>(p); break;         \
-    case 6: mfma::decode_attn_mfma_kernel<6, XDT><<<grid, threads, 0, s>>>(p); break;         \
-    case 7: mfma::decode_attn_mfma_kernel<7, XDT><<<grid, threads, 0, s>>>(p); break;         \
-    default: mfma::decode_attn_mfma_kernel<8, XDT><<<grid, threads, 0, s>>>(p); break;        \
+    case 1: mfma::decode_attn_mfma_kernel<1, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
+    case 2: mfma::decode_attn_mfma_kernel<2, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
+    case 3: mfma::decode_attn_mfma_kernel<3, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
+    case 4: mfma::decode_attn_mfma_kernel<4, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
+    case 5: mfma::decode_attn_mfma_kernel<5, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
+    case 6: mfma::decode_attn_mfma_kernel<6, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
+    case 7: mfma::decode_attn_mfma_kernel<7, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
+    default: mfma::decode_attn_mfma_kernel<8, XDT, W64><<<grid, threads, 0, s>>>(p); break;   \
   }
-  if (fused_dtype == SPK_BF16) {
-    SPK_NREP_CASES(SPK_BF16)
+  if (fused_dtype == SPK_BF16) {  // the caller allows the fused path at head_dim 64 only
+    SPK_NREP_CASES(SPK_BF16, 1)
   } else if (fused_dtype == SPK_F16) {
-    SPK_NREP_CASES(SPK_F16)
+    SPK_NREP_CASES(SPK_F16, 1)
+  } else if (p.head_dim == 128) {
+    SPK_NREP_CASES(0, 2)
   } else {
-    SPK_NREP_CASES(0)
+    SPK_NREP_CASES(0, 1)
   }
 #undef SPK_NREP_CASES
 }
