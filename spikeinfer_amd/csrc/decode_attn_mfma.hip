@@ -384,7 +384,7 @@ __device__ __forceinline__ void fused_spikes(const FusedIn<XDT> &in, int t, int 
 // path, which derives this unit's q and current k/v spikes from p.fz
 // (head_dim 64 only).  W64 = head_dim / 64 (1 or 2).
 template <int NREP, int XDT, int W64>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(W64 == 2 ? (NREP > 4 ? 2 : 3) : (XDT == 0 ? 4 : 3)))) void decode_attn_mfma_kernel(AttnParams p) {
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT == 0 && W64 == 1 ? 4 : 3))) void decode_attn_mfma_kernel(AttnParams p) {
   static_assert(W64 == 1 || (W64 == 2 && XDT == 0), "fused path: head_dim 64 only");
   // Unplanned launch: x = (sequence, timestep, kv head) unit, y = partition.
   // Either way consecutive block ids (dealt round-robin to the 8 XCDs) are
@@ -443,7 +443,8 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(W64
     for (int h = 0; h < 8; ++h) {
       const uint32_t *qp = p.q + t * p.qs0 + n * p.qs1 + (kvh * NREP + h) * p.qs2;
 #pragma unroll
-      for (int w = 0; w < 2 * W64; ++w) q[w][h] = h < NREP ? qp[w] : 0u;
+      for (int w = 0; w < 2 * W64; ++w)  // wave-uniform: kept in SGPRs
+        q[w][h] = h < NREP ? static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(qp[w]))) : 0u;
     }
   }
   __syncthreads();
@@ -533,8 +534,8 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(W64
     __syncthreads();
 #pragma unroll
     for (int h = 0; h < 8; ++h) {
-      q[0][h] = h < NREP ? static_cast<uint32_t>(fw[h]) : 0u;
-      q[1][h] = h < NREP ? static_cast<uint32_t>(fw[h] >> 32) : 0u;
+      q[0][h] = h < NREP ? static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(fw[h]))) : 0u;
+      q[1][h] = h < NREP ? static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(fw[h] >> 32))) : 0u;
     }
     kcur = fw[NREP];
     vcur = fw[NREP + 1];
@@ -557,6 +558,20 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(W64
     }
   }
   int i = 0;
+  if constexpr (W64 == 2) {  // two buffers: the wider words leave room for no third
+    for (; i + 2 <= nfull; i += 2) {
+      step(k0, v0, false, first + i * kStride);
+      load(first + (i + 2) * kStride + lo, k0, v0);
+      step(k1, v1, false, first + (i + 1) * kStride);
+      load(first + (i + 3) * kStride + lo, k1, v1);
+    }
+    if (i < nfull) step(k0, v0, false, first + i * kStride);
+    if (nfull < ntotal) {  // the partial last step: buffer nfull % 2
+      const int j0 = first + nfull * kStride;
+      if (nfull % 2 == 0) step(k0, v0, true, j0);
+      else step(k1, v1, true, j0);
+    }
+  } else {
   for (; i + 3 <= nfull; i += 3) {
     load(first + (i + 2) * kStride + lo, k2, v2);
     step(k0, v0, false, first + i * kStride);
@@ -580,6 +595,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(W64
     if (r == 0) step(k0, v0, true, j0);
     else if (r == 1) step(k1, v1, true, j0);
     else step(k2, v2, true, j0);
+  }
   }
 
   // Per lane: row tile rt holds head 4rt + lane/16 with its four digits in
