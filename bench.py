@@ -201,12 +201,28 @@ def bench_lif(steps, warmup, dev):
         lif_multistep(xg, bg, tg)
 
     stream = torch.cuda.current_stream(dev)
-    ms_qkv = time_calls(qkv, steps, warmup, stream)
+    ms_qkv_eager = time_calls(qkv, steps, warmup, stream)
+    # The same three calls captured in a hipGraph, as a serving runner replays
+    # them (8 layers' worth per graph, so one replay outlasts its own launch):
+    # GPU time without the Python launch gaps between the calls.
+    reps = 8
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        qkv()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            qkv()
+    ms_qkv = time_calls(graph.replay, steps, warmup, stream) / reps
     ms_gate = time_calls(gate, steps, warmup, stream)
     bytes_qkv = T * n_tok * (HQ + 2 * HKV) * D * 2 + T * n_tok * (HQ + 2 * HKV) * 8 + 2 * 8 * n_tok
     bytes_gate = T * n_tok * 4864 * 2 * 2
     return {
         "qkv_ms": round(ms_qkv, 4), "qkv_gbs": round(bytes_qkv / ms_qkv / 1e6, 1),
+        "qkv_ms_eager": round(ms_qkv_eager, 4),
         "gate_ms": round(ms_gate, 4), "gate_gbs": round(bytes_gate / ms_gate / 1e6, 1),
         "total_gbs": round((bytes_qkv + bytes_gate) / (ms_qkv + ms_gate) / 1e6, 1),
     }
