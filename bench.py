@@ -49,7 +49,7 @@ def measured_traffic():
 T, HQ, HKV, D, BS = 4, 14, 2, 64, 16
 
 
-def make_attn_inputs(n_seqs, lo, hi, density, seed, dev, layers=1):
+def make_attn_inputs(n_seqs, lo, hi, density, seed, dev, layers=1, head_dim=D):
     """Synthetic paged cache: Bernoulli(density) bits, shuffled blocks."""
     from spikeinfer_amd.kernels import pack_spikes
 
@@ -71,25 +71,25 @@ def make_attn_inputs(n_seqs, lo, hi, density, seed, dev, layers=1):
     for _ in range(layers):
         kv = []
         for _ in range(2):
-            c = torch.empty((T, HKV, slots, 2), dtype=torch.int32, device=dev)
-            flat = c.view(-1, 2)
+            c = torch.empty((T, HKV, slots, head_dim // 32), dtype=torch.int32, device=dev)
+            flat = c.view(-1, head_dim // 32)
             for s0 in range(0, flat.shape[0], chunk):
                 n = min(chunk, flat.shape[0] - s0)
-                bits = torch.rand((n, D), generator=gd, device=dev) < density
+                bits = torch.rand((n, head_dim), generator=gd, device=dev) < density
                 flat[s0:s0 + n] = pack_spikes(bits)
             kv.append(c)
         caches.append(kv)
-    q = pack_spikes(torch.rand((T, n_seqs, HQ, D), generator=gd, device=dev) < density)
+    q = pack_spikes(torch.rand((T, n_seqs, HQ, head_dim), generator=gd, device=dev) < density)
     return dict(q=q, caches=caches, tables=tables.to(dev), lens=lens.to(dev),
-                lens_cpu=lens, max_blocks=max_blocks)
+                lens_cpu=lens, max_blocks=max_blocks, head_dim=head_dim)
 
 
-def attn_bytes(lens_cpu, out_elem_bytes):
+def attn_bytes(lens_cpu, out_elem_bytes, head_dim=D):
     n = lens_cpu.numel()
     ctx = int(lens_cpu.sum())
-    kv = ctx * T * HKV * 2 * 8
-    q = n * T * HQ * 8
-    out = n * T * HQ * D * out_elem_bytes
+    kv = ctx * T * HKV * 2 * (head_dim // 8)
+    q = n * T * HQ * (head_dim // 8)
+    out = n * T * HQ * head_dim * out_elem_bytes
     table = int(((lens_cpu + BS - 1) // BS).sum()) * 4
     return kv + q + out + table + 4 * n
 
@@ -112,14 +112,15 @@ def bench_attention(inp, steps, warmup, dev, out_dtype=torch.float32, graph=Fals
     from spikeinfer_amd.kernels import decode_attn_workspace_bytes, paged_spike_attn_decode
 
     n = inp["lens"].numel()
-    out = torch.empty((T, n, HQ, D), device=dev, dtype=out_dtype)
-    ws = torch.empty(decode_attn_workspace_bytes(T, n, HQ, HKV, D, BS, inp["max_blocks"]) or 1,
+    hd = inp["head_dim"]
+    out = torch.empty((T, n, HQ, hd), device=dev, dtype=out_dtype)
+    ws = torch.empty(decode_attn_workspace_bytes(T, n, HQ, HKV, hd, BS, inp["max_blocks"]) or 1,
                      dtype=torch.uint8, device=dev)
     layers = inp["caches"]
 
     def step():
         for k, v in layers:
-            paged_spike_attn_decode(inp["q"], k, v, inp["tables"], inp["lens"], D, BS, HQ, HKV,
+            paged_spike_attn_decode(inp["q"], k, v, inp["tables"], inp["lens"], hd, BS, HQ, HKV,
                                     out=out, workspace=ws)
 
     if graph:
@@ -316,6 +317,13 @@ def main():
             ms_p, _ = bench_attention(alt, args.steps, args.warmup, dev)
             extras[f"density_{p}_gbs"] = round(nbytes / ms_p / 1e6, 1)
             del alt
+        print("config 4 at head_dim 128", file=sys.stderr, flush=True)
+        alt = make_attn_inputs(256, 4096, 32768, 0.2, 4000, dev, head_dim=128)
+        ms_h, _ = bench_attention(alt, args.steps, args.warmup, dev)
+        extras["config4_head_dim_128"] = {
+            "us_per_call": round(ms_h * 1000, 1),
+            "gbs": round(attn_bytes(alt["lens_cpu"], 4, 128) / ms_h / 1e6, 1)}
+        del alt
         print("config 3", file=sys.stderr, flush=True)
         c3 = make_attn_inputs(64, 128, 192, 0.2, 3000, dev, layers=24)
         ms3, _ = bench_attention(c3, args.steps, args.warmup, dev, torch.bfloat16, graph=True)
