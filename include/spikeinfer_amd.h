@@ -281,6 +281,29 @@ int spk_lif_gate_mul(const void *x, int dtype, const int64_t x_strides[2],
                      void *out, int T, int64_t rows, int I, void *stream);
 
 /*
+ * Fused MLP gate for decode sizes: the gate|up projection, the gate LIF over T
+ * and the spike * up product in one launch, replacing
+ * lif_multistep(gate_proj(x)) * up_proj(x) (spikeinfer/modeling_fast.py:186-190),
+ * i.e. a bf16 GEMM on the concatenated weight followed by spk_lif_gate_mul.
+ *
+ * spk_mlp_gate_pack reorders W_gu [2*I, hidden] (gate rows, then up rows; bf16,
+ * contiguous) into the kernel's operand order, spk_mlp_gate_packed_bytes(hidden,
+ * I) bytes at w_packed; done once per weight.
+ * spk_mlp_gate_lif: x [T, n_tok, hidden] bf16 contiguous -> y [T, n_tok, I] bf16
+ * contiguous.  Supports T <= 4, hidden a multiple of 128 in [512, 1024] (and
+ * T * 16 * hidden * 2 <= 160 KiB), I / 16 in [64, 512]; returns SPK_EUNSUPPORTED
+ * otherwise (the caller then runs the GEMM and spk_lif_gate_mul).  The GEMM sums
+ * are fp32 in a fixed order, rounded to bf16 before the LIF, as the two-launch
+ * path rounds the GEMM output.
+ */
+size_t spk_mlp_gate_packed_bytes(int hidden, int inter);
+int spk_mlp_gate_pack(const void *w_gu, int inter, int hidden, int dtype, void *w_packed,
+                      void *stream);
+int spk_mlp_gate_lif(const void *x, const void *w_packed, const void *beta,
+                     const void *threshold, int param_dtype, void *y, int T, int n_tok,
+                     int hidden, int inter, int dtype, void *stream);
+
+/*
  * Device-side advance of a decode batch after sampling: for rows i < n_live,
  * where n_live = n_rows, or min(n_rows, *live) when `live` is given (a device
  * count, so a captured step serves any live batch up to n_rows),

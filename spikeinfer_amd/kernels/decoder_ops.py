@@ -284,6 +284,55 @@ def lif_gate_mul(gate_up: torch.Tensor, beta: torch.Tensor, threshold: torch.Ten
     return out
 
 
+def pack_gate_up(w_gu: torch.Tensor) -> torch.Tensor:
+    """Reorders the concatenated gate|up weight ``[2I, hidden]`` (bf16) into the
+    operand order of :func:`mlp_gate_lif`; done once per weight."""
+    dev = _lib.require_gpu(w_gu)
+    if w_gu.ndim != 2 or w_gu.dtype != torch.bfloat16 or not w_gu.is_contiguous():
+        raise ValueError("w_gu must be a contiguous bf16 [2I, hidden] tensor")
+    I2, hidden = w_gu.shape
+    if I2 % 32 or hidden % 32:
+        raise ValueError(f"w_gu shape {tuple(w_gu.shape)}: 2I must be a multiple of 32, hidden of 32")
+    lib = _lib.load()
+    out = torch.empty(lib.spk_mlp_gate_packed_bytes(hidden, I2 // 2) // 2, dtype=torch.bfloat16,
+                      device=dev)
+    _lib.check(lib.spk_mlp_gate_pack(w_gu.data_ptr(), I2 // 2, hidden, _lib.dtype_code(w_gu.dtype),
+                                     out.data_ptr(), _lib.stream_of(dev)), "mlp_gate_pack")
+    return out
+
+
+def mlp_gate_lif(x: torch.Tensor, w_packed: torch.Tensor, beta: torch.Tensor,
+                 threshold: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """``LIF(x @ W_g^T) * (x @ W_u^T)`` for ``x [T, n_tok, hidden]`` in one
+    launch (modeling_fast.py:186-190), from :func:`pack_gate_up`'s weight.
+
+    Returns ``[T, n_tok, I]``, or None when the shape is outside the kernel's
+    range (the caller then runs the GEMM and :func:`lif_gate_mul`).
+    """
+    dev = _lib.require_gpu(x, w_packed, beta, threshold, out)
+    if x.ndim != 3 or x.dtype != torch.bfloat16:
+        raise ValueError("x must be a bf16 [T, n_tok, hidden] tensor")
+    T, n, hidden = x.shape
+    I = beta.numel()
+    if threshold.numel() != I or w_packed.numel() * w_packed.element_size() != 4 * I * hidden:
+        raise ValueError(f"packed weight / beta / threshold do not match hidden={hidden}, I={I}")
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty((T, n, I), dtype=x.dtype, device=dev)
+    elif tuple(out.shape) != (T, n, I) or not out.is_contiguous() or out.dtype != x.dtype:
+        raise ValueError(f"out must be contiguous bf16 [{T}, {n}, {I}]")
+    beta = beta.contiguous()
+    threshold = threshold.to(beta.dtype).contiguous()
+    rc = _lib.load().spk_mlp_gate_lif(
+        x.data_ptr(), w_packed.data_ptr(), beta.data_ptr(), threshold.data_ptr(),
+        _lib.dtype_code(beta.dtype), out.data_ptr(), T, n, hidden, I, _lib.dtype_code(x.dtype),
+        _lib.stream_of(dev))
+    if rc == _lib.SPK_EUNSUPPORTED:
+        return None
+    _lib.check(rc, "mlp_gate_lif")
+    return out
+
+
 def decode_advance(next_tokens, input_ids, positions, seq_lens, slot_mapping, block_tables,
                    block_size: int, n_rows: int, live=None, history=None, step=None) -> None:
     """Moves rows ``[0, n_live)`` of a decode batch to their next token on the

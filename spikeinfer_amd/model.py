@@ -27,8 +27,9 @@ import torch
 import torch.nn.functional as F
 
 from .attention import AttentionMetadata
-from .kernels.decoder_ops import (add_rmsnorm, embed_rmsnorm, lif_gate_mul, qkv_decode_attention,
-                                  qkv_rope_lif_pack, rmsnorm_mean_t)
+from .kernels.decoder_ops import (add_rmsnorm, embed_rmsnorm, lif_gate_mul, mlp_gate_lif,
+                                  pack_gate_up, qkv_decode_attention, qkv_rope_lif_pack,
+                                  rmsnorm_mean_t)
 from .kernels.packing import packed_width
 from .kernels.spike_attention import gather_kv_unpacked, paged_spike_attn_decode
 
@@ -56,7 +57,7 @@ class SpikingQwenConfig:
 
 class _Layer:
     __slots__ = ("input_norm", "post_norm", "w_qkv", "b_qkv", "lif_qkv_beta", "lif_qkv_th",
-                 "w_o", "w_gu", "lif_gate_beta", "lif_gate_th", "w_down")
+                 "w_o", "w_gu", "lif_gate_beta", "lif_gate_th", "w_down", "w_gu_packed")
 
 
 class SpikingDecoder:
@@ -101,6 +102,12 @@ class SpikingDecoder:
         # Decode-only batches run q/k/v spikes and attention as one launch
         # (qkv_decode_attention); False keeps the two launches (same results).
         self.fused_attention = True
+        # Batches of at most fused_mlp_max_tokens tokens run the gate|up GEMM,
+        # the gate LIF and the product as one launch (mlp_gate_lif, from a
+        # repacked copy of w_gu); False keeps the GEMM + lif_gate_mul.
+        self.fused_mlp = True
+        self.fused_mlp_max_tokens = 64
+        self._pack_mlp()
         # Rotary inverse frequencies as Qwen2RotaryEmbedding builds them (fp32, host).
         exps = torch.arange(0, self.D, 2, dtype=torch.int64).float() / self.D
         self.inv_freq = (1.0 / (c.rope_theta ** exps)).to(self.device)
@@ -133,6 +140,17 @@ class SpikingDecoder:
             L.lif_gate_beta = cast(sd[m + "lif_gate.lif.beta"])
             L.lif_gate_th = cast(sd[m + "lif_gate.lif.threshold"])
             L.w_down = cast(sd[m + "down_proj.weight"])
+        self._pack_mlp()
+
+    def _pack_mlp(self) -> None:
+        """The fused MLP gate's operand-order copy of each w_gu (bf16 only)."""
+        for L in self.layers:
+            L.w_gu_packed = None
+            if self.dtype == torch.bfloat16:
+                try:
+                    L.w_gu_packed = pack_gate_up(L.w_gu)
+                except ValueError:
+                    pass
 
     @property
     def weight_bytes(self) -> int:
@@ -141,7 +159,8 @@ class SpikingDecoder:
         n = self.lm_head.numel() + self.final_norm.numel()
         for L in self.layers:
             for name in _Layer.__slots__:
-                n += getattr(L, name).numel()
+                if name != "w_gu_packed":  # a step reads it instead of w_gu, not as well
+                    n += getattr(L, name).numel()
         return n * self.lm_head.element_size()
 
     # -- forward -----------------------------------------------------------
@@ -202,8 +221,12 @@ class SpikingDecoder:
                 self._prefill_attention(dense, k_cache, v_cache, meta, attn)
             o = F.linear(attn.view(T, n, Hq * D), L.w_o)
             x = add_rmsnorm(h, o, L.post_norm, c.rms_norm_eps, out=x)
-            gu = F.linear(x, L.w_gu)
-            delta = F.linear(lif_gate_mul(gu, L.lif_gate_beta, L.lif_gate_th), L.w_down)
+            y = None
+            if self.fused_mlp and L.w_gu_packed is not None and n <= self.fused_mlp_max_tokens:
+                y = mlp_gate_lif(x, L.w_gu_packed, L.lif_gate_beta, L.lif_gate_th)
+            if y is None:
+                y = lif_gate_mul(F.linear(x, L.w_gu), L.lif_gate_beta, L.lif_gate_th)
+            delta = F.linear(y, L.w_down)
         return rmsnorm_mean_t(h, self.final_norm, c.rms_norm_eps, delta=delta)
 
     def _prefill_attention(self, dense, k_cache, v_cache, meta: AttentionMetadata, attn) -> None:

@@ -235,6 +235,81 @@ def test_lif_gate_mul_bit_exact(gpu, dtype):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("T,n,H,I", [(4, 64, 896, 4864), (4, 37, 896, 4864), (4, 1, 896, 4864),
+                                     (4, 16, 512, 1024), (2, 20, 1024, 8192), (3, 5, 640, 2048)])
+def test_mlp_gate_lif_matches_reference(gpu, T, n, H, I):
+    """Fused gate|up GEMM + gate LIF + product against the same computed
+    exactly: the GEMM in fp64 rounded to bf16 (the kernel sums in fp32, in a
+    fixed order, then rounds), the LIF reference, the bf16 product.  A gate sum
+    within fp32 error of a bf16 rounding boundary may round the other way, so a
+    spike may rarely differ (at most 1e-4 of them); products agree to 1 ulp."""
+    from spikeinfer_amd.kernels.decoder_ops import mlp_gate_lif, pack_gate_up
+
+    print(f"mlp_gate_lif T={T} n={n} H={H} I={I}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(T * 1000 + n + H)
+    x = (torch.randn((T, n, H), generator=g, device=gpu) * 1.2).bfloat16()
+    w = (torch.randn((2 * I, H), generator=g, device=gpu) * 0.05).bfloat16()
+    beta = 0.6 + 0.4 * torch.rand(I, generator=g, device=gpu)
+    th = 0.5 + torch.rand(I, generator=g, device=gpu)
+    got = mlp_gate_lif(x, pack_gate_up(w), beta, th)
+    assert got is not None
+    gu = (x.double() @ w.double().t()).to(torch.bfloat16)
+    gate, up = gu[..., :I], gu[..., I:]
+    spikes = lif_ref(gate, beta, th)
+    want = (spikes.float() * up.float()).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    s_got, s_want = got != 0, spikes != 0
+    flips = int((s_got != s_want).sum())
+    assert flips <= max(1, s_want.numel() // 10000), f"{flips} spikes differ"
+    both = s_got & s_want
+    d = (got.float() - want.float()).abs()[both]
+    tol = (want.float().abs()[both] * 2.0 ** -7) + 1e-4 * float(up.float().abs().max())
+    assert bool((d <= tol).all()), f"max product difference {float(d.max())}"
+
+
+def test_mlp_gate_lif_unsupported_shapes_return_none(gpu):
+    from spikeinfer_amd.kernels.decoder_ops import mlp_gate_lif, pack_gate_up
+
+    for T, H, I in ((4, 256, 4864), (5, 896, 4864), (4, 896, 512)):
+        x = torch.zeros((T, 3, H), device=gpu, dtype=torch.bfloat16)
+        w = torch.zeros((2 * I, H), device=gpu, dtype=torch.bfloat16)
+        b = torch.ones(I, device=gpu)
+        assert mlp_gate_lif(x, pack_gate_up(w), b, b) is None
+
+
+def test_model_fused_mlp_matches_two_launches(gpu):
+    """A decode step with the fused MLP gate against the GEMM + lif_gate_mul
+    path (the GEMM sums differ in order only): same tolerances as the
+    reference-forward check."""
+    cfg = SpikingQwenConfig(vocab_size=1024, hidden_size=512, intermediate_size=1024,
+                            num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
+                            head_dim=64)
+    m = SpikingDecoder(cfg, device=gpu, seed=9, init_std=0.06)
+    assert all(L.w_gu_packed is not None for L in m.layers)
+    bs, n = 16, 11
+    g = torch.Generator().manual_seed(8)
+    lens = torch.randint(5, 60, (n,), generator=g)
+    tables = torch.randperm(64, generator=g)[: n * 4].view(n, 4).to(torch.int32)
+    pos = (lens - 1).to(torch.int64)
+    slots = tables[torch.arange(n), pos // bs].to(torch.int64) * bs + pos % bs
+    meta = AttentionMetadata(slot_mapping=slots.to(gpu), block_size=bs, num_decode_tokens=n,
+                             block_tables=tables.to(gpu), seq_lens=lens.to(torch.int32).to(gpu))
+    ids = torch.randint(0, 1024, (n,), generator=g).to(gpu)
+    caches = [PagedSpikeCache(2, m.T, m.Hkv, m.D, 65, bs, device=gpu) for _ in range(2)]
+    for (k0, v0), (k1, v1) in zip(caches[0].layers, caches[1].layers):
+        k0.random_(-2**31, 2**31 - 1)
+        v0.random_(-2**31, 2**31 - 1)
+        k1.copy_(k0)
+        v1.copy_(v0)
+    outs = []
+    for fused, c in zip((True, False), caches):
+        m.fused_mlp = fused
+        outs.append(m.forward_paged(ids, pos.to(gpu), c.layers, meta))
+    m.fused_mlp = True
+    torch.cuda.synchronize()
+    _compare(outs[0], outs[1], caches[0], caches[1], m)
+
+
 def test_decode_advance_moves_live_rows_only(gpu):
     B, mb, bs = 5, 4, 16
     tables = torch.arange(B * mb, dtype=torch.int32, device=gpu).view(B, mb).flip(1).contiguous()
