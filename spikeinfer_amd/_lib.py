@@ -64,6 +64,8 @@ _SIGNATURES = {
         _i64, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _vp]),
     "spk_lif_gate_mul": (_i32, [_vp, _i32, _i64p, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _vp]),
     "spk_mlp_gate_packed_bytes": (_sz, [_i32, _i32]),
+    "spk_linear_pack": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
+    "spk_linear_decode": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
     "spk_mlp_gate_pack": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
     "spk_mlp_gate_lif": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "spk_decode_advance": (_i32, [

@@ -1,0 +1,217 @@
+// Small-M linear layer of the decode step: y = x @ W^T (+ bias), bf16, for the
+// q/k/v and o projections (spikeinfer/modeling_fast.py:121-135, :150-166) at
+// decode batch sizes (M = T * n_tok <= 256 rows, K <= 1280).
+//
+// MI355X design (the same ground rules as the fused MLP gate in mlp_gate.hip):
+// at these sizes a projection is bound by moving x and W into the CUs and by
+// latency, not by the matrix cores.
+//   * A workgroup owns a 64-row group of x, the whole K, in LDS (at most
+//     160 KB), loaded once by global_load_lds into a layout swizzled by row
+//     (16-byte chunk c of row r at chunk c ^ (r % 16)).
+//   * W is repacked once at load in MFMA-fragment order (spk_linear_pack):
+//     one k-step (32 K) of one 16-column tile is one contiguous 1 KB block, so a
+//     wave's B operand arrives with one coalesced 16-byte load per lane.
+//   * The workgroup's 16-column tiles are split into (tile, K-eighth) units
+//     over its 8 waves; each wave issues all of its units' loads at once and
+//     the eight partial sums of a tile are added in a fixed order through LDS
+//     (deterministic).
+//   * v_mfma_f32_16x16x32_bf16: D lane l, acc j = row 4(l/16) + j of the row
+//     tile, column l % 16.
+// Grid: row groups x column ranges (ranges chosen so the launch has about 256
+// workgroups); the row groups of one range are consecutive on one XCD (block b
+// -> XCD b % 8), so W comes from HBM once.
+#include "common.hpp"
+#include "lif_math.hpp"
+
+namespace spk {
+namespace lin {
+
+typedef __bf16 v8b __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+#define SPK_LDS __attribute__((address_space(3)))
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kRows = 64;            // rows of x per workgroup (4 row tiles)
+constexpr int kParts = 8;            // K split of a tile into units
+constexpr int kMaxUnitsPerWave = 2;  // tiles per range <= 2
+constexpr int kMaxPartSteps = 5;     // k-steps per part: K <= 8 * 5 * 32 = 1280
+constexpr int kLdsBytes = 160 * 1024;
+constexpr int kSlotFloats = 4 * 4 * 64;  // one partial: 4 row tiles x 4 x 64 lanes
+
+// Packed W (spk_linear_pack): for tile p (rows 16p..16p+15 of W) and k-step
+// ks, 1 KB at (p * KS + ks) KB: lane l's 16 bytes are W[16p + l%16][32ks +
+// 8(l/16) .. +7].
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void linear_kernel(
+    const uint16_t *x, const v4u *wp, const uint16_t *bias, uint16_t *y, int M, int N, int K,
+    int MG, int R) {
+  extern __shared__ __align__(16) char smem[];
+  const int KS = K / 32, kChunks = K / 8;  // k-steps, 16-byte chunks per row
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x, xcd = b & 7, s = b >> 3;
+  const int m = s % MG, r = (s / MG) * 8 + xcd;
+  const int P = N / 16;
+  const int p0 = r * P / R, np = (r + 1) * P / R - p0;
+  if (np <= 0) return;  // uniform over the workgroup
+  const int m0 = m * kRows;
+
+  // Units (tile, part): wave w takes units w and w + 8 (np <= 2 tiles).
+  const int U = np * kParts;
+  auto part_range = [&](int part, int &k0, int &k1) {
+    k0 = part * KS / kParts;
+    k1 = (part + 1) * KS / kParts;
+  };
+  v4u bq[kMaxUnitsPerWave][kMaxPartSteps];
+#pragma unroll
+  for (int j = 0; j < kMaxUnitsPerWave; ++j) {
+    const int u = wave + kWaves * j;
+    if (u < U) {
+      int k0, k1;
+      part_range(u % kParts, k0, k1);
+      const v4u *src = wp + static_cast<int64_t>((p0 + u / kParts) * KS + k0) * 64 + lane;
+#pragma unroll
+      for (int ks = 0; ks < kMaxPartSteps; ++ks)
+        if (ks < k1 - k0) bq[j][ks] = src[ks * 64];
+    }
+  }
+
+  // x rows m0..m0+63 (clamped to M - 1) into LDS, chunk c of row rr at c ^ (rr % 16).
+  const int total = kRows * kChunks;  // a multiple of 64 (K % 128 == 0)
+  for (int base = wave * 64; base < total; base += kWaves * 64) {
+    const int g = base + lane;
+    const int rr = g / kChunks, pc = g - rr * kChunks;
+    const int c = pc ^ (rr & 15);
+    const int row = min(m0 + rr, M - 1);
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(x + static_cast<int64_t>(row) * K + 8 * c),
+                                     (SPK_LDS void *)(smem + base * 16), 16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+  __syncthreads();
+
+  const int r16 = lane & 15, kq = lane >> 4;
+  v4f acc[kMaxUnitsPerWave][4];
+#pragma unroll
+  for (int j = 0; j < kMaxUnitsPerWave; ++j)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[j][t] = v4f{};
+#pragma unroll
+  for (int j = 0; j < kMaxUnitsPerWave; ++j) {
+    const int u = wave + kWaves * j;
+    if (u < U) {
+      int k0, k1;
+      part_range(u % kParts, k0, k1);
+#pragma unroll
+      for (int ks = 0; ks < kMaxPartSteps; ++ks) {
+        if (ks < k1 - k0) {
+          const int c = 4 * (k0 + ks) + kq;
+          const v8b bw = __builtin_bit_cast(v8b, bq[j][ks]);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int rr = 16 * t + r16;
+            const v8b a = *reinterpret_cast<const v8b *>(smem + rr * (kChunks * 16) + 16 * (c ^ r16));
+            acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bw, acc[j][t], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  // Partials through LDS (x no longer read), slot = unit index.
+  __syncthreads();
+  float *slots = reinterpret_cast<float *>(smem);
+#pragma unroll
+  for (int j = 0; j < kMaxUnitsPerWave; ++j) {
+    const int u = wave + kWaves * j;
+    if (u < U) {
+      float *d = slots + u * kSlotFloats;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d[(t * 4 + i) * 64 + lane] = acc[j][t][i];
+    }
+  }
+  __syncthreads();
+
+  // Epilogue: wave e < np sums tile p0 + e's eight parts in order, adds the
+  // bias and writes y (fp32 sum + bias, rounded once, as the GEMM epilogue).
+  if (wave >= np) return;
+  float sum[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sum[t][i] = 0.f;
+  for (int part = 0; part < kParts; ++part) {
+    const float *d = slots + (wave * kParts + part) * kSlotFloats;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sum[t][i] += d[(t * 4 + i) * 64 + lane];
+  }
+  const int col = 16 * (p0 + wave) + r16;
+  const float bv = bias ? elem_to_f32<SPK_BF16>(bias[col]) : 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = m0 + 16 * t + 4 * kq + i;
+      if (row < M) y[static_cast<int64_t>(row) * N + col] = f32_to_elem<SPK_BF16>(sum[t][i] + bv);
+    }
+}
+
+__global__ __launch_bounds__(256) void linear_pack_kernel(const uint16_t *w, v4u *out, int N, int K) {
+  const int KS = K / 32;
+  const int64_t total = static_cast<int64_t>(N / 16) * KS * 64;
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int l = static_cast<int>(e & 63);
+    const int64_t blk = e >> 6;
+    const int ks = static_cast<int>(blk % KS);
+    const int64_t p = blk / KS;
+    out[e] = *reinterpret_cast<const v4u *>(w + (16 * p + (l & 15)) * K + 32 * ks + 8 * (l >> 4));
+  }
+}
+
+}  // namespace lin
+
+extern "C" int spk_linear_pack(const void *w, int N, int K, int dtype, void *w_packed, void *stream) {
+  if (dtype != SPK_BF16) return fail(SPK_EUNSUPPORTED, "linear_pack: bf16 weights only");
+  if (N <= 0 || K <= 0 || N % 16 || K % 32)
+    return fail(SPK_EINVAL, "linear_pack: N=%d K=%d (need multiples of 16 and 32)", N, K);
+  if ((reinterpret_cast<uintptr_t>(w) & 15) || (reinterpret_cast<uintptr_t>(w_packed) & 15))
+    return fail(SPK_EINVAL, "linear_pack: pointers must be 16-byte aligned");
+  lin::linear_pack_kernel<<<1024, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t *>(w), static_cast<lin::v4u *>(w_packed), N, K);
+  return check_launch("linear_pack");
+}
+
+extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void *bias, void *y,
+                                 int M, int N, int K, int dtype, void *stream) {
+  if (dtype != SPK_BF16) return fail(SPK_EUNSUPPORTED, "linear_decode: bf16 only");
+  if (M < 1 || M > 4 * lin::kRows || N < 16 || N % 16 || K % 128 ||
+      K > lin::kParts * lin::kMaxPartSteps * 32 || static_cast<int64_t>(lin::kRows) * K * 2 > lin::kLdsBytes)
+    return fail(SPK_EUNSUPPORTED, "linear_decode: M=%d N=%d K=%d not supported", M, N, K);
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w_packed) & 15))
+    return fail(SPK_EINVAL, "linear_decode: x and packed weights must be 16-byte aligned");
+  const int MG = (M + lin::kRows - 1) / lin::kRows;
+  // Column ranges: a multiple of 8 (one per XCD), about 256 workgroups in all,
+  // and at most two 16-column tiles each.
+  const int P = N / 16;
+  int R = ((256 / MG) + 7) / 8 * 8;
+  while (R * lin::kMaxUnitsPerWave < P) R += 8;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(lin::linear_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lin::kLdsBytes) != hipSuccess)
+      return fail(SPK_EHIP, "linear_decode: cannot reserve %d bytes of LDS", lin::kLdsBytes);
+    attr = true;
+  }
+  lin::linear_kernel<<<MG * R, lin::kThreads, lin::kLdsBytes, s>>>(
+      static_cast<const uint16_t *>(x), static_cast<const lin::v4u *>(w_packed),
+      static_cast<const uint16_t *>(bias), static_cast<uint16_t *>(y), M, N, K, MG, R);
+  return check_launch("linear_decode");
+}
+
+}  // namespace spk

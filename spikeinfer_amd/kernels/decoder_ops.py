@@ -301,6 +301,43 @@ def pack_gate_up(w_gu: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def pack_linear(w: torch.Tensor) -> torch.Tensor:
+    """Reorders a bf16 weight ``[N, K]`` into the operand order of
+    :func:`linear_decode`; done once per weight."""
+    dev = _lib.require_gpu(w)
+    if w.ndim != 2 or w.dtype != torch.bfloat16 or not w.is_contiguous():
+        raise ValueError("w must be a contiguous bf16 [N, K] tensor")
+    N, K = w.shape
+    if N % 16 or K % 32:
+        raise ValueError(f"w shape {tuple(w.shape)}: N must be a multiple of 16, K of 32")
+    out = torch.empty_like(w)
+    _lib.check(_lib.load().spk_linear_pack(w.data_ptr(), N, K, _lib.dtype_code(w.dtype), out.data_ptr(),
+                                           _lib.stream_of(dev)), "linear_pack")
+    return out
+
+
+def linear_decode(x: torch.Tensor, w_packed: torch.Tensor, bias: torch.Tensor | None = None
+                  ) -> torch.Tensor | None:
+    """``x @ W^T (+ bias)`` for a decode-sized ``x [..., K]`` (at most 256 rows)
+    from :func:`pack_linear`'s weight; None when the shape is outside the
+    kernel's range (the caller then uses ``F.linear``)."""
+    dev = _lib.require_gpu(x, w_packed, bias)
+    if x.dtype != torch.bfloat16 or w_packed.ndim != 2 or w_packed.shape[1] != x.shape[-1]:
+        raise ValueError("x must be bf16 [..., K] and w_packed [N, K]")
+    N, K = w_packed.shape
+    if bias is not None and (bias.numel() != N or bias.dtype != torch.bfloat16):
+        raise ValueError(f"bias must be bf16 with {N} entries")
+    x2 = x.reshape(-1, K).contiguous()
+    y = torch.empty((x2.shape[0], N), dtype=x.dtype, device=dev)
+    rc = _lib.load().spk_linear_decode(
+        x2.data_ptr(), w_packed.data_ptr(), bias.contiguous().data_ptr() if bias is not None else None,
+        y.data_ptr(), x2.shape[0], N, K, _lib.dtype_code(x.dtype), _lib.stream_of(dev))
+    if rc == _lib.SPK_EUNSUPPORTED:
+        return None
+    _lib.check(rc, "linear_decode")
+    return y.view(*x.shape[:-1], N)
+
+
 def mlp_gate_lif(x: torch.Tensor, w_packed: torch.Tensor, beta: torch.Tensor,
                  threshold: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor | None:
     """``LIF(x @ W_g^T) * (x @ W_u^T)`` for ``x [T, n_tok, hidden]`` in one

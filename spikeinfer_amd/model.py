@@ -27,9 +27,9 @@ import torch
 import torch.nn.functional as F
 
 from .attention import AttentionMetadata
-from .kernels.decoder_ops import (add_rmsnorm, embed_rmsnorm, lif_gate_mul, mlp_gate_lif,
-                                  pack_gate_up, qkv_decode_attention, qkv_rope_lif_pack,
-                                  rmsnorm_mean_t)
+from .kernels.decoder_ops import (add_rmsnorm, embed_rmsnorm, lif_gate_mul, linear_decode,
+                                  mlp_gate_lif, pack_gate_up, pack_linear, qkv_decode_attention,
+                                  qkv_rope_lif_pack, rmsnorm_mean_t)
 from .kernels.packing import packed_width
 from .kernels.spike_attention import gather_kv_unpacked, paged_spike_attn_decode
 
@@ -57,7 +57,8 @@ class SpikingQwenConfig:
 
 class _Layer:
     __slots__ = ("input_norm", "post_norm", "w_qkv", "b_qkv", "lif_qkv_beta", "lif_qkv_th",
-                 "w_o", "w_gu", "lif_gate_beta", "lif_gate_th", "w_down", "w_gu_packed")
+                 "w_o", "w_gu", "lif_gate_beta", "lif_gate_th", "w_down", "w_gu_packed",
+                 "w_qkv_packed", "w_o_packed")
 
 
 class SpikingDecoder:
@@ -107,6 +108,9 @@ class SpikingDecoder:
         # repacked copy of w_gu); False keeps the GEMM + lif_gate_mul.
         self.fused_mlp = True
         self.fused_mlp_max_tokens = 64
+        # The same batches run the q/k/v and o projections through
+        # linear_decode (repacked copies of w_qkv, w_o); False keeps F.linear.
+        self.small_linear = True
         self._pack_mlp()
         # Rotary inverse frequencies as Qwen2RotaryEmbedding builds them (fp32, host).
         exps = torch.arange(0, self.D, 2, dtype=torch.int64).float() / self.D
@@ -143,14 +147,25 @@ class SpikingDecoder:
         self._pack_mlp()
 
     def _pack_mlp(self) -> None:
-        """The fused MLP gate's operand-order copy of each w_gu (bf16 only)."""
+        """Operand-order copies of w_gu (fused MLP gate) and of w_qkv, w_o
+        (linear_decode); bf16 only."""
         for L in self.layers:
-            L.w_gu_packed = None
-            if self.dtype == torch.bfloat16:
+            L.w_gu_packed = L.w_qkv_packed = L.w_o_packed = None
+            if self.dtype != torch.bfloat16:
+                continue
+            for name, fn in (("w_gu", pack_gate_up), ("w_qkv", pack_linear), ("w_o", pack_linear)):
                 try:
-                    L.w_gu_packed = pack_gate_up(L.w_gu)
+                    setattr(L, name + "_packed", fn(getattr(L, name)))
                 except ValueError:
                     pass
+
+    def _linear(self, x: torch.Tensor, w: torch.Tensor, b, wp, n: int) -> torch.Tensor:
+        """F.linear, or linear_decode for batches of at most fused_mlp_max_tokens."""
+        if self.small_linear and wp is not None and n <= self.fused_mlp_max_tokens:
+            y = linear_decode(x, wp, b)
+            if y is not None:
+                return y
+        return F.linear(x, w, b)
 
     @property
     def weight_bytes(self) -> int:
@@ -159,7 +174,7 @@ class SpikingDecoder:
         n = self.lm_head.numel() + self.final_norm.numel()
         for L in self.layers:
             for name in _Layer.__slots__:
-                if name != "w_gu_packed":  # a step reads it instead of w_gu, not as well
+                if not name.endswith("_packed"):  # a step reads these instead of the originals
                     n += getattr(L, name).numel()
         return n * self.lm_head.element_size()
 
@@ -203,7 +218,7 @@ class SpikingDecoder:
             if i:
                 x = add_rmsnorm(h, delta, L.input_norm, c.rms_norm_eps, out=x)
             k_cache, v_cache = kv_caches[i]
-            qkv = F.linear(x, L.w_qkv, L.b_qkv)
+            qkv = self._linear(x, L.w_qkv, L.b_qkv, L.w_qkv_packed, n)
             fused = (self.fused_attention and not meta.num_prefills and n_dec == n and
                      qkv_decode_attention(qkv, self.rope_cos, self.rope_sin, positions, L.lif_qkv_beta,
                                           L.lif_qkv_th, k_cache, v_cache, meta.slot_mapping,
@@ -219,7 +234,7 @@ class SpikingDecoder:
                                         num_kv_heads=Hkv, out=attn[:, :n_dec])
             if meta.num_prefills:
                 self._prefill_attention(dense, k_cache, v_cache, meta, attn)
-            o = F.linear(attn.view(T, n, Hq * D), L.w_o)
+            o = self._linear(attn.view(T, n, Hq * D), L.w_o, None, L.w_o_packed, n)
             x = add_rmsnorm(h, o, L.post_norm, c.rms_norm_eps, out=x)
             y = None
             if self.fused_mlp and L.w_gu_packed is not None and n <= self.fused_mlp_max_tokens:

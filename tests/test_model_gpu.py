@@ -277,15 +277,46 @@ def test_mlp_gate_lif_unsupported_shapes_return_none(gpu):
         assert mlp_gate_lif(x, pack_gate_up(w), b, b) is None
 
 
+@pytest.mark.parametrize("M,N,K,bias", [(256, 1152, 896, True), (256, 896, 896, False),
+                                         (44, 1152, 896, True), (4, 896, 896, False),
+                                         (130, 512, 1280, True), (64, 48, 128, False)])
+def test_linear_decode_within_one_ulp(gpu, M, N, K, bias):
+    """Small-M linear against the fp64 product rounded to bf16: every output
+    within 1 bf16 ulp (fp32 sums in a different order may round the other
+    way at a rounding boundary)."""
+    from spikeinfer_amd.kernels.decoder_ops import linear_decode, pack_linear
+
+    print(f"linear_decode M={M} N={N} K={K} bias={bias}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(M + N + K)
+    x = torch.randn((M, K), generator=g, device=gpu).bfloat16()
+    w = (torch.randn((N, K), generator=g, device=gpu) * 0.05).bfloat16()
+    b = (torch.randn(N, generator=g, device=gpu) * 0.1).bfloat16() if bias else None
+    got = linear_decode(x.view(1, M, K), pack_linear(w), b)
+    assert got is not None and got.shape == (1, M, N)
+    want = (x.double() @ w.double().t() + (b.double() if bias else 0)).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    d = (got[0].float() - want.float()).abs()
+    assert bool((d <= want.float().abs() * 2.0 ** -7 + 1e-6).all()), f"max diff {float(d.max())}"
+
+
+def test_linear_decode_unsupported_shapes_return_none(gpu):
+    from spikeinfer_amd.kernels.decoder_ops import linear_decode, pack_linear
+
+    for M, N, K in ((257, 896, 896), (8, 896, 1408), (8, 896, 192)):
+        w = torch.zeros((N, K), device=gpu, dtype=torch.bfloat16)
+        assert linear_decode(torch.zeros((M, K), device=gpu, dtype=torch.bfloat16), pack_linear(w)) is None
+
+
 def test_model_fused_mlp_matches_two_launches(gpu):
-    """A decode step with the fused MLP gate against the GEMM + lif_gate_mul
-    path (the GEMM sums differ in order only): same tolerances as the
-    reference-forward check."""
+    """A decode step with the fused MLP gate and the small-M projections
+    against F.linear + lif_gate_mul (the GEMM sums differ in order only): same
+    tolerances as the reference-forward check."""
     cfg = SpikingQwenConfig(vocab_size=1024, hidden_size=512, intermediate_size=1024,
                             num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
                             head_dim=64)
     m = SpikingDecoder(cfg, device=gpu, seed=9, init_std=0.06)
-    assert all(L.w_gu_packed is not None for L in m.layers)
+    assert all(L.w_gu_packed is not None and L.w_qkv_packed is not None and L.w_o_packed is not None
+               for L in m.layers)
     bs, n = 16, 11
     g = torch.Generator().manual_seed(8)
     lens = torch.randint(5, 60, (n,), generator=g)
@@ -303,9 +334,9 @@ def test_model_fused_mlp_matches_two_launches(gpu):
         v1.copy_(v0)
     outs = []
     for fused, c in zip((True, False), caches):
-        m.fused_mlp = fused
+        m.fused_mlp = m.small_linear = fused
         outs.append(m.forward_paged(ids, pos.to(gpu), c.layers, meta))
-    m.fused_mlp = True
+    m.fused_mlp = m.small_linear = True
     torch.cuda.synchronize()
     _compare(outs[0], outs[1], caches[0], caches[1], m)
 
