@@ -160,6 +160,98 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
 }
 
+// Wide N (the lm_head: 151,936 columns) at M <= 64: the x rows stay in LDS for
+// the whole launch and each wave runs whole-K pairs of 16-column tiles,
+// streaming W through a register ring of up to 10 k-steps; no cross-wave sums.
+// LDS rows are padded by one 16-byte chunk instead of swizzled (row stride
+// = 16 mod 256 bytes: 16 consecutive rows still hit 16 distinct bank groups),
+// so a k-step's fragment address is a per-row-tile base plus an immediate;
+// with the swizzle every (k-step, row tile) address is its own register.
+// Ring depth: up to 10 k-steps of W in flight per wave (a divisor of KS).
+constexpr int ring_depth(int ks) {
+  for (int d = 10; d > 1; --d)
+    if (ks % d == 0) return d;
+  return 1;
+}
+template <int KS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void linear_wide_kernel(
+    const uint16_t *x, const v4u *wp, const uint16_t *bias, uint16_t *y, int M, int N) {
+  extern __shared__ __align__(16) char smem[];
+  constexpr int K = 32 * KS, kChunks = K / 8, kRowChunks = kChunks + 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int PP = N / 32;  // tile pairs
+  const int q0 = static_cast<int>(static_cast<int64_t>(blockIdx.x) * PP / gridDim.x);
+  const int q1 = static_cast<int>(static_cast<int64_t>(blockIdx.x + 1) * PP / gridDim.x);
+  // All 64 rows (clamped copies past M): a branch per row tile would put
+  // control flow between every MFMA, which costs more registers than the
+  // unused products cost time in this memory-bound kernel.
+  for (int base = wave * 64; base < kRows * kRowChunks; base += kWaves * 64) {
+    const int g = base + lane;
+    const int rr = g / kRowChunks, pc = g - rr * kRowChunks;
+    const int row = min(rr, M - 1);
+    const int c = pc < kChunks ? pc : 0;  // the pad chunk loads a copy of chunk 0
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(x + static_cast<int64_t>(row) * K + 8 * c),
+                                     (SPK_LDS void *)(smem + base * 16), 16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+  __syncthreads();
+  const int r16 = lane & 15, kq = lane >> 4;
+  const char *abase = smem + r16 * (kRowChunks * 16) + 16 * kq;  // row r16 of tile 0, chunk kq
+  // W through a buffer resource: the lane's byte offset in a VGPR, the
+  // k-step's (1 KB apart) in an SGPR, so the ring costs no address registers.
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<v4u *>(wp), 0, -1, 0x00020000);
+  auto wload = [&](int vofs, int ks) {
+    return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs, vofs, ks * 1024, 0));
+  };
+  constexpr int D = ring_depth(KS);
+  for (int q = q0 + wave; q < q1; q += kWaves) {
+    const int vofs0 = (2 * q * KS * 64 + lane) * 16, vofs1 = vofs0 + KS * 1024;
+    // Ring of D k-steps: slot ks % D is read by k-step ks's MFMAs and then
+    // refilled with k-step ks + D.
+    v4u r0[D], r1[D];
+#pragma unroll
+    for (int ks = 0; ks < D; ++ks) {
+      r0[ks] = wload(vofs0, ks);
+      r1[ks] = wload(vofs1, ks);
+    }
+    v4f acc0[4], acc1[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc0[t] = acc1[t] = v4f{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      // Keeps each k-step's LDS reads with its MFMAs: hoisted, the reads of
+      // every k-step would be live at once and spill.
+      __builtin_amdgcn_sched_barrier(0);
+      const int slot = ks % D;
+      const v8b w0 = __builtin_bit_cast(v8b, r0[slot]), w1 = __builtin_bit_cast(v8b, r1[slot]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const v8b a = *reinterpret_cast<const v8b *>(abase + t * (16 * kRowChunks * 16) + 64 * ks);
+        acc0[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, w0, acc0[t], 0, 0, 0);
+        acc1[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, w1, acc1[t], 0, 0, 0);
+      }
+      if (ks + D < KS) {
+        r0[slot] = wload(vofs0, ks + D);
+        r1[slot] = wload(vofs1, ks + D);
+      }
+    }
+    const int col = 32 * q + r16;
+    const float bv0 = bias ? elem_to_f32<SPK_BF16>(bias[col]) : 0.f;
+    const float bv1 = bias ? elem_to_f32<SPK_BF16>(bias[col + 16]) : 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * t + 4 * kq + i;
+        if (row < M) {
+          y[static_cast<int64_t>(row) * N + col] = f32_to_elem<SPK_BF16>(acc0[t][i] + bv0);
+          y[static_cast<int64_t>(row) * N + col + 16] = f32_to_elem<SPK_BF16>(acc1[t][i] + bv1);
+        }
+      }
+  }
+}
+
 __global__ __launch_bounds__(256) void linear_pack_kernel(const uint16_t *w, v4u *out, int N, int K) {
   const int KS = K / 32;
   const int64_t total = static_cast<int64_t>(N / 16) * KS * 64;
@@ -199,8 +291,35 @@ extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void
   // and at most two 16-column tiles each.
   const int P = N / 16;
   int R = ((256 / MG) + 7) / 8 * 8;
-  while (R * lin::kMaxUnitsPerWave < P) R += 8;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (MG == 1 && P > lin::kMaxUnitsPerWave * R && N % 32 == 0) {
+    // Wide N: 256 workgroups, each a range of tile pairs.
+#define SPK_WIDE_CASE(KS)                                                                              \
+  case KS: {                                                                                         \
+    static bool attr = false;                                                                        \
+    if (!attr) {                                                                                     \
+      if (hipFuncSetAttribute(reinterpret_cast<const void *>(lin::linear_wide_kernel<KS>),            \
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lin::kLdsBytes) != hipSuccess) \
+        return fail(SPK_EHIP, "linear_decode: cannot reserve %d bytes of LDS", lin::kLdsBytes);      \
+      attr = true;                                                                                   \
+    }                                                                                                \
+    lin::linear_wide_kernel<KS><<<256, lin::kThreads, lin::kLdsBytes, s>>>(                           \
+        static_cast<const uint16_t *>(x), static_cast<const lin::v4u *>(w_packed),                   \
+        static_cast<const uint16_t *>(bias), static_cast<uint16_t *>(y), M, N);                      \
+    return check_launch("linear_decode");                                                           \
+  }
+    switch (K / 32) {
+      SPK_WIDE_CASE(16)
+      SPK_WIDE_CASE(20)
+      SPK_WIDE_CASE(24)
+      SPK_WIDE_CASE(28)
+      SPK_WIDE_CASE(32)
+      SPK_WIDE_CASE(36)
+      SPK_WIDE_CASE(40)
+    }
+#undef SPK_WIDE_CASE
+  }
+  while (R * lin::kMaxUnitsPerWave < P) R += 8;
   static bool attr = false;
   if (!attr) {
     if (hipFuncSetAttribute(reinterpret_cast<const void *>(lin::linear_kernel),

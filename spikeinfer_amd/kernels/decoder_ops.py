@@ -316,26 +316,33 @@ def pack_linear(w: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def linear_decode(x: torch.Tensor, w_packed: torch.Tensor, bias: torch.Tensor | None = None
-                  ) -> torch.Tensor | None:
+def linear_decode(x: torch.Tensor, w_packed: torch.Tensor, bias: torch.Tensor | None = None,
+                  out: torch.Tensor | None = None) -> torch.Tensor | None:
     """``x @ W^T (+ bias)`` for a decode-sized ``x [..., K]`` (at most 256 rows)
-    from :func:`pack_linear`'s weight; None when the shape is outside the
-    kernel's range (the caller then uses ``F.linear``)."""
-    dev = _lib.require_gpu(x, w_packed, bias)
+    from :func:`pack_linear`'s weight, into ``out`` when given (contiguous);
+    None when the shape is outside the kernel's range (the caller then uses
+    ``F.linear``)."""
+    dev = _lib.require_gpu(x, w_packed, bias, out)
     if x.dtype != torch.bfloat16 or w_packed.ndim != 2 or w_packed.shape[1] != x.shape[-1]:
         raise ValueError("x must be bf16 [..., K] and w_packed [N, K]")
     N, K = w_packed.shape
     if bias is not None and (bias.numel() != N or bias.dtype != torch.bfloat16):
         raise ValueError(f"bias must be bf16 with {N} entries")
     x2 = x.reshape(-1, K).contiguous()
-    y = torch.empty((x2.shape[0], N), dtype=x.dtype, device=dev)
+    if out is None:
+        y = torch.empty((x2.shape[0], N), dtype=x.dtype, device=dev)
+    elif out.shape[-1] != N or out.numel() != x2.shape[0] * N or not out.is_contiguous() \
+            or out.dtype != x.dtype:
+        raise ValueError(f"out must be a contiguous {x.dtype} tensor of {x2.shape[0]} x {N}")
+    else:
+        y = out
     rc = _lib.load().spk_linear_decode(
         x2.data_ptr(), w_packed.data_ptr(), bias.contiguous().data_ptr() if bias is not None else None,
         y.data_ptr(), x2.shape[0], N, K, _lib.dtype_code(x.dtype), _lib.stream_of(dev))
     if rc == _lib.SPK_EUNSUPPORTED:
         return None
     _lib.check(rc, "linear_decode")
-    return y.view(*x.shape[:-1], N)
+    return y if out is not None else y.view(*x.shape[:-1], N)
 
 
 def mlp_gate_lif(x: torch.Tensor, w_packed: torch.Tensor, beta: torch.Tensor,

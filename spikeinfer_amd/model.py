@@ -147,8 +147,14 @@ class SpikingDecoder:
         self._pack_mlp()
 
     def _pack_mlp(self) -> None:
-        """Operand-order copies of w_gu (fused MLP gate) and of w_qkv, w_o
-        (linear_decode); bf16 only."""
+        """Operand-order copies of w_gu (fused MLP gate) and of w_qkv, w_o and
+        the lm_head (linear_decode); bf16 only."""
+        self.lm_head_packed = None
+        if self.dtype == torch.bfloat16:
+            try:
+                self.lm_head_packed = pack_linear(self.lm_head)
+            except ValueError:
+                pass
         for L in self.layers:
             L.w_gu_packed = L.w_qkv_packed = L.w_o_packed = None
             if self.dtype != torch.bfloat16:
@@ -283,6 +289,10 @@ class SpikingDecoder:
         """lm_head on the rows that sample (modeling_fast.py:335-355)."""
         if indices is not None:
             hidden = hidden.index_select(0, indices)
+        if self.small_linear and self.lm_head_packed is not None and hidden.shape[0] <= 64:
+            y = linear_decode(hidden, self.lm_head_packed, None, out)
+            if y is not None:
+                return y
         if out is None:
             return F.linear(hidden, self.lm_head)
         return torch.matmul(hidden, self.lm_head.t(), out=out)

@@ -279,11 +279,13 @@ def test_mlp_gate_lif_unsupported_shapes_return_none(gpu):
 
 @pytest.mark.parametrize("M,N,K,bias", [(256, 1152, 896, True), (256, 896, 896, False),
                                          (44, 1152, 896, True), (4, 896, 896, False),
-                                         (130, 512, 1280, True), (64, 48, 128, False)])
+                                         (130, 512, 1280, True), (64, 48, 128, False),
+                                         (64, 151936, 896, False), (5, 20480, 640, True)])
 def test_linear_decode_within_one_ulp(gpu, M, N, K, bias):
     """Small-M linear against the fp64 product rounded to bf16: every output
     within 1 bf16 ulp (fp32 sums in a different order may round the other
-    way at a rounding boundary)."""
+    way at a rounding boundary).  The last two shapes take the wide-N path
+    (the lm_head)."""
     from spikeinfer_amd.kernels.decoder_ops import linear_decode, pack_linear
 
     print(f"linear_decode M={M} N={N} K={K} bias={bias}", flush=True)
@@ -291,8 +293,9 @@ def test_linear_decode_within_one_ulp(gpu, M, N, K, bias):
     x = torch.randn((M, K), generator=g, device=gpu).bfloat16()
     w = (torch.randn((N, K), generator=g, device=gpu) * 0.05).bfloat16()
     b = (torch.randn(N, generator=g, device=gpu) * 0.1).bfloat16() if bias else None
-    got = linear_decode(x.view(1, M, K), pack_linear(w), b)
-    assert got is not None and got.shape == (1, M, N)
+    out = torch.empty((1, M, N), device=gpu, dtype=torch.bfloat16)
+    got = linear_decode(x.view(1, M, K), pack_linear(w), b, out=out)
+    assert got is out
     want = (x.double() @ w.double().t() + (b.double() if bias else 0)).to(torch.bfloat16)
     torch.cuda.synchronize()
     d = (got[0].float() - want.float()).abs()
