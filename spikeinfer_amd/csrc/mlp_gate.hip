@@ -55,10 +55,12 @@ constexpr int kSlotFloats = 2 * kMaxT * 4 * 64;  // one partial: 2 tiles x T row
 // KB: lane l's 16 bytes are W[row][32ks + 8(l/16) .. +7], row = 16p + l%16
 // (+ I for up).
 
-template <int KQ>
+// T is a template parameter: a runtime test per row tile would put branches
+// between the MFMAs (and the accumulator copies they bring cost registers).
+template <int KQ, int T>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void mlp_gate_lif_kernel(
     const uint16_t *x, const v4u *wp, const void *beta_p, const void *th_p, int param_dtype,
-    uint16_t *y, int T, int n, int I, int MG) {
+    uint16_t *y, int n, int I, int MG) {
   constexpr int KS = 4 * KQ;       // k-steps of 32 (H = 32 KS)
   constexpr int H = 32 * KS;
   constexpr int kChunks = 4 * KS;  // 16-byte chunks per x row
@@ -120,13 +122,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       const v8b bg = __builtin_bit_cast(v8b, bq[ks][0]);
       const v8b bu = __builtin_bit_cast(v8b, bq[ks][1]);
 #pragma unroll
-      for (int t = 0; t < kMaxT; ++t) {
-        if (t < T) {
-          const int rr = 16 * t + r16;
-          const v8b a = *reinterpret_cast<const v8b *>(smem + rr * (kChunks * 16) + 16 * (c ^ r16));
-          accg[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bg, accg[t], 0, 0, 0);
-          accu[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bu, accu[t], 0, 0, 0);
-        }
+      for (int t = 0; t < T; ++t) {
+        const int rr = 16 * t + r16;
+        const v8b a = *reinterpret_cast<const v8b *>(smem + rr * (kChunks * 16) + 16 * (c ^ r16));
+        accg[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bg, accg[t], 0, 0, 0);
+        accu[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bu, accu[t], 0, 0, 0);
       }
     }
   };
@@ -218,8 +218,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     if (tok >= n) continue;
     float u = 0.f;
 #pragma unroll
-    for (int t = 0; t < kMaxT; ++t) {
-      if (t >= T) break;
+    for (int t = 0; t < T; ++t) {
       const float g = round_to<SPK_BF16>(sg[t][j]);
       const float up = round_to<SPK_BF16>(su[t][j]);
       const bool spike = lif_step(u, g, beta, th[0]);
@@ -289,19 +288,25 @@ extern "C" int spk_mlp_gate_lif(const void *x, const void *w_packed, const void 
   const auto *xp = static_cast<const uint16_t *>(x);
   const auto *wp = static_cast<const mlp::v4u *>(w_packed);
   auto *yp = static_cast<uint16_t *>(y);
-#define SPK_MLP_CASE(KQ)                                                                             \
-  case KQ: {                                                                                       \
+#define SPK_MLP_LAUNCH(KQ, TT)                                                                       \
+  {                                                                                                \
     static bool attr = false;                                                                      \
     if (!attr) {                                                                                   \
-      if (hipFuncSetAttribute(reinterpret_cast<const void *>(mlp::mlp_gate_lif_kernel<KQ>),         \
+      if (hipFuncSetAttribute(reinterpret_cast<const void *>(mlp::mlp_gate_lif_kernel<KQ, TT>),     \
                               hipFuncAttributeMaxDynamicSharedMemorySize, mlp::kLdsBytes) != hipSuccess) \
         return fail(SPK_EHIP, "mlp_gate_lif: cannot reserve %d bytes of LDS", mlp::kLdsBytes);  \
       attr = true;                                                                                 \
     }                                                                                              \
-    mlp::mlp_gate_lif_kernel<KQ><<<grid, mlp::kThreads, mlp::kLdsBytes, s>>>(                       \
-        xp, wp, beta, threshold, param_dtype, yp, T, n_tok, inter, MG);                            \
-    break;                                                                                         \
+    mlp::mlp_gate_lif_kernel<KQ, TT><<<grid, mlp::kThreads, mlp::kLdsBytes, s>>>(                   \
+        xp, wp, beta, threshold, param_dtype, yp, n_tok, inter, MG);                               \
   }
+#define SPK_MLP_CASE(KQ)                                                                             \
+  case KQ:                                                                                         \
+    if (T == 1) SPK_MLP_LAUNCH(KQ, 1)                                                             \
+    else if (T == 2) SPK_MLP_LAUNCH(KQ, 2)                                                        \
+    else if (T == 3) SPK_MLP_LAUNCH(KQ, 3)                                                        \
+    else SPK_MLP_LAUNCH(KQ, 4)                                                                     \
+    break;
   switch (hidden / 128) {
     SPK_MLP_CASE(4)
     SPK_MLP_CASE(5)
@@ -310,6 +315,7 @@ extern "C" int spk_mlp_gate_lif(const void *x, const void *w_packed, const void 
     SPK_MLP_CASE(8)
   }
 #undef SPK_MLP_CASE
+#undef SPK_MLP_LAUNCH
   return check_launch("mlp_gate_lif");
 }
 
