@@ -229,19 +229,19 @@ def bench_lif(steps, warmup, dev):
     }
 
 
-def bench_decode_step(steps, warmup, dev):
+def bench_decode_step(steps, warmup, dev, batch=64):
     """Config 5: random-init Qwen2.5-0.5B-shaped spiking decoder (bf16 weights
     N(0, 0.02)), batch 64, 128-token random prompts, T=4; one decode step
     (24 layers + lm_head + sampling with temperature 0.8 / top-k 50 / top-p 0.9
     / repetition 1.1 + device-side advance) replayed from one hipGraph.  Prefill
-    is eager and untimed.  tok/s = 64 tokens per step / step time."""
+    is eager and untimed.  tok/s = batch tokens per step / step time."""
     from spikeinfer_amd.model import SpikingDecoder, SpikingQwenConfig
     from spikeinfer_amd.runner import DecodeRunner
     from spikeinfer_amd.sampler import SamplingParams
     from spikeinfer_amd.spike_cache import PagedSpikeCache
 
     cfg = SpikingQwenConfig()
-    B, plen = 64, 128
+    B, plen = batch, 128
     new = warmup + steps + 1
     model = SpikingDecoder(cfg, device=dev, seed=5000)
     max_len = plen + new + 1
@@ -334,6 +334,8 @@ def main():
         extras["config2_lif"] = bench_lif(args.steps, args.warmup, dev)
         print("config 5", file=sys.stderr, flush=True)
         extras["config5_decode"] = bench_decode_step(args.steps, args.warmup, dev)
+        small = bench_decode_step(args.steps, args.warmup, dev, batch=8)
+        extras["config5_decode_batch8"] = {k: small[k] for k in ("decode_tok_s", "ms_per_step")}
     if args.calib_copy_mib:
         src = torch.empty(args.calib_copy_mib << 18, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)

@@ -304,9 +304,9 @@ size_t spk_mlp_gate_packed_bytes(int hidden, int inter);
  * (spikeinfer/modeling_fast.py:121-135, :150-166) in place of a library GEMM.
  * spk_linear_pack reorders W [N, K] (bf16, contiguous) into the kernel's operand
  * order (N * K * 2 bytes at w_packed), once per weight.  spk_linear_decode
- * supports M <= 256, N a multiple of 16, K a multiple of 128 up to 1280, bf16
- * (SPK_EUNSUPPORTED otherwise); sums are fp32 in a fixed order, bias added, then
- * rounded once.
+ * supports M <= 256, N a multiple of 16, K a multiple of 128 up to 1280, or up
+ * to 5120 without a bias (the down projection), bf16 (SPK_EUNSUPPORTED
+ * otherwise); sums are fp32 in a fixed order, bias added, then rounded once.
  */
 int spk_linear_pack(const void *w, int N, int K, int dtype, void *w_packed, void *stream);
 int spk_linear_decode(const void *x, const void *w_packed, const void *bias, void *y, int M, int N,

@@ -1,6 +1,8 @@
 // Small-M linear layer of the decode step: y = x @ W^T (+ bias), bf16, for the
-// q/k/v and o projections (spikeinfer/modeling_fast.py:121-135, :150-166) at
-// decode batch sizes (M = T * n_tok <= 256 rows, K <= 1280).
+// q/k/v, o, down and lm_head projections (spikeinfer/modeling_fast.py:121-135,
+// :150-166, :190, :335-355) at decode batch sizes (M = T * n_tok <= 256 rows).
+// Three launch shapes: the tiled kernel below (K <= 1280), a wide-N variant
+// (the lm_head) and a long-K variant with 16-row groups (the down projection).
 //
 // MI355X design (the same ground rules as the fused MLP gate in mlp_gate.hip):
 // at these sizes a projection is bound by moving x and W into the CUs and by
@@ -252,6 +254,102 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   }
 }
 
+// Long K (the down projection, K = 4864) at M <= 256: 16 rows of x per
+// workgroup (16 * K * 2 <= 160 KB of LDS), 3-4 column tiles per workgroup, and
+// the 8 waves split K into eighths.  Each wave streams its k-steps of W in
+// chunks of 4 through a double buffer (branch-free: a chunk past the wave's
+// range multiplies a zero B), then the eight partials of each tile are added
+// in wave order through LDS.
+constexpr int kTallRows = 16;
+constexpr int kTallChunk = 4;  // k-steps per chunk
+template <int NP>
+__device__ __forceinline__ void linear_tall_run(const v4u *wp, uint16_t *y, int M, int N, int KS,
+                                                int m0, int p0, char *smem) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kChunks = 4 * KS;  // 16-byte chunks per x row
+  const int r16 = lane & 15, kq = lane >> 4;
+  const int k0 = wave * KS / kWaves, nk = (wave + 1) * KS / kWaves - k0;
+  const int nc = ((nk + kTallChunk - 1) / kTallChunk + 1) & ~1;  // chunks, even
+  auto load = [&](int c, v4u (&b)[kTallChunk][NP]) {
+#pragma unroll
+    for (int j = 0; j < kTallChunk; ++j) {
+      const int ks = k0 + min(c * kTallChunk + j, nk - 1);
+#pragma unroll
+      for (int t = 0; t < NP; ++t) b[j][t] = wp[(static_cast<int64_t>(p0 + t) * KS + ks) * 64 + lane];
+    }
+  };
+  v4f acc[NP];
+#pragma unroll
+  for (int t = 0; t < NP; ++t) acc[t] = v4f{};
+  auto compute = [&](int c, const v4u (&b)[kTallChunk][NP]) {
+#pragma unroll
+    for (int j = 0; j < kTallChunk; ++j) {
+      const int kk = c * kTallChunk + j;
+      const int ks = k0 + min(kk, nk - 1);
+      const int ch = 4 * ks + kq;
+      const v8b a = *reinterpret_cast<const v8b *>(smem + r16 * (kChunks * 16) + 16 * (ch ^ r16));
+#pragma unroll
+      for (int t = 0; t < NP; ++t) {
+        const v4u bz = kk < nk ? b[j][t] : v4u{0u, 0u, 0u, 0u};
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(v8b, bz), acc[t], 0, 0, 0);
+      }
+    }
+  };
+  v4u bA[kTallChunk][NP], bB[kTallChunk][NP];
+  load(0, bA);
+  for (int c = 0; c < nc; c += 2) {
+    load(c + 1, bB);
+    compute(c, bA);
+    load(c + 2, bA);  // past the end: clamped re-reads, never used
+    compute(c + 1, bB);
+  }
+  __syncthreads();  // every wave is done with the x rows: the LDS takes the partials
+  float *slots = reinterpret_cast<float *>(smem);
+#pragma unroll
+  for (int t = 0; t < NP; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) slots[((wave * NP + t) * 4 + i) * 64 + lane] = acc[t][i];
+  __syncthreads();
+  if (wave >= NP) return;
+  float sum[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sum[i] += slots[((w * NP + wave) * 4 + i) * 64 + lane];
+  const int col = 16 * (p0 + wave) + r16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = m0 + 4 * kq + i;
+    if (row < M) y[static_cast<int64_t>(row) * N + col] = f32_to_elem<SPK_BF16>(sum[i]);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void linear_tall_kernel(
+    const uint16_t *x, const v4u *wp, uint16_t *y, int M, int N, int K, int MG, int R) {
+  extern __shared__ __align__(16) char smem[];
+  const int KS = K / 32, kChunks = K / 8;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x, xcd = b & 7, s = b >> 3;
+  const int m = s % MG, r = (s / MG) * 8 + xcd;
+  const int P = N / 16;
+  const int p0 = r * P / R, np = (r + 1) * P / R - p0;
+  if (np <= 0) return;  // uniform over the workgroup
+  const int m0 = m * kTallRows;
+  for (int base = wave * 64; base < kTallRows * kChunks; base += kWaves * 64) {
+    const int g = base + lane;
+    const int rr = g / kChunks, pc = g - rr * kChunks;
+    const int c = pc ^ (rr & 15);
+    const int row = min(m0 + rr, M - 1);
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(x + static_cast<int64_t>(row) * K + 8 * c),
+                                     (SPK_LDS void *)(smem + base * 16), 16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+  __syncthreads();
+  if (np == 4) linear_tall_run<4>(wp, y, M, N, KS, m0, p0, smem);
+  else if (np == 3) linear_tall_run<3>(wp, y, M, N, KS, m0, p0, smem);
+  else if (np == 2) linear_tall_run<2>(wp, y, M, N, KS, m0, p0, smem);
+  else linear_tall_run<1>(wp, y, M, N, KS, m0, p0, smem);
+}
+
 __global__ __launch_bounds__(256) void linear_pack_kernel(const uint16_t *w, v4u *out, int N, int K) {
   const int KS = K / 32;
   const int64_t total = static_cast<int64_t>(N / 16) * KS * 64;
@@ -281,6 +379,27 @@ extern "C" int spk_linear_pack(const void *w, int N, int K, int dtype, void *w_p
 extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void *bias, void *y,
                                  int M, int N, int K, int dtype, void *stream) {
   if (dtype != SPK_BF16) return fail(SPK_EUNSUPPORTED, "linear_decode: bf16 only");
+  if (K > lin::kParts * lin::kMaxPartSteps * 32 && !bias && M >= 1 && M <= 4 * lin::kRows &&
+      N >= 16 && N % 16 == 0 && K % 128 == 0 &&
+      static_cast<int64_t>(lin::kTallRows) * K * 2 <= lin::kLdsBytes) {
+    // Long K: 16-row groups, 3-4 tiles per range.
+    if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w_packed) & 15))
+      return fail(SPK_EINVAL, "linear_decode: x and packed weights must be 16-byte aligned");
+    const int MG = (M + lin::kTallRows - 1) / lin::kTallRows;
+    int R = ((256 / MG) + 7) / 8 * 8;
+    while (R * 4 < N / 16) R += 8;
+    static bool attr = false;
+    if (!attr) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void *>(lin::linear_tall_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lin::kLdsBytes) != hipSuccess)
+        return fail(SPK_EHIP, "linear_decode: cannot reserve %d bytes of LDS", lin::kLdsBytes);
+      attr = true;
+    }
+    lin::linear_tall_kernel<<<MG * R, lin::kThreads, lin::kLdsBytes, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint16_t *>(x), static_cast<const lin::v4u *>(w_packed),
+        static_cast<uint16_t *>(y), M, N, K, MG, R);
+    return check_launch("linear_decode");
+  }
   if (M < 1 || M > 4 * lin::kRows || N < 16 || N % 16 || K % 128 ||
       K > lin::kParts * lin::kMaxPartSteps * 32 || static_cast<int64_t>(lin::kRows) * K * 2 > lin::kLdsBytes)
     return fail(SPK_EUNSUPPORTED, "linear_decode: M=%d N=%d K=%d not supported", M, N, K);

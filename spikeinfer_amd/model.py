@@ -58,7 +58,7 @@ class SpikingQwenConfig:
 class _Layer:
     __slots__ = ("input_norm", "post_norm", "w_qkv", "b_qkv", "lif_qkv_beta", "lif_qkv_th",
                  "w_o", "w_gu", "lif_gate_beta", "lif_gate_th", "w_down", "w_gu_packed",
-                 "w_qkv_packed", "w_o_packed")
+                 "w_qkv_packed", "w_o_packed", "w_down_packed")
 
 
 class SpikingDecoder:
@@ -110,7 +110,10 @@ class SpikingDecoder:
         self.fused_mlp_max_tokens = 64
         # The same batches run the q/k/v and o projections through
         # linear_decode (repacked copies of w_qkv, w_o); False keeps F.linear.
+        # The down projection (long K) goes there only up to small_down_max_rows
+        # rows (T * tokens): beyond, the library GEMM is faster.
         self.small_linear = True
+        self.small_down_max_rows = 128
         self._pack_mlp()
         # Rotary inverse frequencies as Qwen2RotaryEmbedding builds them (fp32, host).
         exps = torch.arange(0, self.D, 2, dtype=torch.int64).float() / self.D
@@ -156,10 +159,11 @@ class SpikingDecoder:
             except ValueError:
                 pass
         for L in self.layers:
-            L.w_gu_packed = L.w_qkv_packed = L.w_o_packed = None
+            L.w_gu_packed = L.w_qkv_packed = L.w_o_packed = L.w_down_packed = None
             if self.dtype != torch.bfloat16:
                 continue
-            for name, fn in (("w_gu", pack_gate_up), ("w_qkv", pack_linear), ("w_o", pack_linear)):
+            for name, fn in (("w_gu", pack_gate_up), ("w_qkv", pack_linear), ("w_o", pack_linear),
+                             ("w_down", pack_linear)):
                 try:
                     setattr(L, name + "_packed", fn(getattr(L, name)))
                 except ValueError:
@@ -247,7 +251,11 @@ class SpikingDecoder:
                 y = mlp_gate_lif(x, L.w_gu_packed, L.lif_gate_beta, L.lif_gate_th)
             if y is None:
                 y = lif_gate_mul(F.linear(x, L.w_gu), L.lif_gate_beta, L.lif_gate_th)
-            delta = F.linear(y, L.w_down)
+            delta = None
+            if T * n <= self.small_down_max_rows:
+                delta = self._linear(y, L.w_down, None, L.w_down_packed, n)
+            if delta is None:
+                delta = F.linear(y, L.w_down)
         return rmsnorm_mean_t(h, self.final_norm, c.rms_norm_eps, delta=delta)
 
     def _prefill_attention(self, dense, k_cache, v_cache, meta: AttentionMetadata, attn) -> None:

@@ -280,12 +280,15 @@ def test_mlp_gate_lif_unsupported_shapes_return_none(gpu):
 @pytest.mark.parametrize("M,N,K,bias", [(256, 1152, 896, True), (256, 896, 896, False),
                                          (44, 1152, 896, True), (4, 896, 896, False),
                                          (130, 512, 1280, True), (64, 48, 128, False),
-                                         (64, 151936, 896, False), (5, 20480, 640, True)])
+                                         (64, 151936, 896, False), (5, 20480, 640, True),
+                                         (128, 896, 4864, False), (44, 896, 4864, False),
+                                         (4, 896, 4864, False), (256, 896, 4864, False),
+                                         (20, 64, 2048, False)])
 def test_linear_decode_within_one_ulp(gpu, M, N, K, bias):
     """Small-M linear against the fp64 product rounded to bf16: every output
     within 1 bf16 ulp (fp32 sums in a different order may round the other
-    way at a rounding boundary).  The last two shapes take the wide-N path
-    (the lm_head)."""
+    way at a rounding boundary).  Wide N (the lm_head) and long K (the down
+    projection) take their own paths."""
     from spikeinfer_amd.kernels.decoder_ops import linear_decode, pack_linear
 
     print(f"linear_decode M={M} N={N} K={K} bias={bias}", flush=True)
@@ -305,21 +308,23 @@ def test_linear_decode_within_one_ulp(gpu, M, N, K, bias):
 def test_linear_decode_unsupported_shapes_return_none(gpu):
     from spikeinfer_amd.kernels.decoder_ops import linear_decode, pack_linear
 
-    for M, N, K in ((257, 896, 896), (8, 896, 1408), (8, 896, 192)):
+    for M, N, K, bias in ((257, 896, 896, False), (8, 896, 5248, False), (8, 896, 192, False),
+                          (8, 896, 2048, True)):
         w = torch.zeros((N, K), device=gpu, dtype=torch.bfloat16)
-        assert linear_decode(torch.zeros((M, K), device=gpu, dtype=torch.bfloat16), pack_linear(w)) is None
+        b = torch.zeros(N, device=gpu, dtype=torch.bfloat16) if bias else None
+        assert linear_decode(torch.zeros((M, K), device=gpu, dtype=torch.bfloat16), pack_linear(w), b) is None
 
 
 def test_model_fused_mlp_matches_two_launches(gpu):
     """A decode step with the fused MLP gate and the small-M projections
     against F.linear + lif_gate_mul (the GEMM sums differ in order only): same
     tolerances as the reference-forward check."""
-    cfg = SpikingQwenConfig(vocab_size=1024, hidden_size=512, intermediate_size=1024,
+    cfg = SpikingQwenConfig(vocab_size=1024, hidden_size=512, intermediate_size=2048,
                             num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
                             head_dim=64)
     m = SpikingDecoder(cfg, device=gpu, seed=9, init_std=0.06)
     assert all(L.w_gu_packed is not None and L.w_qkv_packed is not None and L.w_o_packed is not None
-               for L in m.layers)
+               and L.w_down_packed is not None for L in m.layers)
     bs, n = 16, 11
     g = torch.Generator().manual_seed(8)
     lens = torch.randint(5, 60, (n,), generator=g)
