@@ -60,6 +60,31 @@ def test_host_side_validation_without_a_gpu():
     assert lib.spk_pack(None, 9, 1, None, 4, 4, None) == _lib.SPK_EINVAL
 
 
+def test_decode_gemm_entry_points_validate_on_the_host():
+    """The decode GEMM entry points reject unsupported or malformed calls
+    before any launch (fake pointers are never dereferenced)."""
+    lib = _lib.load()
+    bf16, f16, f32 = 2, 1, 0
+    A, B = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x1001)  # 16-byte aligned / not
+    assert lib.spk_linear_pack(None, 20, 896, bf16, None, None) == _lib.SPK_EINVAL
+    assert lib.spk_linear_pack(None, 896, 896, f16, None, None) == _lib.SPK_EUNSUPPORTED
+    assert lib.spk_linear_decode(A, A, None, A, 8, 896, 896, f16, None) == _lib.SPK_EUNSUPPORTED
+    assert lib.spk_linear_decode(A, A, None, A, 300, 896, 896, bf16, None) == _lib.SPK_EUNSUPPORTED
+    assert lib.spk_linear_decode(A, A, None, A, 8, 896, 192, bf16, None) == _lib.SPK_EUNSUPPORTED
+    assert lib.spk_linear_decode(A, A, A, A, 8, 896, 2048, bf16, None) == _lib.SPK_EUNSUPPORTED
+    assert lib.spk_linear_decode(B, A, None, A, 8, 896, 896, bf16, None) == _lib.SPK_EINVAL
+    assert b"aligned" in lib.spk_last_error()
+    assert lib.spk_linear_decode(A, B, None, A, 8, 896, 4864, bf16, None) == _lib.SPK_EINVAL
+    assert lib.spk_mlp_gate_pack(None, 20, 896, bf16, None, None) == _lib.SPK_EINVAL
+    assert lib.spk_mlp_gate_lif(A, A, A, A, f32, A, 4, 8, 896, 4864, f16, None) == _lib.SPK_EUNSUPPORTED
+    assert lib.spk_mlp_gate_lif(A, A, A, A, 7, A, 4, 8, 896, 4864, bf16, None) == _lib.SPK_EINVAL
+    assert lib.spk_mlp_gate_lif(A, A, A, A, f32, A, 5, 8, 896, 4864, bf16, None) == _lib.SPK_EUNSUPPORTED
+    assert lib.spk_mlp_gate_lif(A, A, A, A, f32, A, 4, 8, 256, 4864, bf16, None) == _lib.SPK_EUNSUPPORTED
+    assert lib.spk_mlp_gate_lif(A, A, A, A, f32, A, 4, 8, 896, 512, bf16, None) == _lib.SPK_EUNSUPPORTED
+    assert lib.spk_mlp_gate_lif(B, A, A, A, f32, A, 4, 8, 896, 4864, bf16, None) == _lib.SPK_EINVAL
+    assert lib.spk_mlp_gate_packed_bytes(896, 4864) == 2 * 4864 * 896 * 2
+
+
 def test_workspace_sizing():
     lib = _lib.load()
     # config 3 shape: one partition, no workspace
