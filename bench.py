@@ -288,7 +288,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(every (sequence, kv head, t) unit is independent; see DESIGN.md)", file=sys.stderr)
+              "(every (sequence, kv head, t) unit is independent of the others)", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
