@@ -317,6 +317,13 @@ def main():
             ms_p, _ = bench_attention(alt, args.steps, args.warmup, dev)
             extras[f"density_{p}_gbs"] = round(nbytes / ms_p / 1e6, 1)
             del alt
+        print("batch 256 x fixed 8k context", file=sys.stderr, flush=True)
+        alt = make_attn_inputs(256, 8192, 8192, 0.2, 4000, dev)
+        ms_8k, _ = bench_attention(alt, args.steps, args.warmup, dev)
+        gbs_8k = attn_bytes(alt["lens_cpu"], 4) / ms_8k / 1e6
+        extras["batch256_ctx8192"] = {"us_per_call": round(ms_8k * 1000, 1), "gbs": round(gbs_8k, 1),
+                                      "frac_of_hbm_peak": round(gbs_8k / HBM_PEAK_GBS, 4)}
+        del alt
         print("config 4 at head_dim 128", file=sys.stderr, flush=True)
         alt = make_attn_inputs(256, 4096, 32768, 0.2, 4000, dev, head_dim=128)
         ms_h, _ = bench_attention(alt, args.steps, args.warmup, dev)
