@@ -251,6 +251,19 @@ extern "C" size_t spk_decode_attn_workspace_bytes(int T, int N, int Hq, int Hkv,
   return partials + order;
 }
 
+// Compute units of the current device (cached per device; 256 if the query fails).
+static int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 // Shared by spk_decode_attn and spk_qkv_decode_attn: validation, parameters,
 // path choice and launches.  fz != nullptr selects the fused q/k/v path
 // (matrix-core kernel only; its x dtype in fused_dtype).
@@ -310,7 +323,15 @@ static int decode_attn_impl(const int32_t *q, const int64_t q_strides[4], const 
     const bool plan = plan_launch(ctx_max);
     int32_t *order = plan_in_workspace(ctx_max, (int64_t)p.num_parts * N)
                          ? reinterpret_cast<int32_t *>(p.ws + partial_floats) : nullptr;
-    launch_decode_mfma(p, plan, order, s, fz ? fused_dtype : 0);
+    // Short contexts whose whole grid is resident at once (8 two-wave
+    // workgroups per CU) run 2 waves per unit: one round of workgroups
+    // instead of two.  Longer or ragged-long launches keep 4 waves, whose
+    // longest-first order balances them better.
+    const int64_t items = (int64_t)N * T * Hkv * p.num_parts;
+    int waves = !fz && head_dim == 64 && ctx_max <= 8192 && items <= 8 * (int64_t)device_cus() ? 2 : 4;
+    const char *wv = getenv("SPIKEINFER_AMD_ATTN_WAVES");  // tests force either launch
+    if (wv && (strcmp(wv, "2") == 0 || strcmp(wv, "4") == 0)) waves = atoi(wv);
+    launch_decode_mfma(p, plan, order, s, fz ? fused_dtype : 0, waves);
   } else if (fz) {
     return fail(SPK_EUNSUPPORTED, "qkv_decode_attn: needs head_dim 64, Hq/Hkv <= 8, aligned caches");
   } else switch (W) {

@@ -94,6 +94,9 @@ inline bool plan_in_workspace(int64_t ctx_max, int64_t items) {
 // Launches the matrix-core kernel; `plan` orders it longest first, from
 // `order` when not null (after the planner kernel fills it), else in-kernel.
 // fused_dtype: 0 for q from p.q, else the dtype (SPK_BF16 / SPK_F16) of p.fz.x.
-void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s, int fused_dtype = 0);
+// waves: 4, or 2 for the short-context launch (plain path, head_dim 64 only;
+// otherwise 4 is used).
+void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s, int fused_dtype = 0,
+                        int waves = 4);
 
 }  // namespace spk

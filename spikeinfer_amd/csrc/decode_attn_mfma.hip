@@ -51,7 +51,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 namespace mfma {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;  // waves per workgroup, except the short-context launch (KW = 2)
 constexpr int kStepTokens = 128;      // tokens per wave step (2 per lane)
 constexpr int kMaxPartBlocks = kMaxStagedBlocks;  // block-table entries staged per partition
 
@@ -68,12 +68,12 @@ struct alignas(16) WaveStage {
 };
 
 // Cross-wave reduction: 8 * W64 values + 2 denominators per lane.
-template <int W64>
-constexpr int kReduceFloats = (kWaves - 1) * 64 * (8 * W64 + 2);
-template <int W64>
-constexpr int kSmemBytes = (kWaves * (int)sizeof(WaveStage<W64>) > kReduceFloats<W64> * 4)
-                               ? kWaves * (int)sizeof(WaveStage<W64>)
-                               : kReduceFloats<W64> * 4;
+template <int W64, int KW>
+constexpr int kReduceFloats = (KW - 1) * 64 * (8 * W64 + 2);
+template <int W64, int KW>
+constexpr int kSmemBytes = (KW * (int)sizeof(WaveStage<W64>) > kReduceFloats<W64, KW> * 4)
+                               ? KW * (int)sizeof(WaveStage<W64>)
+                               : kReduceFloats<W64, KW> * 4;
 
 __device__ __forceinline__ v2i tr_b4(const SPK_LDS char *p) {
   return __builtin_amdgcn_ds_read_tr4_b64_v2i32((SPK_LDS v2i *)p);
@@ -218,9 +218,10 @@ __device__ __forceinline__ void contract_step(const WaveStage<W64> &st, int lane
 // (uniform over the block).  Needs N * num_parts <= kInlinePlanItems; `sh`
 // holds kMaxBuckets + 8 ints and is free again after the call.
 constexpr int kMaxBuckets = 130;  // part_len <= 32768 tokens, 256 per bucket
+template <int KW>
 __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh) {
-  constexpr int kThreads = kWaves * 64;
-  int *count = sh, *wsum = sh + kMaxBuckets, *res = wsum + kWaves;
+  constexpr int kThreads = KW * 64;
+  int *count = sh, *wsum = sh + kMaxBuckets, *res = wsum + KW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int M = p.N * p.num_parts;
   const int nb = (p.part_len >> 8) + 2;
@@ -291,7 +292,7 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh) {
   return res[2];
 }
 
-// One workgroup = 4 waves = one (partition, t, kv head, sequence); waves take
+// One workgroup = KW waves (4, or 2 for short contexts) = one (partition, t, kv head, sequence); waves take
 // the partition's 128-token steps round-robin (two steps of loads in flight
 // per wave) and reduce at the end in a fixed order.
 // Fused path: the unit's spikes at timestep t from the q/k/v currents, as
@@ -383,18 +384,19 @@ __device__ __forceinline__ void fused_spikes(const FusedIn<XDT> &in, int t, int 
 // XDT = 0: queries come packed in p.q.  XDT = SPK_BF16 / SPK_F16: the fused
 // path, which derives this unit's q and current k/v spikes from p.fz
 // (head_dim 64 only).  W64 = head_dim / 64 (1 or 2).
-template <int NREP, int XDT, int W64>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT == 0 && W64 == 1 ? 4 : 3))) void decode_attn_mfma_kernel(AttnParams p) {
+template <int NREP, int XDT, int W64, int KW>
+__global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 0 && W64 == 1 ? 4 : 3))) void decode_attn_mfma_kernel(AttnParams p) {
   static_assert(W64 == 1 || (W64 == 2 && XDT == 0), "fused path: head_dim 64 only");
+  static_assert(KW == kWaves || (KW == 2 && XDT == 0 && W64 == 1), "2-wave launch: plain path, head_dim 64");
   // Unplanned launch: x = (sequence, timestep, kv head) unit, y = partition.
   // Either way consecutive block ids (dealt round-robin to the 8 XCDs) are
   // sibling units of equal length.
   const int units = p.N * p.T * p.Hkv;
   int unit = blockIdx.x, part = blockIdx.y;
-  __shared__ __align__(16) char smem[kSmemBytes<W64>];
+  __shared__ __align__(16) char smem[kSmemBytes<W64, KW>];
   if (p.plan_inline) {  // planned launch: longest work items first
     const int ups = p.T * p.Hkv;
-    const int i = plan_slot(p, (int)blockIdx.x / ups, reinterpret_cast<int *>(smem));
+    const int i = plan_slot<KW>(p, (int)blockIdx.x / ups, reinterpret_cast<int *>(smem));
     if (i < 0) return;
     unit = (i % p.N) * ups + (int)blockIdx.x % ups;
     part = i / p.N;
@@ -431,7 +433,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT
   // Physical blocks outside the cache are replaced by block 0 here, once, so
   // the loads below never leave [0, num_slots) (a pair never straddles a block).
   const uint32_t num_blocks = static_cast<uint32_t>(min<int64_t>(p.num_slots >> p.bs_log2, 0xffffffffll));
-  for (int b = tid; b < nblk; b += kWaves * 64) {
+  for (int b = tid; b < nblk; b += KW * 64) {
     const uint32_t phys = static_cast<uint32_t>(p.bt[n * p.bts0 + (blk0 + b) * p.bts1]);
     blocks[b] = static_cast<int32_t>(phys < num_blocks ? phys : 0u);
   }
@@ -480,7 +482,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT
 
   v4f acc[2][4 * W64] = {}, accl[2] = {};
 
-  constexpr int kStride = kWaves * kStepTokens;
+  constexpr int kStride = KW * kStepTokens;
   const int first = start + wave * kStepTokens;
   const int span = end - first;
   const int nfull = span > 0 ? (span / kStride) + ((span % kStride) >= kStepTokens ? 1 : 0) : 0;
@@ -634,7 +636,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(XDT
   }
   __syncthreads();
   if (wave != 0) return;
-  for (int w = 1; w < kWaves; ++w) {
+  for (int w = 1; w < KW; ++w) {
     const float *src = red + ((w - 1) * 64 + lane) * kRed;
 #pragma unroll
     for (int k = 0; k < kVals; ++k) val[k] += src[k];
@@ -775,8 +777,10 @@ __global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, in
 
 }  // namespace mfma
 
-void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s, int fused_dtype) {
-  const int threads = mfma::kWaves * 64;
+void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s, int fused_dtype,
+                        int waves) {
+  const bool two = waves == 2 && fused_dtype == 0 && p.head_dim == 64;
+  const int threads = (two ? 2 : mfma::kWaves) * 64;
   const int units = p.N * p.T * p.Hkv;
   dim3 grid(units, p.num_parts);
   p.order = nullptr;
@@ -790,25 +794,27 @@ void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s, 
     p.order = order;
     grid = dim3(units * p.num_parts);
   }
-#define SPK_NREP_CASES(XDT, W64)                                                              \
-  switch (p.nrep) {                                                                           \
-    case 1: mfma::decode_attn_mfma_kernel<1, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
-    case 2: mfma::decode_attn_mfma_kernel<2, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
-    case 3: mfma::decode_attn_mfma_kernel<3, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
-    case 4: mfma::decode_attn_mfma_kernel<4, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
-    case 5: mfma::decode_attn_mfma_kernel<5, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
-    case 6: mfma::decode_attn_mfma_kernel<6, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
-    case 7: mfma::decode_attn_mfma_kernel<7, XDT, W64><<<grid, threads, 0, s>>>(p); break;    \
-    default: mfma::decode_attn_mfma_kernel<8, XDT, W64><<<grid, threads, 0, s>>>(p); break;   \
+#define SPK_NREP_CASES(XDT, W64, KW)                                                              \
+  switch (p.nrep) {                                                                               \
+    case 1: mfma::decode_attn_mfma_kernel<1, XDT, W64, KW><<<grid, threads, 0, s>>>(p); break;    \
+    case 2: mfma::decode_attn_mfma_kernel<2, XDT, W64, KW><<<grid, threads, 0, s>>>(p); break;    \
+    case 3: mfma::decode_attn_mfma_kernel<3, XDT, W64, KW><<<grid, threads, 0, s>>>(p); break;    \
+    case 4: mfma::decode_attn_mfma_kernel<4, XDT, W64, KW><<<grid, threads, 0, s>>>(p); break;    \
+    case 5: mfma::decode_attn_mfma_kernel<5, XDT, W64, KW><<<grid, threads, 0, s>>>(p); break;    \
+    case 6: mfma::decode_attn_mfma_kernel<6, XDT, W64, KW><<<grid, threads, 0, s>>>(p); break;    \
+    case 7: mfma::decode_attn_mfma_kernel<7, XDT, W64, KW><<<grid, threads, 0, s>>>(p); break;    \
+    default: mfma::decode_attn_mfma_kernel<8, XDT, W64, KW><<<grid, threads, 0, s>>>(p); break;   \
   }
   if (fused_dtype == SPK_BF16) {  // the caller allows the fused path at head_dim 64 only
-    SPK_NREP_CASES(SPK_BF16, 1)
+    SPK_NREP_CASES(SPK_BF16, 1, 4)
   } else if (fused_dtype == SPK_F16) {
-    SPK_NREP_CASES(SPK_F16, 1)
+    SPK_NREP_CASES(SPK_F16, 1, 4)
   } else if (p.head_dim == 128) {
-    SPK_NREP_CASES(0, 2)
+    SPK_NREP_CASES(0, 2, 4)
+  } else if (two) {
+    SPK_NREP_CASES(0, 1, 2)
   } else {
-    SPK_NREP_CASES(0, 1)
+    SPK_NREP_CASES(0, 1, 4)
   }
 #undef SPK_NREP_CASES
 }
