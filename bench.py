@@ -229,6 +229,23 @@ def bench_lif(steps, warmup, dev):
     }
 
 
+def bench_pack(steps, warmup, dev):
+    """Standalone pack_spikes / unpack_spikes on config-2's q shape: bf16 {0,1}
+    spikes [T, 4096, 14, 64] <-> int32 words [T, 4096, 14, 2]."""
+    from spikeinfer_amd.kernels import pack_spikes, unpack_spikes
+
+    g = torch.Generator(device=dev).manual_seed(2100)
+    x = (torch.rand((T, 4096, HQ, D), generator=g, device=dev) < 0.2).bfloat16()
+    words = pack_spikes(x)
+    stream = torch.cuda.current_stream(dev)
+    ms_p = time_calls(lambda: pack_spikes(x), steps, warmup, stream)
+    ms_u = time_calls(lambda: unpack_spikes(words, D, torch.bfloat16), steps, warmup, stream)
+    nbytes = x.numel() * 2 + words.numel() * 4  # spikes one way, words the other
+    return {"elements": x.numel(), "pack_us": round(ms_p * 1000, 1),
+            "pack_gbs": round(nbytes / ms_p / 1e6, 1), "unpack_us": round(ms_u * 1000, 1),
+            "unpack_gbs": round(nbytes / ms_u / 1e6, 1)}
+
+
 def bench_decode_step(steps, warmup, dev, batch=64):
     """Config 5: random-init Qwen2.5-0.5B-shaped spiking decoder (bf16 weights
     N(0, 0.02)), batch 64, 128-token random prompts, T=4; one decode step
@@ -337,6 +354,8 @@ def main():
         extras["config3_attn_us_per_step_24_layers"] = round(ms3 * 1000, 1)
         extras["config3_attn_gbs"] = round(attn_bytes(c3["lens_cpu"], 2) * 24 / ms3 / 1e6, 1)
         del c3
+        print("pack / unpack", file=sys.stderr, flush=True)
+        extras["pack_unpack"] = bench_pack(args.steps, args.warmup, dev)
         print("config 2", file=sys.stderr, flush=True)
         extras["config2_lif"] = bench_lif(args.steps, args.warmup, dev)
         print("config 5", file=sys.stderr, flush=True)

@@ -262,6 +262,108 @@ __global__ __launch_bounds__(256) void unpack_kernel(const uint32_t *words, int6
   }
 }
 
+// Vector forms for rows of whole 64-channel chunks (C % 64 == 0) with
+// 16-byte aligned rows: each lane moves 16 bytes (PER = 16 / element size
+// elements), G = 64 / PER lanes cover one chunk, i.e. one uint64 of packed
+// words (int32 words 2c, 2c+1 of the row, little-endian).  Same bit tests as
+// load_nonzero / the same values as store_spike.
+template <int DT>
+struct PackVec {
+  static constexpr int kEsz = DT == SPK_U8 ? 1 : (DT == SPK_F16 || DT == SPK_BF16) ? 2 : 4;
+  static constexpr int kPer = 16 / kEsz;  // elements per lane
+  static constexpr int kG = 64 / kPer;    // lanes per 64-channel chunk
+  // Bit i set where element i of the lane's 16 bytes is nonzero.
+  __device__ static uint32_t bits(const uint4 &v) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t b = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (kEsz == 4) {
+        const uint32_t m = DT == SPK_F32 ? 0x7fffffffu : 0xffffffffu;
+        b |= ((w[j] & m) != 0u ? 1u : 0u) << j;
+      } else if constexpr (kEsz == 2) {
+        b |= ((w[j] & 0x7fffu) != 0u ? 1u : 0u) << (2 * j);
+        b |= ((w[j] & 0x7fff0000u) != 0u ? 1u : 0u) << (2 * j + 1);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) b |= ((w[j] >> (8 * k)) & 0xffu ? 1u : 0u) << (4 * j + k);
+      }
+    }
+    return b;
+  }
+  // 16 bytes of 0/1 elements from kPer bits.
+  __device__ static uint4 spikes(uint32_t b) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (kEsz == 4) {
+        w[j] = (b >> j) & 1u ? (DT == SPK_F32 ? 0x3f800000u : 1u) : 0u;
+      } else if constexpr (kEsz == 2) {
+        constexpr uint32_t one = DT == SPK_F16 ? 0x3c00u : 0x3f80u;
+        w[j] = ((b >> (2 * j)) & 1u ? one : 0u) | ((b >> (2 * j + 1)) & 1u ? one << 16 : 0u);
+      } else {
+        uint32_t x = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x |= ((b >> (4 * j + k)) & 1u) << (8 * k);
+        w[j] = x;
+      }
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
+// The loop runs per wave (every lane takes part in the shuffles); lanes past
+// the last chunk load nothing and store nothing.
+template <int DT>
+__global__ __launch_bounds__(256) void pack_vec_kernel(const char *x, int64_t row_stride_bytes,
+                                                       uint64_t *out, int64_t rows, int C) {
+  using P = PackVec<DT>;
+  const int lane = threadIdx.x & 63, sub = lane % P::kG;
+  const int64_t cpr = C >> 6, total = rows * cpr;
+  constexpr int kPerWave = 64 / P::kG;
+  const int64_t step = (int64_t)gridDim.x * (blockDim.x >> 6) * kPerWave;
+  for (int64_t base = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * kPerWave;
+       base < total; base += step) {
+    const int64_t ci = base + lane / P::kG;
+    const bool valid = ci < total;
+    const int64_t row = valid ? ci / cpr : 0;
+    const int64_t ch = valid ? ci - row * cpr : 0;
+    uint32_t b = 0;
+    if (valid) {
+      typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+      const v4u v = __builtin_nontemporal_load(
+          reinterpret_cast<const v4u *>(x + row * row_stride_bytes + (ch * 64 + sub * P::kPer) * P::kEsz));
+      b = P::bits(make_uint4(v.x, v.y, v.z, v.w));
+    }
+    // Bit offset of this lane in the chunk's word; kPer divides 32, so a
+    // lane's bits never straddle the two halves.
+    const int sh = sub * P::kPer;
+    uint32_t lo = sh < 32 ? b << sh : 0u;
+    uint32_t hi = sh < 32 ? 0u : b << (sh - 32);
+#pragma unroll
+    for (int off = 1; off < P::kG; off <<= 1) {
+      lo |= __shfl_xor(lo, off);
+      hi |= __shfl_xor(hi, off);
+    }
+    if (valid && sub == 0) out[ci] = (static_cast<uint64_t>(hi) << 32) | lo;
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void unpack_vec_kernel(const uint64_t *words, int64_t rows, int C,
+                                                         char *out) {
+  using P = PackVec<DT>;
+  const int64_t total_lanes = rows * (C >> 6) * P::kG;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total_lanes;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t ci = i / P::kG;  // chunk (row-major over rows x C/64)
+    const int sub = static_cast<int>(i - ci * P::kG);
+    const uint64_t w = words[ci];
+    const uint32_t b = static_cast<uint32_t>(w >> (sub * P::kPer)) & ((1u << P::kPer) - 1u);
+    reinterpret_cast<uint4 *>(out)[i] = P::spikes(b);
+  }
+}
+
 inline unsigned grid_for(int64_t items, int per_block) {
   int64_t g = (items + per_block - 1) / per_block;
   if (g < 1) g = 1;
@@ -351,7 +453,26 @@ extern "C" int spk_pack(const void *x, int x_dtype, int64_t x_row_stride, int32_
   if (rows < 0 || C <= 0) return fail(SPK_EINVAL, "bad sizes rows=%lld C=%d", (long long)rows, C);
   if (!valid_any_dtype(x_dtype)) return fail(SPK_EINVAL, "unsupported dtype %d", x_dtype);
   if (rows == 0) return SPK_OK;
-  pack_kernel<<<grid_for(rows, 4), 256, 0, static_cast<hipStream_t>(stream)>>>(
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int esz = x_dtype == SPK_U8 ? 1 : (x_dtype == SPK_F16 || x_dtype == SPK_BF16) ? 2 : 4;
+  if (C % 64 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ((x_row_stride * esz) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(out) & 7) == 0) {
+    const int64_t chunks = rows * (C / 64);
+    const int per_block = 4 * (64 / (64 * esz / 16));  // chunks per 4-wave block
+    const unsigned grid = grid_for(chunks, per_block);
+    const char *xb = static_cast<const char *>(x);
+    uint64_t *o = reinterpret_cast<uint64_t *>(out);
+    const int64_t rs = x_row_stride * esz;
+    switch (x_dtype) {
+      case SPK_F32: pack_vec_kernel<SPK_F32><<<grid, 256, 0, s>>>(xb, rs, o, rows, C); break;
+      case SPK_F16: pack_vec_kernel<SPK_F16><<<grid, 256, 0, s>>>(xb, rs, o, rows, C); break;
+      case SPK_BF16: pack_vec_kernel<SPK_BF16><<<grid, 256, 0, s>>>(xb, rs, o, rows, C); break;
+      case SPK_U8: pack_vec_kernel<SPK_U8><<<grid, 256, 0, s>>>(xb, rs, o, rows, C); break;
+      default: pack_vec_kernel<SPK_I32><<<grid, 256, 0, s>>>(xb, rs, o, rows, C); break;
+    }
+    return check_launch("pack");
+  }
+  pack_kernel<<<grid_for(rows, 4), 256, 0, s>>>(
       x, x_dtype, x_row_stride, reinterpret_cast<uint32_t *>(out), rows, C);
   return check_launch("pack");
 }
@@ -361,7 +482,24 @@ extern "C" int spk_unpack(const int32_t *words, int64_t rows, int C, void *out, 
   if (rows < 0 || C <= 0) return fail(SPK_EINVAL, "bad sizes rows=%lld C=%d", (long long)rows, C);
   if (!valid_any_dtype(out_dtype)) return fail(SPK_EINVAL, "unsupported dtype %d", out_dtype);
   if (rows == 0) return SPK_OK;
-  unpack_kernel<<<grid_for(rows * C, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int esz = out_dtype == SPK_U8 ? 1 : (out_dtype == SPK_F16 || out_dtype == SPK_BF16) ? 2 : 4;
+  if (C % 64 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(words) & 7) == 0) {
+    const int64_t lanes = rows * (C / 64) * (4 * esz);  // 16 output bytes per lane
+    const unsigned grid = grid_for(lanes, 256);
+    const uint64_t *w = reinterpret_cast<const uint64_t *>(words);
+    char *o = static_cast<char *>(out);
+    switch (out_dtype) {
+      case SPK_F32: unpack_vec_kernel<SPK_F32><<<grid, 256, 0, s>>>(w, rows, C, o); break;
+      case SPK_F16: unpack_vec_kernel<SPK_F16><<<grid, 256, 0, s>>>(w, rows, C, o); break;
+      case SPK_BF16: unpack_vec_kernel<SPK_BF16><<<grid, 256, 0, s>>>(w, rows, C, o); break;
+      case SPK_U8: unpack_vec_kernel<SPK_U8><<<grid, 256, 0, s>>>(w, rows, C, o); break;
+      default: unpack_vec_kernel<SPK_I32><<<grid, 256, 0, s>>>(w, rows, C, o); break;
+    }
+    return check_launch("unpack");
+  }
+  unpack_kernel<<<grid_for(rows * C, 256), 256, 0, s>>>(
       reinterpret_cast<const uint32_t *>(words), rows, C, out, out_dtype);
   return check_launch("unpack");
 }

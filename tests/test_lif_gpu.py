@@ -88,7 +88,7 @@ def test_lif_mem0_and_bf16_params(gpu):
 
 # ---- packing ---------------------------------------------------------------
 @pytest.mark.parametrize("channels", [1, 31, 32, 33, 63, 64, 128, 256, 4864])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.uint8])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.uint8, torch.int32])
 def test_pack_roundtrip_and_bytes(channels, dtype, gpu):
     from spikeinfer_amd.kernels import pack_spikes, unpack_spikes
 
@@ -115,6 +115,23 @@ def test_pack_known_answers(gpu):
         assert w == 1 << ch
     with pytest.raises(ValueError, match="expected 4 words"):
         unpack_spikes(pack_spikes(torch.ones(1, 64, device=gpu)), 128)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 7, 33, 1000])
+def test_pack_signed_zero_nan_and_row_counts(dtype, rows, gpu):
+    """64-channel rows (the 16-byte-per-lane kernels): -0.0 packs as 0, NaN and
+    tiny values as 1, for row counts that leave partial waves."""
+    from spikeinfer_amd.kernels import pack_spikes, unpack_spikes
+
+    g = torch.Generator().manual_seed(rows)
+    vals = torch.tensor([0.0, -0.0, 1.0, -2.5, float("nan"), 1e-30, float("inf")], dtype=torch.float32)
+    idx = torch.randint(0, len(vals), (rows, 128), generator=g)
+    x = vals[idx].to(dtype)
+    bits = (x.float() != 0) | x.float().isnan()
+    words = pack_spikes(x.to(gpu))
+    assert np.array_equal(words.cpu().numpy(), orc.np_pack(bits.numpy().astype(np.uint8)))
+    assert torch.equal(unpack_spikes(words, 128, dtype).cpu(), bits.to(dtype))
 
 
 def test_pack_noncontiguous(gpu):
