@@ -1,658 +1,16 @@
-// Batched token sampler: one workgroup per row of logits, no host round trip.
-//
-// Reference semantics: spikeinfer/engine/sampler.py:48-177 -- penalties
-// (repetition, then presence + frequency; :98-119), temperature (:69-75),
-// min_p (:137-141), top_k (:143-153), top_p (:155-159), then a draw from the
-// softmax of what survived (:162-168); greedy rows (temperature < 1e-5,
-// sampling_params.py:74) take the argmax of the penalised logits (:64-67).
-//
-// MI355X design.  No sort of the 151,936-entry row.  Every filter keeps a
-// prefix of the row in one total order -- value descending, index ascending
-// (the reference leaves the order of equal logits to torch.topk; this kernel
-// fixes it) -- so each cut is a key K plus, among the elements of key K, the
-// ones up to some index:
-//   * min_p keeps exp(x - max) >= min_p (a value threshold);
-//   * top_k: radix select (11/11/10-bit digits of the order-preserving key)
-//     on element counts finds the k-th element, and a radix select on the
-//     indices of its ties finds how far into them the cut goes;
-//   * top_p: the same on probability mass finds the last element whose
-//     preceding mass is below top_p of the surviving mass.  Mass is fixed
-//     point (weight * 2^40 in uint64), so sums are exact and the cut is
-//     deterministic whatever the atomic order.
-// The draw takes the element whose interval of the kept mass, accumulated in
-// the same total order, holds u * total, for a caller-supplied uniform u in
-// [0, 1): one more mass select and one index select.
-// Nothing depends on the order elements are visited in, so every pass over
-// the row is a coalesced sweep.  With a top-k cut, one sweep gathers the
-// elements at or above a sample-estimated threshold into LDS (a few hundred at
-// top-k 50) and every later pass runs over those; histograms, the seen-token
-// bitmap and the count hash live in LDS too.
-#include "common.hpp"
-#include "lif_math.hpp"
+// Batched token sampler: the C-ABI entry (the kernels are in
+// sampler_kernel.hpp, instantiated per logits dtype in sampler_f32.hip,
+// sampler_f16.hip and sampler_bf16.hip so they compile in parallel).
+#include "sampler_kernel.hpp"
 
 namespace spk {
 namespace smp {
-
-constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / 64;
-constexpr int kBins = 2048;            // 11-bit digits
-constexpr int kMaxVocab = 262144;      // bitmap capacity (32 KB)
-constexpr int kMaxHist = 2048;         // history tokens per row
-constexpr int kHashSlots = 2 * kMaxHist;
-constexpr float kGreedyTemp = 1e-5f;
-constexpr double kMassScale = 1099511627776.0;  // 2^40
-
-constexpr int kCand = 8192;  // LDS candidate capacity (the fast path)
-constexpr int kNoCutCand = 4096;  // without a top-k cut: about 1.5x this many candidates (the margin below)
-
-struct Params {
-  float temp, min_p, top_p, rep, presence, frequency;
-  int top_k;
-  bool use_hash;
-};
-
-struct Shared {
-  uint32_t seen[kMaxVocab / 32];      // generated-token bitmap
-  int32_t hkey[kHashSlots];           // token + 1 -> count (frequency penalty)
-  int32_t hcnt[kHashSlots];
-  unsigned long long hist[kBins];     // radix histograms (counts or fixed-point mass)
-  float cx[kCand];                    // candidates, in index order: value x ...
-  int32_t ci[kCand];                  // ... and vocabulary index
-  unsigned long long wsum[kWaves];
-  unsigned long long bcast[4];
-  float fbcast[kWaves];
-};
-
-// Order-preserving unsigned key of a float (larger float -> larger key).
-__device__ __forceinline__ uint32_t fkey(float x) {
-  const uint32_t b = __float_as_uint(x);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-__device__ __forceinline__ float unkey(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
-
-__device__ __forceinline__ int hash_slot(int tok) {
-  return static_cast<int>((static_cast<uint32_t>(tok) * 2654435761u) % kHashSlots);
-}
-
-// Penalised logit (sampler.py:98-119): repetition first, then presence and
-// frequency, for tokens generated so far.
-// Penalty of a token known to be in the history.
-__device__ __forceinline__ float penalise_seen(const Params &P, const Shared &sh, int i, float v) {
-  if (P.rep != 1.f) v = v > 0.f ? v / P.rep : v * P.rep;
-  if (P.presence != 0.f || P.frequency != 0.f) {
-    float cnt = 1.f;
-    if (P.use_hash) {
-      int s = hash_slot(i);
-      while (sh.hkey[s] != i + 1) s = (s + 1) % kHashSlots;
-      cnt = static_cast<float>(sh.hcnt[s]);
-    }
-    v = v - (P.presence + P.frequency * cnt);
-  }
-  return v;
-}
-
-__device__ __forceinline__ float penalise(const Params &P, const Shared &sh, int i, float v) {
-  if (!((sh.seen[i >> 5] >> (i & 31)) & 1u)) return v;
-  return penalise_seen(P, sh, i, v);
-}
-
-__device__ __forceinline__ unsigned long long shfl_up_u64(unsigned long long v, int d) {
-  const uint32_t lo = __shfl_up(static_cast<uint32_t>(v), d);
-  const uint32_t hi = __shfl_up(static_cast<uint32_t>(v >> 32), d);
-  return (static_cast<unsigned long long>(hi) << 32) | lo;
-}
-
-// Exclusive prefix sum over the workgroup in thread order; *total gets the sum.
-__device__ __forceinline__ unsigned long long block_exclusive_scan(unsigned long long v, Shared &sh,
-                                                   unsigned long long *total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  unsigned long long inc = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const unsigned long long o = shfl_up_u64(inc, d);
-    if (lane >= d) inc += o;
-  }
-  __syncthreads();
-  if (lane == 63) sh.wsum[wave] = inc;
-  __syncthreads();
-  unsigned long long before = 0, all = 0;
-  for (int w = 0; w < kWaves; ++w) {
-    const unsigned long long s = sh.wsum[w];
-    if (w < wave) before += s;
-    all += s;
-  }
-  *total = all;
-  return before + inc - v;
-}
-
-__device__ __forceinline__ float block_max(float v, Shared &sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d));
-  __syncthreads();
-  if (lane == 0) sh.fbcast[wave] = v;
-  __syncthreads();
-  float m = sh.fbcast[0];
-  for (int w = 1; w < kWaves; ++w) m = fmaxf(m, sh.fbcast[w]);
-  return m;
-}
-
-__device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v, Shared &sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) {
-    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), d);
-    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), d);
-    const unsigned long long o = (static_cast<unsigned long long>(hi) << 32) | lo;
-    v = o > v ? o : v;
-  }
-  __syncthreads();
-  if (lane == 0) sh.wsum[wave] = v;
-  __syncthreads();
-  unsigned long long m = sh.wsum[0];
-  for (int w = 1; w < kWaves; ++w) m = sh.wsum[w] > m ? sh.wsum[w] : m;
-  return m;
-}
-
-// Given the 2048-bin histogram in sh.hist, finds the bin b (scanning from the
-// top) with above < target <= above + hist[b], where above = base + the bins
-// over b.  Writes b and its `above` to sh.bcast[0..1]; bcast[2] = 1 if found.
-constexpr int kBinsPerThread = kBins / kThreads;
-__device__ __forceinline__ void select_bin(Shared &sh, unsigned long long base, double target) {
-  const int top = kBins - 1 - kBinsPerThread * static_cast<int>(threadIdx.x);  // this thread's highest bin
-  unsigned long long h[kBinsPerThread], sum = 0;
-#pragma unroll
-  for (int r = 0; r < kBinsPerThread; ++r) sum += (h[r] = sh.hist[top - r]);
-  unsigned long long total;
-  unsigned long long before = base + block_exclusive_scan(sum, sh, &total);
-  if (threadIdx.x == 0) sh.bcast[2] = 0;
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < kBinsPerThread; ++r) {
-    if ((double)before < target && target <= (double)(before + h[r])) {
-      sh.bcast[0] = top - r;
-      sh.bcast[1] = before;
-      sh.bcast[2] = 1;
-    }
-    before += h[r];
-  }
-  __syncthreads();
-}
-
-__device__ __forceinline__ unsigned long long mass_of(float x, float m) {
-  return static_cast<unsigned long long>(static_cast<double>(expf(x - m)) * kMassScale);
-}
-
-__device__ __forceinline__ void zero_hist(Shared &sh) {
-  __syncthreads();
-  for (int b = threadIdx.x; b < kBins; b += kThreads) sh.hist[b] = 0;
-  __syncthreads();
-}
-
-// ---- element sources ----------------------------------------------------------------
-// each(f) visits every element once, f(index, x), in no particular order.
-
-// The logits row in global memory; x = penalise(raw) / temperature.  Coalesced
-// 16-byte loads, eight in flight per thread.
-template <int DT, bool VEC>
-struct GlobalSrc {
-  typedef typename Elem<DT>::T E;
-  static constexpr int W = VEC ? Elem<DT>::kVec : 1;
-  static constexpr int kInFlight = 8;
-  typedef E Vec __attribute__((ext_vector_type(W)));
-  const E *p;
-  int V;
-  Params P;
-  const Shared *sh;
-
-  __device__ __forceinline__ float x(int i, E raw) const {
-    return penalise(P, *sh, i, elem_to_f32<DT>(raw)) / P.temp;
-  }
-  template <class F> __device__ __forceinline__ void each_raw(F f) const {
-    const int nv = V / W;
-    const Vec *pv = reinterpret_cast<const Vec *>(p);
-    int v = threadIdx.x;
-    for (; v + (kInFlight - 1) * kThreads < nv; v += kInFlight * kThreads) {
-      Vec a[kInFlight];
-#pragma unroll
-      for (int u = 0; u < kInFlight; ++u) a[u] = pv[v + u * kThreads];
-#pragma unroll
-      for (int u = 0; u < kInFlight; ++u)
-#pragma unroll
-        for (int j = 0; j < W; ++j) f((v + u * kThreads) * W + j, a[u][j]);
-    }
-    for (; v < nv; v += kThreads) {
-      const Vec a = pv[v];
-#pragma unroll
-      for (int j = 0; j < W; ++j) f(v * W + j, a[j]);
-    }
-    for (int i = nv * W + threadIdx.x; i < V; i += kThreads) f(i, p[i]);
-  }
-  template <class F> __device__ __forceinline__ void each(F f) const {
-    each_raw([&](int i, E raw) { f(i, x(i, raw)); });
-  }
-  // f(i, v) with v the penalised logit, not divided by the temperature (an
-  // order-preserving map of x): one bitmap word per vector, none without
-  // history.
-  template <class F> __device__ __forceinline__ void each_pen(F f, bool has_hist) const {
-    const int nv = V / W;
-    const Vec *pv = reinterpret_cast<const Vec *>(p);
-    auto one = [&](int b, const Vec &a) {
-      const uint32_t bits = has_hist ? (sh->seen[b >> 5] >> (b & 31)) : 0u;
-#pragma unroll
-      for (int j = 0; j < W; ++j) {
-        float v = elem_to_f32<DT>(a[j]);
-        if ((bits >> j) & 1u) v = penalise_seen(P, *sh, b + j, v);
-        f(b + j, v);
-      }
-    };
-    int v = threadIdx.x;
-    for (; v + (kInFlight - 1) * kThreads < nv; v += kInFlight * kThreads) {
-      Vec a[kInFlight];
-#pragma unroll
-      for (int u = 0; u < kInFlight; ++u) a[u] = pv[v + u * kThreads];
-#pragma unroll
-      for (int u = 0; u < kInFlight; ++u) one((v + u * kThreads) * W, a[u]);
-    }
-    for (; v < nv; v += kThreads) one(v * W, pv[v]);
-    for (int i = nv * W + threadIdx.x; i < V; i += kThreads) {
-      const float raw = elem_to_f32<DT>(p[i]);
-      f(i, has_hist ? penalise(P, *sh, i, raw) : raw);
-    }
-  }
-};
-
-// Candidates gathered into LDS (any order).
-struct CandSrc {
-  const Shared *sh;
-  int n;
-  template <class F> __device__ __forceinline__ void each(F f) const {
-    for (int j = threadIdx.x; j < n; j += kThreads) f(sh->ci[j], sh->cx[j]);
-  }
-};
-
-// Every kSampleStride-th element of the row, gathered into the candidate value
-// array before the candidates themselves are.
-constexpr int kSampleStride = 32;
-struct SampleSrc {
-  const Shared *sh;
-  int n;
-  template <class F> __device__ __forceinline__ void each(F f) const {
-    for (int j = threadIdx.x; j < n; j += kThreads) f(j, sh->cx[j]);
-  }
-};
-
-// ---- order statistics over a source ---------------------------------------------------
-// All cuts below are prefixes of one total order: key descending, then index
-// ascending.  They are found with radix selects (11/11/10-bit digits of the
-// key, 10/10-bit digits of the index), so no pass depends on visiting order.
-
-// Key of the k-th largest element (k >= 1) among those where pred(i, x) holds;
-// `above` gets how many have a larger key.
-template <class Src, class Pred>
-__device__ __forceinline__ uint32_t radix_rank(const Src &src, Shared &sh, unsigned long long k,
-                                               Pred pred, unsigned long long &above) {
-  uint32_t prefix = 0;
-  above = 0;
-  for (int pass = 0; pass < 3; ++pass) {
-    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
-    const int hi_shift = shift + (pass == 2 ? 10 : 11);
-    zero_hist(sh);
-    src.each([&](int i, float x) {
-      if (!pred(i, x)) return;
-      const uint32_t key = fkey(x);
-      if (pass > 0 && (key >> hi_shift) != (prefix >> hi_shift)) return;
-      atomicAdd(&sh.hist[(key >> shift) & dmask], 1ull);
-    });
-    __syncthreads();
-    select_bin(sh, above, static_cast<double>(k));
-    prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
-    above = sh.bcast[1];
-  }
-  return prefix;
-}
-
-// Key K where the fixed-point mass of the pred elements, accumulated from the
-// largest key down, reaches `target`: mass(keys > K) < target <=
-// mass(keys >= K).  `extra` is mass to count at key Kx besides the visited
-// elements (ties whose membership is decided by index).  Returns false if
-// the total is below target.
-template <class Src, class Pred>
-__device__ __forceinline__ bool mass_select(const Src &src, Shared &sh, Pred pred, float m,
-                                            double target, uint32_t Kx, unsigned long long extra,
-                                            uint32_t &K, unsigned long long &above) {
-  uint32_t prefix = 0;
-  above = 0;
-  for (int pass = 0; pass < 3; ++pass) {
-    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
-    const int hi_shift = shift + (pass == 2 ? 10 : 11);
-    zero_hist(sh);
-    src.each([&](int i, float x) {
-      if (!pred(i, x)) return;
-      const uint32_t key = fkey(x);
-      if (pass > 0 && (key >> hi_shift) != (prefix >> hi_shift)) return;
-      atomicAdd(&sh.hist[(key >> shift) & dmask], mass_of(x, m));
-    });
-    __syncthreads();
-    if (threadIdx.x == 0 && extra && (pass == 0 || (Kx >> hi_shift) == (prefix >> hi_shift)))
-      sh.hist[(Kx >> shift) & dmask] += extra;
-    __syncthreads();
-    select_bin(sh, above, target);
-    if (!sh.bcast[2]) return false;
-    prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
-    above = sh.bcast[1];
-  }
-  K = prefix;
-  return true;
-}
-
-// Index of the j-th smallest index (j >= 1) among the pred elements (indices
-// below 2^20; the vocabulary limit is 2^18).
-template <class Src, class Pred>
-__device__ __forceinline__ int index_rank(const Src &src, Shared &sh, unsigned long long j,
-                                          Pred pred) {
-  // Ascending index = descending (2^20 - 1 - index).
-  uint32_t prefix = 0;
-  unsigned long long above = 0;
-  for (int pass = 0; pass < 2; ++pass) {
-    const int shift = pass == 0 ? 10 : 0;
-    zero_hist(sh);
-    src.each([&](int i, float x) {
-      if (!pred(i, x)) return;
-      const uint32_t r = 0xfffffu - static_cast<uint32_t>(i);
-      if (pass > 0 && (r >> 10) != (prefix >> 10)) return;
-      atomicAdd(&sh.hist[(r >> shift) & 0x3ffu], 1ull);
-    });
-    __syncthreads();
-    select_bin(sh, above, static_cast<double>(j));
-    prefix |= static_cast<uint32_t>(sh.bcast[0]) << shift;
-    above = sh.bcast[1];
-  }
-  return static_cast<int>(0xfffffu - prefix);
-}
-
-template <class Src, class Pred>
-__device__ __forceinline__ unsigned long long count_if(const Src &src, Shared &sh, Pred pred) {
-  unsigned long long c = 0, total;
-  src.each([&](int i, float x) { c += pred(i, x) ? 1 : 0; });
-  block_exclusive_scan(c, sh, &total);
-  return total;
-}
-
-template <class Src, class Pred>
-__device__ __forceinline__ unsigned long long mass_if(const Src &src, Shared &sh, float m, Pred pred) {
-  unsigned long long z = 0, total;
-  src.each([&](int i, float x) {
-    if (pred(i, x)) z += mass_of(x, m);
-  });
-  block_exclusive_scan(z, sh, &total);
-  return total;
-}
-
-// min_p -> top_k -> top_p -> draw over a source; returns the token.  `Z_all`
-// (when have_Z) is the alive mass of the whole row, used when the source is a
-// candidate subset and no top-k cut bounds the survivors inside it.
-// `partial`: src holds only a prefix of the order (the candidates), no top-k
-// was requested, and Z_all is the mass of every element min_p keeps in the
-// whole row.  A top-p cut or a draw that falls beyond the prefix then returns
-// -1 (the caller takes the whole row) instead of being decided on the prefix.
-template <class Src>
-__device__ __forceinline__ int64_t filter_and_draw(const Src src, Shared &sh, const Params P,
-                                                   float m, long long k_req, bool have_Z,
-                                                   unsigned long long Z_all, float u,
-                                                   bool partial = false) {
-  auto alive = [&](float x) { return P.min_p <= 0.f || expf(x - m) >= P.min_p; };
-  constexpr int kAll = 0x7fffffff;
-
-  // top-k: kept = key > Kk, or key == Kk and index <= Ik.
-  uint32_t Kk = 0;
-  int Ik = kAll;
-  bool k_cut = false;
-  if (k_req > 0) {
-    const unsigned long long alive_cnt = count_if(src, sh, [&](int, float x) { return alive(x); });
-    if (static_cast<unsigned long long>(k_req) < alive_cnt) {
-      unsigned long long above;
-      Kk = radix_rank(src, sh, static_cast<unsigned long long>(k_req),
-                      [&](int, float x) { return alive(x); }, above);
-      Ik = index_rank(src, sh, static_cast<unsigned long long>(k_req) - above,
-                      [&](int, float x) { return alive(x) && fkey(x) == Kk; });
-      k_cut = true;
-    }
-  }
-  auto in_s = [&](int i, float x) {
-    const uint32_t k = fkey(x);
-    return alive(x) && (k > Kk || (k == Kk && i <= Ik));
-  };
-
-  // top-p over the survivors: kept = in_s and (key > Kf, or key == Kf and
-  // index <= If), the shortest prefix whose mass reaches top_p of theirs.
-  uint32_t Kf = Kk;
-  int If = Ik;
-  if (P.top_p < 1.f) {
-    const unsigned long long Z = (have_Z && !k_cut) ? Z_all : mass_if(src, sh, m, in_s);
-    const double target = static_cast<double>(P.top_p) * static_cast<double>(Z);
-    uint32_t K;
-    unsigned long long above;
-    if (mass_select(src, sh, in_s, m, target, 0u, 0ull, K, above)) {
-      const unsigned long long w = mass_of(unkey(K), m);
-      // Ties at K kept: the first j (by index) with above + (j - 1) * w < target.
-      unsigned long long j =
-          w ? static_cast<unsigned long long>(ceil((target - static_cast<double>(above)) / static_cast<double>(w)))
-            : 1;
-      if (j < 1) j = 1;
-      auto tie = [&](int i, float x) { return in_s(i, x) && fkey(x) == K; };
-      const unsigned long long c = count_if(src, sh, tie);
-      Kf = K;
-      If = j >= c ? kAll : index_rank(src, sh, j, tie);
-    } else if (partial) {
-      return -1;  // the cut lies past the prefix
-    }
-  }
-  auto kept = [&](int i, float x) {
-    const uint32_t k = fkey(x);
-    return in_s(i, x) && (k > Kf || (k == Kf && i <= If));
-  };
-
-  // Draw: the element whose interval of the kept mass, accumulated in the same
-  // order (key descending, index ascending), holds u * total.
-  // Kept mass: over src, except for a prefix with nothing cut (then the whole
-  // row's min_p survivors).
-  const bool whole = partial && !(P.top_p < 1.f);
-  const unsigned long long Wtot = whole ? Z_all : mass_if(src, sh, m, kept);
-  unsigned long long T = static_cast<unsigned long long>(static_cast<double>(u) * static_cast<double>(Wtot));
-  if (T >= Wtot) T = Wtot ? Wtot - 1 : 0;
-  uint32_t K;
-  unsigned long long above;
-  if (!mass_select(src, sh, kept, m, static_cast<double>(T) + 1.0, 0u, 0ull, K, above)) {
-    if (whole) return -1;  // the draw lies past the prefix
-    // Unreachable otherwise: the largest kept element always weighs 2^40.
-    return static_cast<int64_t>(index_rank(src, sh, 1, kept));
-  }
-  const unsigned long long w = mass_of(unkey(K), m);
-  const unsigned long long jt = w ? (T - above) / w : 0;
-  return static_cast<int64_t>(
-      index_rank(src, sh, jt + 1, [&](int i, float x) { return kept(i, x) && fkey(x) == K; }));
-}
-
-template <int DT, bool VEC>
-__global__ __launch_bounds__(kThreads) void sample_kernel(
-    const void *logits, int64_t row_stride, int V, const float *temperature,
-    const int32_t *top_k, const float *top_p, const float *min_p, const float *rep,
-    const float *presence, const float *frequency, const int64_t *history, int64_t hist_stride,
-    const int32_t *hist_len, int64_t hist_len_stride, const float *uniforms, int64_t *out) {
-  typedef typename Elem<DT>::T E;
-  extern __shared__ __align__(16) char smem_raw[];
-  Shared &sh = *reinterpret_cast<Shared *>(smem_raw);
-  const int row = blockIdx.x;
-  const int tid = threadIdx.x;
-  Params P;
-  P.temp = temperature[row];
-  P.top_k = top_k ? top_k[row] : -1;
-  P.top_p = top_p ? top_p[row] : 1.f;
-  P.min_p = min_p ? min_p[row] : 0.f;
-  P.rep = rep ? rep[row] : 1.f;
-  P.presence = presence ? presence[row] : 0.f;
-  P.frequency = frequency ? frequency[row] : 0.f;
-  P.use_hash = P.frequency != 0.f;
-
-  // ---- history -> seen bitmap (+ counts) ------------------------------------
-  const int nwords = (V + 31) >> 5;
-  for (int w = tid; w < nwords; w += kThreads) sh.seen[w] = 0u;
-  if (P.use_hash)
-    for (int s = tid; s < kHashSlots; s += kThreads) sh.hkey[s] = 0, sh.hcnt[s] = 0;
-  __syncthreads();
-  int nh = 0;
-  if (history && hist_len) {
-    nh = hist_len[row * hist_len_stride];
-    // At most one row of history (the row stride) and kMaxHist tokens.
-    const int64_t cap = hist_stride < kMaxHist ? hist_stride : kMaxHist;
-    nh = nh < 0 ? 0 : (nh > cap ? static_cast<int>(cap) : nh);
-    for (int j = tid; j < nh; j += kThreads) {
-      const int64_t tok = history[row * hist_stride + j];
-      if (tok < 0 || tok >= V) continue;
-      const int t32 = static_cast<int>(tok);
-      atomicOr(&sh.seen[t32 >> 5], 1u << (t32 & 31));
-      if (P.use_hash) {
-        int s = hash_slot(t32);
-        while (true) {
-          const int prev = atomicCAS(&sh.hkey[s], 0, t32 + 1);
-          if (prev == 0 || prev == t32 + 1) break;
-          s = (s + 1) % kHashSlots;
-        }
-        atomicAdd(&sh.hcnt[s], 1);
-      }
-    }
-  }
-  __syncthreads();
-
-  GlobalSrc<DT, VEC> g;
-  g.p = reinterpret_cast<const E *>(logits) + row * row_stride;
-  g.V = V;
-  g.P = P;
-  g.sh = &sh;
-
-  // ---- greedy: argmax of the penalised logits, first index on ties ------------
-  if (P.temp < kGreedyTemp) {
-    unsigned long long best = 0;
-    g.each_raw([&](int i, E raw) {
-      const unsigned long long k =
-          (static_cast<unsigned long long>(fkey(penalise(P, sh, i, elem_to_f32<DT>(raw)))) << 32) |
-          (0xffffffffu - static_cast<uint32_t>(i));
-      best = k > best ? k : best;
-    });
-    best = block_max_u64(best, sh);
-    if (tid == 0) out[row] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
-    return;
-  }
-
-  const long long k_req = (P.top_k < 0 || P.top_k >= V) ? -1 : P.top_k;
-  const float u = uniforms ? uniforms[row] : 0.f;
-
-  // ---- pass A (on the penalised logits v; x = v / temperature preserves
-  // their order): max, and every 32nd value as a sample ----
-  const bool has_hist = nh > 0;
-  float mv = -INFINITY;
-  const bool sample = true;  // the candidate bound comes from these samples
-  g.each_pen([&](int i, float v) {
-    mv = fmaxf(mv, v);
-    if (sample && (i % kSampleStride) == 0) sh.cx[i / kSampleStride] = v;
-  }, has_hist);
-  mv = block_max(mv, sh);
-  const float m = mv / P.temp;  // the largest x
-
-  // ---- candidates: the elements at or above a bound L, a prefix of the
-  // order, gathered into LDS.  L is taken from the samples: with a top-k cut,
-  // the r-th largest sample, r a margin above k / kSampleStride, so that when
-  // the candidates number at least k and fit in LDS the k largest (alive or
-  // not) are among them, and so is everything any later cut keeps.  Without a
-  // top-k cut, about kNoCutCand candidates; the same sweep then sums the mass
-  // of every min_p survivor of the row, and the candidates decide the row
-  // whenever the top-p cut and the draw fall inside them.  Otherwise the row
-  // itself is the source.  The bound is taken 64 key steps low: an element
-  // just under it in v may round to the same x as one above it.
-  int64_t tok = -1;
-  unsigned long long Z_alive = 0;
-  {
-    SampleSrc smp_src;
-    smp_src.sh = &sh;
-    smp_src.n = (V + kSampleStride - 1) / kSampleStride;
-    const long long kk = k_req > 0 ? (k_req + kSampleStride - 1) / kSampleStride
-                                   : kNoCutCand / kSampleStride;
-    const long long r = min<long long>(smp_src.n, kk + (kk + 1) / 2 + 8);
-    unsigned long long above;
-    const uint32_t Ls =
-        radix_rank(smp_src, sh, static_cast<unsigned long long>(r), [](int, float) { return true; }, above);
-    const uint32_t L = Ls > 64u ? Ls - 64u : 0u;
-    // Unordered append; the counter keeps counting past the capacity.
-    __syncthreads();
-    if (tid == 0) sh.bcast[3] = 0;
-    __syncthreads();
-    const bool sum_alive = k_req <= 0;
-    unsigned long long z = 0;
-    g.each_pen([&](int i, float v) {
-      if (sum_alive) {
-        const float x = v / P.temp;
-        if (P.min_p <= 0.f || expf(x - m) >= P.min_p) z += mass_of(x, m);
-      }
-      if (fkey(v) < L) return;
-      const unsigned long long o = atomicAdd(&sh.bcast[3], 1ull);
-      if (o < static_cast<unsigned long long>(kCand)) {
-        sh.cx[o] = v / P.temp;
-        sh.ci[o] = i;
-      }
-    }, has_hist);
-    __syncthreads();
-    const unsigned long long n_c = sh.bcast[3];
-    if (sum_alive) block_exclusive_scan(z, sh, &Z_alive);
-    if (n_c <= static_cast<unsigned long long>(kCand) &&
-        n_c >= static_cast<unsigned long long>(k_req > 0 ? k_req : 1)) {
-      CandSrc cs;
-      cs.sh = &sh;
-      cs.n = static_cast<int>(n_c);
-      tok = k_req > 0 ? filter_and_draw(cs, sh, P, m, k_req, false, 0, u)
-                      : filter_and_draw(cs, sh, P, m, k_req, true, Z_alive, u, true);
-    }
-  }
-  if (tok < 0) tok = filter_and_draw(g, sh, P, m, k_req, k_req <= 0, Z_alive, u);
-  if (tid == 0) out[row] = tok;
-}
-
-struct Args {
-  const void *logits;
-  int64_t row_stride;
-  int V;
-  const float *temperature;
-  const int32_t *top_k;
-  const float *top_p, *min_p, *rep, *presence, *frequency;
-  const int64_t *history;
-  int64_t hist_stride;
-  const int32_t *hist_len;
-  int64_t hist_len_stride;
-  const float *uniforms;
-  int64_t *out;
-};
-
-template <int DT, bool VEC>
-int launch(const Args &a, int rows, hipStream_t stream) {
-  static bool attr_set = false;  // per instantiation
-  const size_t shm = sizeof(Shared);
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&sample_kernel<DT, VEC>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(shm));
-    if (e != hipSuccess) return fail(SPK_EHIP, "sample: %s", hipGetErrorString(e));
-    attr_set = true;
-  }
-  sample_kernel<DT, VEC><<<rows, kThreads, shm, stream>>>(
-      a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.top_p, a.min_p, a.rep, a.presence,
-      a.frequency, a.history, a.hist_stride, a.hist_len, a.hist_len_stride, a.uniforms, a.out);
-  return check_launch("sample");
-}
-
+extern template int launch<SPK_F32, true>(const Args &, int, hipStream_t);
+extern template int launch<SPK_F32, false>(const Args &, int, hipStream_t);
+extern template int launch<SPK_F16, true>(const Args &, int, hipStream_t);
+extern template int launch<SPK_F16, false>(const Args &, int, hipStream_t);
+extern template int launch<SPK_BF16, true>(const Args &, int, hipStream_t);
+extern template int launch<SPK_BF16, false>(const Args &, int, hipStream_t);
 }  // namespace smp
 }  // namespace spk
 
