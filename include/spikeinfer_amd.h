@@ -69,7 +69,8 @@ int spk_abi_version(void);
  * position p < seq_lens[n] lives in slot block_tables[n][p/bs]*bs + p%bs; the
  * score is popcount(q & k) * scale; out = softmax(scores) @ unpacked(v).
  * W must equal ceil(head_dim/32); head_dim <= 128; block_size a power of two.
- * A sequence with seq_len <= 0 gets an all-zero output row.  Slots outside
+ * A sequence with seq_len <= 0 gets an all-zero output row; a seq_len past
+ * max_blocks*block_size is clamped to it (the table addresses no more).  Slots outside
  * [0, num_slots) are never dereferenced, so a corrupt block table cannot
  * fault the GPU (the output rows of such a sequence are unspecified).  scale must satisfy
  * 0 < scale*head_dim <= 80 (the softmax uses the fixed offset popcount(q)).
@@ -92,6 +93,62 @@ int spk_decode_attn(const int32_t *q, const int64_t q_strides[4],
 size_t spk_decode_attn_workspace_bytes(int T, int N, int Hq, int Hkv,
                                        int head_dim, int block_size,
                                        int max_blocks);
+
+/*
+ * The split-context halves of spk_decode_attn as separate operators.  The
+ * reference has no split (its kernel walks each context in one program,
+ * spike_attention.py:67-150, docs/architecture.md:225-228); these exist so a
+ * context split into partitions -- within one launch, or across launches or
+ * devices -- can be combined by the caller.
+ *
+ * spk_decode_attn_partials: same inputs and indexing as spk_decode_attn; the
+ * context of every sequence is cut into partitions of part_len tokens
+ * (a multiple of block_size, at most 32768) and partition p of row (t, n, h)
+ * writes, unnormalised,
+ *   partials[(((p*T + t)*N + n)*Hq + h)*(head_dim + 1) + c] = sum_j w_j * v_j[c]
+ *   ... + head_dim]                                        = sum_j w_j
+ * with w_j = exp(-popcount(q & ~k_j) * scale), j over the partition's tokens.
+ * The weights share the fixed offset popcount(q), so partials of any
+ * partitioning add.  partials_bytes must cover
+ * ceil(max_blocks*block_size / part_len) * T*N*Hq*(head_dim+1) floats;
+ * partitions at or past a sequence's length are not written.
+ *
+ * spk_decode_attn_combine: out[t, n, h, c] = sum_p a / sum_p l over the
+ * partitions p < ceil(seq_lens[n] / part_len) (at most num_parts), summed in
+ * partition order; a sequence with seq_len <= 0 gets zeros.
+ */
+int spk_decode_attn_partials(const int32_t *q, const int64_t q_strides[4],
+                             const int32_t *k_cache, const int64_t k_strides[4],
+                             const int32_t *v_cache, const int64_t v_strides[4],
+                             int64_t num_slots, const int32_t *block_tables,
+                             int64_t bt_stride0, int64_t bt_stride1,
+                             const int32_t *seq_lens, int T, int N, int Hq, int Hkv,
+                             int head_dim, int block_size, int max_blocks, float scale,
+                             int part_len, float *partials, size_t partials_bytes,
+                             void *stream);
+int spk_decode_attn_combine(const float *partials, int num_parts, int part_len,
+                            const int32_t *seq_lens, void *out, int out_dtype,
+                            const int64_t out_strides[4], int T, int N, int Hq,
+                            int head_dim, void *stream);
+
+/*
+ * Prefill reader: one sequence's first seq_len cached tokens as dense 0/1
+ * spikes, K and V in one launch.  Replaces gather_kv_unpacked
+ * (spikeinfer/kernels/spike_attention.py:224-244: slot-matrix index_select,
+ * then unpack_spikes, once per cache).
+ *
+ *   k_cache, v_cache int32 [T, H, num_slots, W] at cache_strides (v_cache may
+ *            be NULL, then v_out must be too)
+ *   block_table  the sequence's row, n_table entries at stride bt_stride
+ *   k_out, v_out [T, H, seq_len, head_dim] contiguous in out_dtype (any type)
+ * Token p reads slot table[p/bs]*bs + p%bs; positions past the table or whose
+ * block lies outside the cache read as zeros.
+ */
+int spk_gather_unpack(const int32_t *k_cache, const int32_t *v_cache,
+                      const int64_t cache_strides[4], int64_t num_slots,
+                      const int32_t *block_table, int64_t bt_stride, int n_table,
+                      int seq_len, void *k_out, void *v_out, int out_dtype, int T,
+                      int H, int head_dim, int block_size, void *stream);
 
 /*
  * Raw integer attention scores popcount(q & k) for every (t, n, h, position

@@ -42,6 +42,13 @@ _SIGNATURES = {
         _vp, _i64p, _vp, _i64p, _vp, _i64p, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _i64p,
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
     "spk_decode_attn_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "spk_decode_attn_partials": (_i32, [
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _i64, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32,
+        _i32, _i32, _i32, _f32, _i32, _vp, _sz, _vp]),
+    "spk_decode_attn_combine": (_i32, [
+        _vp, _i32, _i32, _vp, _vp, _i32, _i64p, _i32, _i32, _i32, _i32, _vp]),
+    "spk_gather_unpack": (_i32, [
+        _vp, _vp, _i64p, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "spk_qkv_decode_attn": (_i32, [
         _vp, _i32, _i64p, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _vp, _i64p, _i64, _vp,
         _i64, _i64, _vp, _vp, _i32, _i64p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp,

@@ -21,78 +21,58 @@ import torch.nn.functional as F
 
 from .kernels.lif import lif_multistep, lif_pack_write
 from .kernels.packing import pack_spikes, packed_width
-from .kernels.spike_attention import gather_kv_unpacked, paged_spike_attn_decode
+from .kernels.spike_attention import gather_kv_unpacked_pair, paged_spike_attn_decode
 
 
 @dataclass
 class AttentionMetadata:
-    """Everything attention needs that is not a weight or an activation
-    (spikeinfer/attention.py:33-95)."""
+    """Per-step batch description consumed by the attention operators.
 
-    slot_mapping: torch.Tensor
-    """int64 ``[n_tok]``: physical cache slot of each token of the batch."""
+    Field names are the engine's contract (spikeinfer/attention.py:33-95).
+    Tokens are ordered decodes first: rows ``[0, num_decode_tokens)`` are one
+    decode token per sequence, described by ``block_tables``/``seq_lens``;
+    the rest are prefill chunks described by the four ``prefill_*`` lists.
+    """
 
+    slot_mapping: torch.Tensor  # int64 [n_tok]: cache slot each token's K/V bits go to
     block_size: int
     num_decode_tokens: int = 0
-
+    # int32 [n_dec, max_blocks]; unused entries hold the cache's pad block
     block_tables: torch.Tensor | None = None
-    """int32 ``[n_dec, max_blocks]``; rows padded with the pad block."""
+    # int32 [n_dec]; counts the token being decoded (its K/V is written first)
     seq_lens: torch.Tensor | None = None
-    """int32 ``[n_dec]``: cached length including the token being decoded."""
-
+    # chunk i covers batch rows [starts[i], starts[i] + query_lens[i]) and sits
+    # after context_lens[i] already-cached positions of its sequence
     prefill_query_starts: list[int] = field(default_factory=list)
     prefill_query_lens: list[int] = field(default_factory=list)
     prefill_context_lens: list[int] = field(default_factory=list)
     prefill_block_tables: list[torch.Tensor] = field(default_factory=list)
 
-    _mirrors: dict = field(default_factory=dict, repr=False, compare=False)
-
     @property
     def num_prefills(self) -> int:
         return len(self.prefill_query_lens)
 
-    def on(self, device: torch.device) -> "AttentionMetadata":
-        """This metadata with its tensors on ``device`` (memoised per device)."""
-        if self.slot_mapping.device == device:
-            return self
-        key = str(device)
-        mirror = self._mirrors.get(key)
-        if mirror is None:
-            move = lambda t: None if t is None else t.to(device, non_blocking=True)
-            mirror = AttentionMetadata(
-                slot_mapping=move(self.slot_mapping),
-                block_size=self.block_size,
-                num_decode_tokens=self.num_decode_tokens,
-                block_tables=move(self.block_tables),
-                seq_lens=move(self.seq_lens),
-                prefill_query_starts=self.prefill_query_starts,
-                prefill_query_lens=self.prefill_query_lens,
-                prefill_context_lens=self.prefill_context_lens,
-                prefill_block_tables=[move(t) for t in self.prefill_block_tables],
-            )
-            self._mirrors[key] = mirror
-        return mirror
-
 
 def _causal_offset_mask(query_len: int, total_len: int, device, dtype) -> torch.Tensor:
-    """Mask of ``query_len`` queries sitting after ``total_len - query_len`` cached
-    positions (spikeinfer/attention.py:320-330 semantics)."""
+    """Additive mask letting query i (at position total_len - query_len + i)
+    see positions <= its own (spikeinfer/attention.py:320-330)."""
     ctx = total_len - query_len
     mask = torch.full((query_len, total_len), float("-inf"), device=device, dtype=dtype)
     return torch.triu(mask, diagonal=ctx + 1)
 
 
 def _prefill(q_dense, k_cache, v_cache, meta, out, num_q_heads, num_kv_heads, head_dim):
-    """Prefill chunks: unpack-gather the sequence's cache, SDPA with the offset
-    causal mask (spikeinfer/attention.py:161-178)."""
+    """Each prefill chunk attends to its sequence's whole cached prefix plus
+    itself: one gather-unpack launch yields dense K and V, then SDPA with the
+    offset causal mask (spikeinfer/attention.py:161-178)."""
     dtype, device = q_dense.dtype, q_dense.device
     for i in range(meta.num_prefills):
         start = meta.prefill_query_starts[i]
         q_len = meta.prefill_query_lens[i]
         total = meta.prefill_context_lens[i] + q_len
         table = meta.prefill_block_tables[i]
-        k_all = gather_kv_unpacked(k_cache, table, total, head_dim, meta.block_size, dtype)
-        v_all = gather_kv_unpacked(v_cache, table, total, head_dim, meta.block_size, dtype)
+        k_all, v_all = gather_kv_unpacked_pair(k_cache, v_cache, table, total, head_dim,
+                                               meta.block_size, dtype)
         q = q_dense[:, :, start:start + q_len, :]  # [T, H_q, q_len, D]
         o = F.scaled_dot_product_attention(
             q, k_all, v_all,

@@ -20,6 +20,8 @@
 //     order (bit-reproducible run to run).
 #include "decode_attn.hpp"
 
+#include <algorithm>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 
@@ -47,7 +49,7 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_general(AttnParams p
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  const int len = p.lens[n];
+  const int len = seq_len(p, n);
   const int nparts_seq = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
   if (part >= nparts_seq) return;
   const int start = part * p.part_len;
@@ -144,7 +146,7 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_general(AttnParams p
   }
   __syncthreads();
 
-  const bool single = nparts_seq == 1;
+  const bool single = nparts_seq == 1 && !p.partials_only;
   for (int idx = tid; idx < p.nrep * hd; idx += kAttnThreads) {
     const int h = idx / hd;
     const int ch = idx % hd;
@@ -175,17 +177,18 @@ __global__ __launch_bounds__(256) void decode_attn_combine(AttnParams p) {
   const int hq = static_cast<int>(row % p.Hq);
   const int n = static_cast<int>((row / p.Hq) % p.N);
   const int t = static_cast<int>(row / ((int64_t)p.Hq * p.N));
-  const int len = p.lens[n];
+  const int len = seq_len(p, n);
   const int nparts = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
-  if (nparts <= 1) return;
+  if (nparts <= 1 && !p.partials_only) return;  // the attention kernel wrote it
   const int64_t stride_part = (int64_t)p.T * p.N * p.Hq * (hd + 1);
   const float *src = p.ws + row * (hd + 1);
   float a = 0.f, l = 0.f;
-  for (int q = 0; q < nparts; ++q) {
+  for (int q = 0; q < min(nparts, p.num_parts); ++q) {
     a += src[q * stride_part + ch];
     l += src[q * stride_part + hd];
   }
-  store_f32_as(p.out, t * p.os0 + n * p.os1 + hq * p.os2 + ch * p.os3, p.out_dtype, a / l);
+  store_f32_as(p.out, t * p.os0 + n * p.os1 + hq * p.os2 + ch * p.os3, p.out_dtype,
+               len <= 0 ? 0.f : a / l);
 }
 
 // Integer scores popc(q & k) for every valid position (score-path check).
@@ -196,7 +199,7 @@ __global__ __launch_bounds__(256) void decode_scores_kernel(AttnParams p, int32_
   const int kvh = blockIdx.y % p.Hkv;
   const int n = blockIdx.z;
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  const int len = p.lens[n];
+  const int len = seq_len(p, n);
   if (j >= len || j >= max_len) return;
   const int phys = p.bt[n * p.bts0 + (j >> p.bs_log2) * p.bts1];
   const int64_t slot = (static_cast<int64_t>(phys) << p.bs_log2) | (j & ((1 << p.bs_log2) - 1));
@@ -275,17 +278,29 @@ static int decode_attn_impl(const int32_t *q, const int64_t q_strides[4], const 
                             const int64_t out_strides[4], int T, int N, int Hq, int Hkv,
                             int head_dim, int block_size, int max_blocks, float scale,
                             void *workspace, size_t workspace_bytes, void *stream,
-                            const FusedParams *fz, int fused_dtype) {
+                            const FusedParams *fz, int fused_dtype, int forced_part_len = 0,
+                            float *partials = nullptr, size_t partials_bytes = 0) {
   int rc = check_common(T, N, Hq, Hkv, head_dim, block_size);
   if (rc) return rc;
-  if (!valid_float_dtype(out_dtype)) return fail(SPK_EINVAL, "out dtype %d not a float type", out_dtype);
+  if (!partials && !valid_float_dtype(out_dtype))
+    return fail(SPK_EINVAL, "out dtype %d not a float type", out_dtype);
   if ((!fz && q_strides[3] != 1) || k_strides[3] != 1 || v_strides[3] != 1)
     return fail(SPK_EINVAL, "packed word axis must be contiguous");
   if (!(scale > 0.f) || scale * head_dim > 80.f)
     return fail(SPK_EINVAL, "scale=%g outside (0, 80/head_dim]", (double)scale);
   if (max_blocks <= 0) return fail(SPK_EINVAL, "max_blocks=%d", max_blocks);
+  const int64_t ctx_max = (int64_t)max_blocks * block_size;
+  if (partials) {
+    if (forced_part_len < block_size || forced_part_len % block_size || forced_part_len > 32768)
+      return fail(SPK_EINVAL, "part_len=%d must be a multiple of block_size=%d in [%d, 32768]",
+                  forced_part_len, block_size, block_size);
+    const size_t need_p = (size_t)((ctx_max + forced_part_len - 1) / forced_part_len) * T * N * Hq *
+                          (head_dim + 1) * sizeof(float);
+    if (partials_bytes < need_p)
+      return fail(SPK_EINVAL, "partials buffer of %zu bytes, need %zu", partials_bytes, need_p);
+  }
   if (N == 0) return SPK_OK;
-  const size_t need = spk_decode_attn_workspace_bytes(T, N, Hq, Hkv, head_dim, block_size, max_blocks);
+  const size_t need = partials ? 0 : spk_decode_attn_workspace_bytes(T, N, Hq, Hkv, head_dim, block_size, max_blocks);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(SPK_EINVAL, "workspace of %zu bytes, need %zu", workspace_bytes, need);
 
@@ -305,10 +320,11 @@ static int decode_attn_impl(const int32_t *q, const int64_t q_strides[4], const 
   p.os0 = out_strides[0]; p.os1 = out_strides[1]; p.os2 = out_strides[2]; p.os3 = out_strides[3];
   p.T = T; p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.head_dim = head_dim;
   p.bs_log2 = ilog2(block_size); p.nrep = Hq / Hkv; p.scale = scale;
-  const int64_t ctx_max = (int64_t)max_blocks * block_size;
-  p.part_len = choose_part_len((int64_t)N * T * Hkv, ctx_max, block_size);
+  p.ctx_cap = (int)std::min<int64_t>(ctx_max, INT32_MAX);
+  p.part_len = partials ? forced_part_len : choose_part_len((int64_t)N * T * Hkv, ctx_max, block_size);
   p.num_parts = (int)((ctx_max + p.part_len - 1) / p.part_len);
-  p.ws = static_cast<float *>(workspace);
+  p.ws = partials ? partials : static_cast<float *>(workspace);
+  p.partials_only = partials != nullptr;
   if (p.ws == nullptr && need > 0) return fail(SPK_EINVAL, "workspace required");
   if (fz) p.fz = *fz;
 
@@ -320,8 +336,11 @@ static int decode_attn_impl(const int32_t *q, const int64_t q_strides[4], const 
   if (!force_general && mfma_path_supported(p)) {
     build_digit_table(scale, p.digits);
     const size_t partial_floats = p.num_parts > 1 ? (size_t)p.num_parts * T * N * Hq * (head_dim + 1) : 0;
-    const bool plan = plan_launch(ctx_max);
-    int32_t *order = plan_in_workspace(ctx_max, (int64_t)p.num_parts * N)
+    // The partials entry orders its items only when the kernel can do it
+    // itself (it has no workspace for a planner's list).
+    const bool plan = plan_launch(ctx_max) &&
+                      (!partials || (int64_t)p.num_parts * N <= kInlinePlanItems);
+    int32_t *order = !partials && plan_in_workspace(ctx_max, (int64_t)p.num_parts * N)
                          ? reinterpret_cast<int32_t *>(p.ws + partial_floats) : nullptr;
     // Short contexts whose whole grid is resident at once (8 two-wave
     // workgroups per CU) run 2 waves per unit: one round of workgroups
@@ -341,7 +360,7 @@ static int decode_attn_impl(const int32_t *q, const int64_t q_strides[4], const 
     default: launch_general<4>(p, grid, s); break;
   }
   if ((rc = check_launch("decode_attn"))) return rc;
-  if (p.num_parts > 1) {
+  if (p.num_parts > 1 && !partials) {
     const int64_t elems = (int64_t)T * N * Hq * head_dim;
     decode_attn_combine<<<static_cast<unsigned>((elems + 255) / 256), 256, 0, s>>>(p);
     if ((rc = check_launch("decode_attn_combine"))) return rc;
@@ -361,6 +380,50 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
                           block_tables, bt_stride0, bt_stride1, seq_lens, out, out_dtype,
                           out_strides, T, N, Hq, Hkv, head_dim, block_size, max_blocks, scale,
                           workspace, workspace_bytes, stream, nullptr, 0);
+}
+
+extern "C" int spk_decode_attn_partials(const int32_t *q, const int64_t q_strides[4],
+                                        const int32_t *k_cache, const int64_t k_strides[4],
+                                        const int32_t *v_cache, const int64_t v_strides[4],
+                                        int64_t num_slots, const int32_t *block_tables,
+                                        int64_t bt_stride0, int64_t bt_stride1,
+                                        const int32_t *seq_lens, int T, int N, int Hq, int Hkv,
+                                        int head_dim, int block_size, int max_blocks, float scale,
+                                        int part_len, float *partials, size_t partials_bytes,
+                                        void *stream) {
+  if (!partials) return fail(SPK_EINVAL, "decode_attn_partials: null partials buffer");
+  const int64_t ostr[4] = {0, 0, 0, 0};
+  return decode_attn_impl(q, q_strides, k_cache, k_strides, v_cache, v_strides, num_slots,
+                          block_tables, bt_stride0, bt_stride1, seq_lens, nullptr, SPK_F32, ostr,
+                          T, N, Hq, Hkv, head_dim, block_size, max_blocks, scale, nullptr, 0,
+                          stream, nullptr, 0, part_len, partials, partials_bytes);
+}
+
+extern "C" int spk_decode_attn_combine(const float *partials, int num_parts, int part_len,
+                                       const int32_t *seq_lens, void *out, int out_dtype,
+                                       const int64_t out_strides[4], int T, int N, int Hq,
+                                       int head_dim, void *stream) {
+  if (T <= 0 || N < 0 || Hq <= 0 || head_dim <= 0 || num_parts <= 0 || part_len <= 0)
+    return fail(SPK_EINVAL, "decode_attn_combine: bad sizes T=%d N=%d Hq=%d D=%d parts=%d part_len=%d",
+                T, N, Hq, head_dim, num_parts, part_len);
+  if (!valid_float_dtype(out_dtype)) return fail(SPK_EINVAL, "out dtype %d not a float type", out_dtype);
+  if (N == 0) return SPK_OK;
+  if (!partials || !seq_lens || !out) return fail(SPK_EINVAL, "decode_attn_combine: null pointer");
+  AttnParams p{};
+  p.lens = seq_lens;
+  // Partitions past num_parts do not exist in the buffer: lengths beyond
+  // num_parts * part_len are clamped to it.
+  p.ctx_cap = (int)std::min<int64_t>((int64_t)num_parts * part_len, INT32_MAX);
+  p.out = out; p.out_dtype = out_dtype;
+  p.os0 = out_strides[0]; p.os1 = out_strides[1]; p.os2 = out_strides[2]; p.os3 = out_strides[3];
+  p.T = T; p.N = N; p.Hq = Hq; p.head_dim = head_dim;
+  p.part_len = part_len; p.num_parts = num_parts;
+  p.ws = const_cast<float *>(partials);
+  p.partials_only = 1;
+  const int64_t elems = (int64_t)T * N * Hq * head_dim;
+  decode_attn_combine<<<static_cast<unsigned>((elems + 255) / 256), 256, 0,
+                        static_cast<hipStream_t>(stream)>>>(p);
+  return check_launch("decode_attn_combine");
 }
 
 extern "C" int spk_qkv_decode_attn(const void *x, int x_dtype, const int64_t x_strides[2],
@@ -428,6 +491,7 @@ extern "C" int spk_decode_scores(const int32_t *q, const int64_t q_strides[4],
   p.lens = seq_lens;
   p.T = T; p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.head_dim = head_dim;
   p.bs_log2 = ilog2(block_size); p.nrep = Hq / Hkv;
+  p.ctx_cap = max_len;  // positions past max_len have no score slot
   hipStream_t s = static_cast<hipStream_t>(stream);
   dim3 grid((max_len + 255) / 256, T * Hkv, N);
   switch ((head_dim + 31) / 32) {

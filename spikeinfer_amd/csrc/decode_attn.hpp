@@ -45,6 +45,11 @@ struct AttnParams {
   int out_dtype;
   int64_t os0, os1, os2, os3;
   int T, N, Hq, Hkv, head_dim, bs_log2, nrep;
+  // Tokens the block table can address (max_blocks * block_size, at most
+  // INT_MAX): every kernel reads seq_lens through seq_len(), which clamps to
+  // it, so a length past the table never indexes beyond the table's row or
+  // the sized partitions.
+  int ctx_cap;
   float scale;
   int part_len;      // tokens per partition (multiple of 256 and of block size)
   int num_parts;     // partitions per sequence at most
@@ -56,6 +61,10 @@ struct AttnParams {
   // Matrix-core path: the main kernel computes the longest-first order itself
   // (N * num_parts <= kInlinePlanItems) instead of reading `order`.
   int plan_inline;
+  // Every (sequence, partition) writes its partial sums to `ws`, also when the
+  // sequence has a single partition (spk_decode_attn_partials); the combine
+  // then normalises every row.
+  int partials_only;
   // Matrix-core path: for d = popc(q & ~k) in 0..head_dim (<= 128), the four
   // e4m3 digits of exp(-d*scale) * 2^8 (byte s weighs 2^-(4s)), built on the
   // host once per scale (build_digit_table) and copied into LDS by every
@@ -63,6 +72,10 @@ struct AttnParams {
   uint32_t digits[kDigitEntries];
   FusedParams fz;  // used by the fused instantiations only
 };
+
+// Length of sequence n as the kernels use it: seq_lens[n] clamped to the
+// tokens the block table can address.
+__device__ __forceinline__ int seq_len(const AttnParams &p, int n) { return min(p.lens[n], p.ctx_cap); }
 
 // Fills digits[0..128] for `scale` (host; reuses the last table when unchanged).
 void build_digit_table(float scale, uint32_t digits[kDigitEntries]);

@@ -228,7 +228,7 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh) {
   // Bucket of item i, -1 when the sequence has no such partition.
   auto key = [&](int i) {
     const int n = i % p.N, part = i / p.N;
-    const int len = p.lens[n];
+    const int len = seq_len(p, n);
     const int nparts = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
     if (part >= nparts) return -1;
     const int size = min(p.part_len, len - part * p.part_len);
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  const int len = p.lens[n];
+  const int len = seq_len(p, n);
   const int nparts_seq = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
   if (part >= nparts_seq) return;
   const int start = part * p.part_len;
@@ -644,7 +644,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
     for (int k = 0; k < 2; ++k) lh[k] += src[kVals + k];
   }
 
-  const bool single = nparts_seq == 1;
+  const bool single = nparts_seq == 1 && !p.partials_only;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const int h = 4 * rt + (lane >> 4);
@@ -734,7 +734,7 @@ namespace mfma {
 // adjacent.  Items past a sequence's length are left out (their blocks exit).
 // Ties are placed in arbitrary order: each item computes the same sums
 // wherever it runs, so outputs do not depend on it.
-__global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, int N, int UPS,
+__global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, int ctx_cap, int N, int UPS,
                                                         int part_len, int num_parts,
                                                         int32_t *order) {
   __shared__ int count[kMaxBuckets];
@@ -753,7 +753,7 @@ __global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, in
   };
   for (int i = tid; i < N * num_parts; i += blockDim.x) {
     const int n = i % N, part = i / N;
-    const int len = lens[n];
+    const int len = min(lens[n], ctx_cap);
     if (exists(len, part)) atomicAdd(&count[bucket(len, part)], UPS);
   }
   __syncthreads();
@@ -768,7 +768,7 @@ __global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, in
   __syncthreads();
   for (int i = tid; i < N * num_parts; i += blockDim.x) {
     const int n = i % N, part = i / N;
-    const int len = lens[n];
+    const int len = min(lens[n], ctx_cap);
     if (!exists(len, part)) continue;
     const int at = atomicAdd(&offset[bucket(len, part)], UPS);
     for (int ut = 0; ut < UPS; ++ut) order[at + ut] = part * (N * UPS) + n * UPS + ut;
@@ -789,7 +789,7 @@ void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s, 
     p.plan_inline = 1;
     grid = dim3(units * p.num_parts);
   } else if (plan) {
-    mfma::decode_attn_plan<<<1, 1024, 0, s>>>(p.lens, p.N, p.T * p.Hkv, p.part_len, p.num_parts,
+    mfma::decode_attn_plan<<<1, 1024, 0, s>>>(p.lens, p.ctx_cap, p.N, p.T * p.Hkv, p.part_len, p.num_parts,
                                               order);
     p.order = order;
     grid = dim3(units * p.num_parts);

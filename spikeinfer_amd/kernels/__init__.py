@@ -1,7 +1,9 @@
 """Public kernel API, mirroring spikeinfer/kernels/__init__.py:1-29.
 
-Every function here launches HIP kernels on gfx950 through the C ABI in
-include/spikeinfer_amd.h; none has a CPU fallback.
+The operators launch HIP kernels on gfx950 through the C ABI in
+include/spikeinfer_amd.h and have no CPU fallback.  The ``*_ref`` /
+``*_cpu`` names (reference_paths.py) are the reference's eager-torch paths,
+restated; the operators never call them.
 """
 from .lif import lif_multistep, lif_pack_write, validate_thresholds
 from .packing import (
@@ -11,15 +13,28 @@ from .packing import (
     packed_width,
     unpack_spikes,
 )
+from .reference_paths import (
+    lif_multistep_ref,
+    paged_spike_attn_decode_cpu,
+    paged_spike_attn_decode_ref,
+    unpack_spikes_torch,
+)
 from .spike_attention import (
+    combine_partitions,
     decode_attn_workspace_bytes,
     gather_kv_unpacked,
+    gather_kv_unpacked_pair,
+    paged_spike_attn_decode_partials,
     paged_spike_attn_decode,
     paged_spike_attn_scores,
 )
 
 __all__ = [
     "lif_multistep",
+    "lif_multistep_ref",
+    "paged_spike_attn_decode_ref",
+    "paged_spike_attn_decode_cpu",
+    "unpack_spikes_torch",
     "lif_pack_write",
     "validate_thresholds",
     "pack_spikes",
@@ -31,4 +46,7 @@ __all__ = [
     "paged_spike_attn_scores",
     "decode_attn_workspace_bytes",
     "gather_kv_unpacked",
+    "gather_kv_unpacked_pair",
+    "paged_spike_attn_decode_partials",
+    "combine_partitions",
 ]

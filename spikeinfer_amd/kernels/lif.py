@@ -49,8 +49,8 @@ def lif_multistep(x, beta, threshold, mem0=None, out_dtype=None, return_membrane
     M = x3.shape[1]
     beta_c = _param(beta, N, dev)
     th_c = _param(threshold, N, dev)
-    if beta_c.dtype != th_c.dtype:
-        th_c = th_c.to(beta_c.dtype)
+    if beta_c.dtype != th_c.dtype:  # mixed dtypes: both to fp32 (exact), as the reference loads them
+        beta_c, th_c = beta_c.float(), th_c.float()
     spike_dtype = torch.uint8 if out_dtype == torch.bool else out_dtype
     spikes = torch.empty((T, M, N), device=dev, dtype=spike_dtype)
     u_out = torch.empty((M, N), device=dev, dtype=torch.float32) if return_membrane else None
@@ -132,8 +132,8 @@ def lif_pack_write(
         spike_dtype = _lib.dtype_code(sd)
     beta_c = _param(beta, D, dev)
     th_c = _param(threshold, D, dev)
-    if beta_c.dtype != th_c.dtype:
-        th_c = th_c.to(beta_c.dtype)
+    if beta_c.dtype != th_c.dtype:  # mixed dtypes: both to fp32 (exact), as the reference loads them
+        beta_c, th_c = beta_c.float(), th_c.float()
     _lib.check(
         _lib.load().spk_lif_pack_write(
             x.data_ptr(), _lib.dtype_code(x.dtype), _lib.strides(x),

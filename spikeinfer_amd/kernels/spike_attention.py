@@ -13,7 +13,7 @@ import math
 import torch
 
 from .. import _lib
-from .packing import packed_width, unpack_spikes
+from .packing import packed_width
 
 
 def _as_int32(t: torch.Tensor) -> torch.Tensor:
@@ -152,6 +152,35 @@ def paged_spike_attn_scores(
     return scores
 
 
+def _gather(k_cache, v_cache, block_table, seq_len, head_dim, block_size, dtype):
+    dev = _lib.require_gpu(k_cache, v_cache, block_table)
+    _check_packed("cache", k_cache)
+    if v_cache is not None and (v_cache.shape != k_cache.shape or v_cache.stride() != k_cache.stride()):
+        raise ValueError("k and v caches must have the same shape and strides")
+    if k_cache.shape[-1] != packed_width(head_dim):
+        raise ValueError(f"cache has {k_cache.shape[-1]} words, expected {packed_width(head_dim)}")
+    T, H = k_cache.shape[0], k_cache.shape[1]
+    table = _as_int32(block_table)
+    if table.ndim != 1:
+        raise ValueError("block_table must be one sequence's 1-D row")
+    target = torch.uint8 if dtype == torch.bool else dtype
+    k_out = torch.empty((T, H, seq_len, head_dim), dtype=target, device=dev)
+    v_out = torch.empty_like(k_out) if v_cache is not None else None
+    _lib.check(
+        _lib.load().spk_gather_unpack(
+            k_cache.data_ptr(), _lib.ptr(v_cache), _lib.strides(k_cache), k_cache.shape[2],
+            table.data_ptr(), table.stride(0), table.numel(), seq_len, k_out.data_ptr(),
+            _lib.ptr(v_out), _lib.dtype_code(target), T, H, head_dim, block_size,
+            _lib.stream_of(dev),
+        ),
+        "gather_kv_unpacked",
+    )
+    if dtype == torch.bool:
+        k_out = k_out.view(torch.bool)
+        v_out = v_out.view(torch.bool) if v_out is not None else None
+    return k_out, v_out
+
+
 def gather_kv_unpacked(
     cache: torch.Tensor,
     block_table: torch.Tensor,
@@ -160,12 +189,103 @@ def gather_kv_unpacked(
     block_size: int,
     dtype: torch.dtype,
 ) -> torch.Tensor:
-    """One sequence's cached spikes as dense ``[T, H_kv, S, D]`` (prefill
-    reader, spike_attention.py:224-244): slot gather, then the HIP unpack."""
-    n_blocks = (seq_len + block_size - 1) // block_size
-    slots = (
-        block_table[:n_blocks, None].to(torch.int64) * block_size
-        + torch.arange(block_size, device=cache.device)[None, :]
-    ).reshape(-1)[:seq_len]
-    words = cache.index_select(2, slots)
-    return unpack_spikes(words, head_dim, dtype)
+    """One sequence's first ``seq_len`` cached tokens as dense ``[T, H_kv, S, D]``
+    0/1 spikes (the prefill reader, spike_attention.py:224-244), in one HIP
+    launch: block-table walk and unpack together, no packed temporary."""
+    return _gather(cache, None, block_table, seq_len, head_dim, block_size, dtype)[0]
+
+
+def gather_kv_unpacked_pair(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_len: int,
+    head_dim: int,
+    block_size: int,
+    dtype: torch.dtype,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``gather_kv_unpacked`` of the K and the V cache in one launch."""
+    return _gather(k_cache, v_cache, block_table, seq_len, head_dim, block_size, dtype)
+
+
+def paged_spike_attn_decode_partials(
+    q_packed: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    head_dim: int,
+    block_size: int,
+    num_q_heads: int,
+    num_kv_heads: int,
+    part_len: int,
+    partials: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Unnormalised per-partition sums of the decode attention:
+    ``float32 [P, T, N, H_q, head_dim + 1]`` with ``P = ceil(max_blocks *
+    block_size / part_len)``; entry ``[p, t, n, h, :head_dim]`` is
+    ``sum_j w_j v_j`` and ``[..., head_dim]`` is ``sum_j w_j`` over the
+    tokens ``j`` of partition ``p`` (``w_j = exp(-popcount(q & ~k_j) /
+    sqrt(head_dim))``, the fixed softmax offset, so partials of any split add).
+    Partitions at or past a sequence's length are left unwritten.  Finish with
+    :func:`combine_partitions`."""
+    T, n_seqs, n_heads, words = q_packed.shape
+    if words != packed_width(head_dim) or n_heads != num_q_heads:
+        raise ValueError("q_packed does not match head_dim / num_q_heads")
+    dev = _lib.require_gpu(q_packed, k_cache, v_cache, block_tables, seq_lens, partials)
+    for name, t in (("q_packed", q_packed), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _check_packed(name, t)
+    block_tables = _as_int32(block_tables)
+    seq_lens = _as_int32(seq_lens).contiguous()
+    max_blocks = block_tables.shape[1]
+    P = -(-max_blocks * block_size // part_len)
+    shape = (P, T, n_seqs, num_q_heads, head_dim + 1)
+    if partials is None:
+        partials = torch.empty(shape, dtype=torch.float32, device=dev)
+    elif tuple(partials.shape) != shape or partials.dtype != torch.float32 or not partials.is_contiguous():
+        raise ValueError(f"partials must be contiguous float32 {shape}")
+    if n_seqs == 0:
+        return partials
+    _lib.check(
+        _lib.load().spk_decode_attn_partials(
+            q_packed.data_ptr(), _lib.strides(q_packed), k_cache.data_ptr(), _lib.strides(k_cache),
+            v_cache.data_ptr(), _lib.strides(v_cache), k_cache.shape[2], block_tables.data_ptr(),
+            block_tables.stride(0), block_tables.stride(1), seq_lens.data_ptr(), T, n_seqs,
+            num_q_heads, num_kv_heads, head_dim, block_size, max_blocks,
+            1.0 / math.sqrt(head_dim), part_len, partials.data_ptr(),
+            partials.numel() * 4, _lib.stream_of(dev),
+        ),
+        "paged_spike_attn_decode_partials",
+    )
+    return partials
+
+
+def combine_partitions(
+    partials: torch.Tensor,
+    seq_lens: torch.Tensor,
+    part_len: int,
+    out: torch.Tensor | None = None,
+    dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """``[P, T, N, H_q, D + 1]`` partials -> ``[T, N, H_q, D]`` attention
+    output: for each row, the sums over partitions ``p < ceil(seq_len /
+    part_len)`` in partition order, ``out = sum a / sum l`` (zeros for
+    ``seq_len <= 0``)."""
+    if partials.ndim != 5 or partials.dtype != torch.float32 or not partials.is_contiguous():
+        raise ValueError("partials must be contiguous float32 [P, T, N, H_q, D + 1]")
+    P, T, n_seqs, n_heads, d1 = partials.shape
+    dev = _lib.require_gpu(partials, seq_lens, out)
+    seq_lens = _as_int32(seq_lens).contiguous()
+    if out is None:
+        out = torch.empty((T, n_seqs, n_heads, d1 - 1), dtype=dtype, device=dev)
+    elif tuple(out.shape) != (T, n_seqs, n_heads, d1 - 1):
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected {(T, n_seqs, n_heads, d1 - 1)}")
+    _lib.check(
+        _lib.load().spk_decode_attn_combine(
+            partials.data_ptr(), P, part_len, seq_lens.data_ptr(), out.data_ptr(),
+            _lib.dtype_code(out.dtype), _lib.strides(out), T, n_seqs, n_heads, d1 - 1,
+            _lib.stream_of(dev),
+        ),
+        "combine_partitions",
+    )
+    return out

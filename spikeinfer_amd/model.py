@@ -31,7 +31,7 @@ from .kernels.decoder_ops import (add_rmsnorm, embed_rmsnorm, lif_gate_mul, line
                                   mlp_gate_lif, pack_gate_up, pack_linear, qkv_decode_attention,
                                   qkv_rope_lif_pack, rmsnorm_mean_t)
 from .kernels.packing import packed_width
-from .kernels.spike_attention import gather_kv_unpacked, paged_spike_attn_decode
+from .kernels.spike_attention import gather_kv_unpacked_pair, paged_spike_attn_decode
 
 
 @dataclass
@@ -284,8 +284,8 @@ class SpikingDecoder:
             if ctx == 0:
                 k_all, v_all = dk[:, :, start:start + q_len], dv[:, :, start:start + q_len]
             else:
-                k_all = gather_kv_unpacked(k_cache, table, total, D, meta.block_size, self.dtype)
-                v_all = gather_kv_unpacked(v_cache, table, total, D, meta.block_size, self.dtype)
+                k_all, v_all = gather_kv_unpacked_pair(k_cache, v_cache, table, total, D,
+                                                       meta.block_size, self.dtype)
             mask = torch.full((q_len, total), float("-inf"), device=attn.device, dtype=self.dtype)
             mask = torch.triu(mask, diagonal=ctx + 1)
             o = F.scaled_dot_product_attention(dq[:, :, start:start + q_len], k_all, v_all,

@@ -206,7 +206,15 @@ class DecodeRunner:
     @torch.no_grad()
     def generate(self, prompts: list[list[int]], params: list[SamplingParams],
                  max_new_tokens: int, shuffle_blocks: int | None = None) -> torch.Tensor:
-        """``[n, max_new_tokens]`` generated token ids (first from prefill)."""
+        """``[n, max_new_tokens]`` generated token ids (first from prefill).
+
+        Raises ValueError when ``max_new_tokens`` exceeds the history the
+        runner was built with (its ``max_new_tokens`` argument).
+        """
+        if max_new_tokens > self.history.shape[1]:
+            raise ValueError(
+                f"max_new_tokens={max_new_tokens} exceeds the runner's history of "
+                f"{self.history.shape[1]} tokens (construct it with a larger max_new_tokens)")
         self.start(prompts, params, shuffle_blocks)
         if self.graph is None:
             self.capture((self.bucket_for(len(prompts)),))

@@ -44,12 +44,13 @@ def test_slot_matrix_known_answer():
     assert slot_mapping(tables[0], 9, 1, 4) == [29]
 
 
-def test_metadata_on_same_device_is_identity_and_memoises():
+def test_metadata_counts_prefill_chunks():
     meta = AttentionMetadata(slot_mapping=torch.arange(3), block_size=16, num_decode_tokens=3,
                              block_tables=torch.zeros(3, 2, dtype=torch.int32),
                              seq_lens=torch.ones(3, dtype=torch.int32))
-    assert meta.on(torch.device("cpu")) is meta
     assert meta.num_prefills == 0
+    meta.prefill_query_lens.append(5)
+    assert meta.num_prefills == 1
 
 
 def test_paged_attention_refuses_cpu_tensors():
