@@ -8,11 +8,14 @@ plus q, output, block-table entries and lengths).  A "step" is one call of
 paged_spike_attn_decode over the whole batch (decode kernel + partition
 combine), inputs resident in HBM.
 
-Also reported: the density sweep {0.05, 0.2, 0.5} (runtime must be flat),
-config 3 (batch 64, ctx U[128,192], 24 layers -> attention time per decode
-step), config 2 (fused LIF + pack + cache write, 4096 tokens), config 5 (decode
-tok/s of the whole spiking decoder step at batch 64, replayed from one
-hipGraph), and the CPU oracle timed on a bounded sample of config 4 on the host
+Also reported: the density sweep {0.05, 0.2, 0.5} (runtime must be flat;
+interleaved rounds, medians), the same call replayed from a hipGraph (kernel
+time without host launch work), config 3 (batch 64, ctx U[128,192], 24 layers
+-> attention time per decode step), config 2 (fused LIF + pack + cache write,
+4096 tokens), config 5 (decode tok/s of the whole spiking decoder step at
+batch 64 over the 63 decode steps of 64 output tokens, replayed from one
+hipGraph), and the CPU paths (the reference's torch CPU strategy restated,
+and the C oracle) timed on bounded samples of configs 4, 1 and 3 on the host
 cores.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip-extras]
@@ -124,8 +127,10 @@ def bench_attention(inp, steps, warmup, dev, out_dtype=torch.float32, graph=Fals
                                     out=out, workspace=ws)
 
     if graph:
-        # One decode step's attention calls captured in a hipGraph (as the
-        # serving runner replays them): launch cost without Python in between.
+        # `graph` decode steps' attention calls captured in one hipGraph (as
+        # the serving runner replays them): launch cost without Python in
+        # between.  The time is per step.
+        reps = int(graph)
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
@@ -135,42 +140,144 @@ def bench_attention(inp, steps, warmup, dev, out_dtype=torch.float32, graph=Fals
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            step()
-        ms = time_calls(g.replay, steps, warmup, torch.cuda.current_stream(dev))
+            for _ in range(reps):
+                step()
+        ms = time_calls(g.replay, steps, warmup, torch.cuda.current_stream(dev)) / reps
     else:
         ms = time_calls(step, steps, warmup, torch.cuda.current_stream(dev))
     return ms, out
 
 
-def cpu_baseline(inp, dev, budget_s=15.0):
-    """C oracle (OpenMP) on a bounded sample of the same config-4 batch."""
+def cpu_info():
+    """What the CPU legs ran on: nproc, the lscpu model name, torch threads."""
+    model = None
+    try:
+        import subprocess
+
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except Exception:  # noqa: BLE001 - lscpu is informational only
+        pass
+    return {"nproc": os.cpu_count(), "lscpu_model": model,
+            "torch_threads": torch.get_num_threads()}
+
+
+def _median_ms(fn, iters, warm=2):
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def cpu_baseline(inp, dev, budget_s=15.0, threads=16):
+    """The CPU paths on the host cores, on bounded samples of configs 4, 1
+    and 3 (`cores` = threads used, at most the box's CPU share of 16):
+
+    * torch leg -- spikeinfer_amd.kernels.paged_spike_attn_decode_cpu, the
+      reference's CPU strategy restated (spike_attention_cpu.py:103-222:
+      grouped slot-matrix gather, unpack, SDPA with enable_gqa); the
+      `value`, since it is the faster CPU strategy and the one the
+      reference's own CPU numbers are for;
+    * C leg -- the float64 popcount oracle (oracle/spike_oracle.c, OpenMP).
+    """
     import numpy as np
 
     from oracle import oracle as orc
+    from spikeinfer_amd.kernels import paged_spike_attn_decode_cpu
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = min(threads, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
     orc.threads(threads)
     k, v = inp["caches"][0]
-    kc, vc = k.cpu().numpy(), v.cpu().numpy()
-    q = inp["q"].cpu().numpy()
-    tables = inp["tables"].cpu().numpy()
-    lens = inp["lens_cpu"].numpy()
-    done_bytes, elapsed, n_done = 0, 0.0, 0
-    while n_done < len(lens) and elapsed < budget_s:
-        sl = slice(n_done, n_done + 4)
-        t0 = time.perf_counter()
-        orc.decode_attn(q[:, sl], kc, vc, tables[sl], lens[sl], D, BS, HQ, HKV)
-        elapsed += time.perf_counter() - t0
-        done_bytes += attn_bytes(torch.from_numpy(lens[sl]), 4)
-        n_done += lens[sl].size
+    kt, vt = k.cpu(), v.cpu()
+    kc, vc = kt.numpy(), vt.numpy()
+    qt = inp["q"].cpu()
+    q = qt.numpy()
+    tables_t = inp["tables"].cpu()
+    tables = tables_t.numpy()
+    lens_t = inp["lens_cpu"]
+    lens = lens_t.numpy()
+
+    def sample(run, share):
+        done_bytes, elapsed, n_done = 0, 0.0, 0
+        while n_done < len(lens) and elapsed < budget_s * share:
+            sl = slice(n_done, n_done + 4)
+            t0 = time.perf_counter()
+            run(sl)
+            elapsed += time.perf_counter() - t0
+            done_bytes += attn_bytes(torch.from_numpy(lens[sl]), 4)
+            n_done += lens[sl].size
+        return done_bytes / elapsed / 1e9, n_done, elapsed
+
+    torch_gbs, torch_n, torch_s = sample(
+        lambda sl: paged_spike_attn_decode_cpu(qt[:, sl], kt, vt, tables_t[sl], lens_t[sl], D, BS,
+                                               HQ, HKV), 0.5)
+    c_gbs, c_n, c_s = sample(
+        lambda sl: orc.decode_attn(q[:, sl], kc, vc, tables[sl], lens[sl], D, BS, HQ, HKV), 0.5)
+
+    # configs 1 and 3 (whole inputs: they are small)
+    small = {}
+    for name, n, lo, hi, layers in (("config1", 1, 128, 128, 1), ("config3", 64, 128, 192, 24)):
+        c = make_attn_inputs(n, lo, hi, 0.2, 1000 if n == 1 else 3000, dev, layers=1)
+        ck, cv = (x.cpu() for x in c["caches"][0])
+        cq, ctab, clen = c["q"].cpu(), c["tables"].cpu(), c["lens_cpu"]
+        ms_t = _median_ms(lambda: paged_spike_attn_decode_cpu(cq, ck, cv, ctab, clen, D, BS, HQ, HKV), 20)
+        ms_c = _median_ms(lambda: orc.decode_attn(cq.numpy(), ck.numpy(), cv.numpy(), ctab.numpy(),
+                                                  clen.numpy(), D, BS, HQ, HKV), 20)
+        small[name] = {"torch_us_per_layer": round(ms_t * 1e3, 1),
+                       "c_oracle_us_per_layer": round(ms_c * 1e3, 1),
+                       "layers": layers,
+                       "torch_ms_per_step": round(ms_t * layers, 3),
+                       "c_oracle_ms_per_step": round(ms_c * layers, 3)}
     return {
-        "value": round(done_bytes / elapsed / 1e9, 3),
+        "value": round(torch_gbs, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"first {n_done} of {len(lens)} config-4 sequences (ctx U[4096,32768], "
-                  f"p=0.2), C oracle float64 softmax, {elapsed:.1f} s",
+        "sample": f"config 4 (ctx U[4096,32768], p=0.2): first {torch_n} of {len(lens)} sequences "
+                  f"in {torch_s:.1f} s through the torch restatement of the reference CPU strategy "
+                  f"(grouped gather + unpack + SDPA, fp32)",
+        "legs": {
+            "torch_reference_strategy": {"gbs": round(torch_gbs, 3), "sequences": torch_n,
+                                         "seconds": round(torch_s, 2)},
+            "c_oracle_popcount_f64": {"gbs": round(c_gbs, 3), "sequences": c_n,
+                                      "seconds": round(c_s, 2)},
+        },
+        "configs_1_3": small,
+        "host": cpu_info(),
     }
+
+
+def density_sweep(inp, nbytes, args, dev, repeats=3):
+    """Config 4 at densities 0.05 / 0.2 / 0.5 (same lengths and tables),
+    interleaved: `repeats` rounds, each timing every density for `steps`
+    calls, in a rotated order, so clock warm-up and drift fall on all three
+    alike.  Reports each density's median and its runs."""
+    print("config 4 density sweep", file=sys.stderr, flush=True)
+    sets = {0.2: inp}
+    for p in (0.05, 0.5):
+        sets[p] = make_attn_inputs(256, 4096, 32768, p, 4000, dev)
+    order = [0.05, 0.2, 0.5]
+    runs = {p: [] for p in order}
+    for r in range(repeats):
+        for p in order[r % 3:] + order[:r % 3]:
+            ms_p, _ = bench_attention(sets[p], args.steps, args.warmup, dev)
+            runs[p].append(round(ms_p * 1000, 2))
+    out = {}
+    for p in order:
+        us = sorted(runs[p])[len(runs[p]) // 2]
+        out[str(p)] = {"median_us": us, "gbs": round(nbytes / us / 1e3, 1), "runs_us": runs[p]}
+    med = [out[str(p)]["median_us"] for p in order]
+    out["max_over_min"] = round(max(med) / min(med), 4)
+    del sets
+    return out
 
 
 def bench_lif(steps, warmup, dev):
@@ -246,12 +353,13 @@ def bench_pack(steps, warmup, dev):
             "unpack_gbs": round(nbytes / ms_u / 1e6, 1)}
 
 
-def bench_decode_step(steps, warmup, dev, batch=64):
+def bench_decode_step(steps, warmup, dev, batch=64, out_tokens=64):
     """Config 5: random-init Qwen2.5-0.5B-shaped spiking decoder (bf16 weights
     N(0, 0.02)), batch 64, 128-token random prompts, T=4; one decode step
     (24 layers + lm_head + sampling with temperature 0.8 / top-k 50 / top-p 0.9
     / repetition 1.1 + device-side advance) replayed from one hipGraph.  Prefill
-    is eager and untimed.  tok/s = batch tokens per step / step time."""
+    is eager and untimed; the timed window is the out_tokens - 1 decode steps
+    that follow it.  tok/s = batch tokens per step / step time."""
     from spikeinfer_amd.model import SpikingDecoder, SpikingQwenConfig
     from spikeinfer_amd.runner import DecodeRunner
     from spikeinfer_amd.sampler import SamplingParams
@@ -259,7 +367,7 @@ def bench_decode_step(steps, warmup, dev, batch=64):
 
     cfg = SpikingQwenConfig()
     B, plen = batch, 128
-    new = warmup + steps + 1
+    new = max(out_tokens, warmup + 1)
     model = SpikingDecoder(cfg, device=dev, seed=5000)
     max_len = plen + new + 1
     blocks = B * math.ceil(max_len / BS) + 1
@@ -275,10 +383,17 @@ def bench_decode_step(steps, warmup, dev, batch=64):
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
     runner.capture((B,))
+    runner.replay(warmup)
+    # The timed run: a fresh prefill (untimed, it samples output token 1),
+    # then exactly out_tokens - 1 replays of the captured step for tokens
+    # 2 .. out_tokens.
+    runner.start(prompts, params, shuffle_blocks=5002)
+    torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    ms = time_calls(lambda: runner.replay(1), steps, warmup, stream)
-    toks = runner.history[:B, :steps + warmup + 1]
+    ms = time_calls(lambda: runner.replay(1), out_tokens - 1, 0, stream)
+    toks = runner.history[:B, :out_tokens]
     return {
+        "output_tokens": out_tokens,
         "decode_tok_s": round(B / ms * 1000, 1),
         "ms_per_step": round(ms, 4),
         "weight_gbs": round(model.weight_bytes / ms / 1e6, 1),
@@ -313,10 +428,10 @@ def main():
         if args.only == "config2":
             res = bench_lif(args.steps, args.warmup, dev)
         elif args.only == "config5":
-            res = bench_decode_step(args.steps, args.warmup, dev)
+            res = bench_decode_step(args.steps, args.warmup, dev, out_tokens=64)
         else:
             c3 = make_attn_inputs(64, 128, 192, 0.2, 3000, dev, layers=24)
-            ms3, _ = bench_attention(c3, args.steps, args.warmup, dev, torch.bfloat16, graph=True)
+            ms3, _ = bench_attention(c3, args.steps, args.warmup, dev, torch.bfloat16, graph=1)
             res = {"config3_attn_us_per_step_24_layers": round(ms3 * 1000, 1)}
         print(json.dumps({"workload": args.only, **res}), flush=True)
         return
@@ -328,12 +443,14 @@ def main():
     gbs = nbytes / ms / 1e6
     extras = {}
     if not args.skip_extras:
-        for p in (0.05, 0.5):
-            print(f"config 4 density {p}", file=sys.stderr, flush=True)
-            alt = make_attn_inputs(256, 4096, 32768, p, 4000, dev)
-            ms_p, _ = bench_attention(alt, args.steps, args.warmup, dev)
-            extras[f"density_{p}_gbs"] = round(nbytes / ms_p / 1e6, 1)
-            del alt
+        extras["config4_density_sweep"] = density_sweep(inp, nbytes, args, dev)
+        print("config 4 in a hipGraph", file=sys.stderr, flush=True)
+        ms_g, _ = bench_attention(inp, args.steps, args.warmup, dev, graph=10)
+        extras["config4_graph"] = {
+            "us_per_call": round(ms_g * 1000, 2), "gbs": round(nbytes / ms_g / 1e6, 1),
+            "frac_of_hbm_peak": round(nbytes / ms_g / 1e6 / HBM_PEAK_GBS, 4),
+            "note": "10 calls per graph replay: kernel time plus the inter-kernel gap, "
+                    "without host launch work"}
         print("batch 256 x fixed 8k context", file=sys.stderr, flush=True)
         alt = make_attn_inputs(256, 8192, 8192, 0.2, 4000, dev)
         ms_8k, _ = bench_attention(alt, args.steps, args.warmup, dev)
@@ -350,7 +467,7 @@ def main():
         del alt
         print("config 3", file=sys.stderr, flush=True)
         c3 = make_attn_inputs(64, 128, 192, 0.2, 3000, dev, layers=24)
-        ms3, _ = bench_attention(c3, args.steps, args.warmup, dev, torch.bfloat16, graph=True)
+        ms3, _ = bench_attention(c3, args.steps, args.warmup, dev, torch.bfloat16, graph=1)
         extras["config3_attn_us_per_step_24_layers"] = round(ms3 * 1000, 1)
         extras["config3_attn_gbs"] = round(attn_bytes(c3["lens_cpu"], 2) * 24 / ms3 / 1e6, 1)
         del c3
@@ -359,8 +476,8 @@ def main():
         print("config 2", file=sys.stderr, flush=True)
         extras["config2_lif"] = bench_lif(args.steps, args.warmup, dev)
         print("config 5", file=sys.stderr, flush=True)
-        extras["config5_decode"] = bench_decode_step(args.steps, args.warmup, dev)
-        small = bench_decode_step(args.steps, args.warmup, dev, batch=8)
+        extras["config5_decode"] = bench_decode_step(args.steps, args.warmup, dev, out_tokens=64)
+        small = bench_decode_step(args.steps, args.warmup, dev, batch=8, out_tokens=64)
         extras["config5_decode_batch8"] = {k: small[k] for k in ("decode_tok_s", "ms_per_step")}
     if args.calib_copy_mib:
         src = torch.empty(args.calib_copy_mib << 18, dtype=torch.float32, device=dev).fill_(1.0)

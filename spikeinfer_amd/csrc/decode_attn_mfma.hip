@@ -224,7 +224,7 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh) {
   int *count = sh, *wsum = sh + kMaxBuckets, *res = wsum + KW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int M = p.N * p.num_parts;
-  const int nb = (p.part_len >> 8) + 2;
+  const int nb = ((p.part_len + 255) >> 8) + 2;  // bucket of a full partition + 1
   // Bucket of item i, -1 when the sequence has no such partition.
   auto key = [&](int i) {
     const int n = i % p.N, part = i / p.N;
@@ -740,7 +740,7 @@ __global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, in
   __shared__ int count[kMaxBuckets];
   __shared__ int offset[kMaxBuckets];
   const int tid = threadIdx.x;
-  const int nb = (part_len >> 8) + 2;
+  const int nb = ((part_len + 255) >> 8) + 2;
   for (int b = tid; b < nb; b += blockDim.x) count[b] = 0;
   __syncthreads();
   auto bucket = [&](int len, int part) {

@@ -235,6 +235,8 @@ def paged_spike_attn_decode_partials(
     dev = _lib.require_gpu(q_packed, k_cache, v_cache, block_tables, seq_lens, partials)
     for name, t in (("q_packed", q_packed), ("k_cache", k_cache), ("v_cache", v_cache)):
         _check_packed(name, t)
+    if part_len <= 0 or part_len % block_size:
+        raise ValueError(f"part_len={part_len} must be a positive multiple of block_size={block_size}")
     block_tables = _as_int32(block_tables)
     seq_lens = _as_int32(seq_lens).contiguous()
     max_blocks = block_tables.shape[1]
