@@ -89,6 +89,29 @@ int spk_decode_attn(const int32_t *q, const int64_t q_strides[4],
                     int max_blocks, float scale, void *workspace,
                     size_t workspace_bytes, void *stream);
 
+/*
+ * spk_decode_attn without a workspace argument, for callers that cannot
+ * allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  Same
+ * arguments and results as spk_decode_attn; the partial sums and launch-order
+ * list it may need live in a fixed device array of the library,
+ * SPK_DECODE_ATTN_SCRATCH_BYTES per GPU (held until the process ends).
+ * Shapes whose spk_decode_attn_workspace_bytes exceeds that are rejected with
+ * SPK_EINVAL.  Calls allocate nothing; every call on one GPU shares that
+ * GPU's array, so calls that overlap in time on one GPU (e.g. on two streams)
+ * race and must be ordered by the caller.
+ */
+#define SPK_DECODE_ATTN_SCRATCH_BYTES (16u << 20)
+int spk_decode_attn_noalloc(const int32_t *q, const int64_t q_strides[4],
+                            const int32_t *k_cache, const int64_t k_strides[4],
+                            const int32_t *v_cache, const int64_t v_strides[4],
+                            int64_t num_slots, const int32_t *block_tables,
+                            int64_t bt_stride0, int64_t bt_stride1,
+                            const int32_t *seq_lens, void *out, int out_dtype,
+                            const int64_t out_strides[4], int T, int N, int Hq,
+                            int Hkv, int head_dim, int block_size, int max_blocks,
+                            float scale, void *stream);
+
 /* Bytes of workspace spk_decode_attn needs for this launch shape. */
 size_t spk_decode_attn_workspace_bytes(int T, int N, int Hq, int Hkv,
                                        int head_dim, int block_size,

@@ -29,6 +29,7 @@ _DTYPE_CODES = {
 }
 
 ABI_VERSION = 1
+DECODE_ATTN_SCRATCH_BYTES = 16 << 20  # SPK_DECODE_ATTN_SCRATCH_BYTES
 
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _vp = ctypes.c_void_p
@@ -41,6 +42,9 @@ _SIGNATURES = {
     "spk_decode_attn": (_i32, [
         _vp, _i64p, _vp, _i64p, _vp, _i64p, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _i64p,
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
+    "spk_decode_attn_noalloc": (_i32, [
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _i64p,
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp]),
     "spk_decode_attn_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "spk_decode_attn_partials": (_i32, [
         _vp, _i64p, _vp, _i64p, _vp, _i64p, _i64, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32,

@@ -24,6 +24,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 namespace spk {
 
@@ -380,6 +381,64 @@ extern "C" int spk_decode_attn(const int32_t *q, const int64_t q_strides[4], con
                           block_tables, bt_stride0, bt_stride1, seq_lens, out, out_dtype,
                           out_strides, T, N, Hq, Hkv, head_dim, block_size, max_blocks, scale,
                           workspace, workspace_bytes, stream, nullptr, 0);
+}
+
+// ---- the allocation-free variant of spk_decode_attn ---------------------
+// The partial sums and the launch-order list live in this file-scope device
+// array instead of a caller workspace.  Each GPU the library runs on holds its
+// own copy (kNoAllocScratchBytes, until the process ends).  Host code never
+// passes `scratch` itself to a kernel: its name in host code is a stand-in,
+// not a device address; the device address comes from hipGetSymbolAddress,
+// looked up once per device with that device current.
+constexpr size_t kNoAllocScratchBytes = SPK_DECODE_ATTN_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static int scratch_on_current_device(void **out) {
+  constexpr int kMaxDevices = 64;
+  static void *ptrs[kMaxDevices] = {};
+  static std::mutex mu;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(SPK_EHIP, "decode_attn_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(SPK_EUNSUPPORTED, "decode_attn_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(SPK_EHIP, "decode_attn_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    ptrs[dev] = ptr;
+  }
+  *out = ptrs[dev];
+  return SPK_OK;
+}
+
+extern "C" int spk_decode_attn_noalloc(const int32_t *q, const int64_t q_strides[4],
+                                       const int32_t *k_cache, const int64_t k_strides[4],
+                                       const int32_t *v_cache, const int64_t v_strides[4],
+                                       int64_t num_slots, const int32_t *block_tables,
+                                       int64_t bt_stride0, int64_t bt_stride1,
+                                       const int32_t *seq_lens, void *out, int out_dtype,
+                                       const int64_t out_strides[4], int T, int N, int Hq,
+                                       int Hkv, int head_dim, int block_size, int max_blocks,
+                                       float scale, void *stream) {
+  const size_t need = spk_decode_attn_workspace_bytes(T, N, Hq, Hkv, head_dim, block_size, max_blocks);
+  if (need > kNoAllocScratchBytes)
+    return fail(SPK_EINVAL,
+                "decode_attn_noalloc: this shape needs %zu bytes of scratch, more than the "
+                "library's fixed %zu (use spk_decode_attn with a workspace)",
+                need, kNoAllocScratchBytes);
+  void *ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_on_current_device(&ws);
+    if (rc) return rc;
+  }
+  // Nothing in the scratch needs clearing: every partial the combine reads
+  // and every entry of the launch order is written by this call first.
+  return decode_attn_impl(q, q_strides, k_cache, k_strides, v_cache, v_strides, num_slots,
+                          block_tables, bt_stride0, bt_stride1, seq_lens, out, out_dtype,
+                          out_strides, T, N, Hq, Hkv, head_dim, block_size, max_blocks, scale,
+                          ws, need, stream, nullptr, 0);
 }
 
 extern "C" int spk_decode_attn_partials(const int32_t *q, const int64_t q_strides[4],
