@@ -148,6 +148,44 @@ def bench_attention(inp, steps, warmup, dev, out_dtype=torch.float32, graph=Fals
     return ms, out
 
 
+def _attn_call(inp, dev):
+    from spikeinfer_amd.kernels import decode_attn_workspace_bytes, paged_spike_attn_decode
+
+    n, hd = inp["lens"].numel(), inp["head_dim"]
+    out = torch.empty((T, n, HQ, hd), device=dev)
+    ws = torch.empty(decode_attn_workspace_bytes(T, n, HQ, HKV, hd, BS, inp["max_blocks"]) or 1,
+                     dtype=torch.uint8, device=dev)
+    k, v = inp["caches"][0]
+    return lambda: paged_spike_attn_decode(inp["q"], k, v, inp["tables"], inp["lens"], hd, BS, HQ,
+                                           HKV, out=out, workspace=ws)
+
+
+def call_series(inp, chunks, dev, chunk=10):
+    """Per-call time (us) of `chunks` consecutive chunks of `chunk` back-to-back
+    calls, started after 0.5 s idle: shows the power-management transient."""
+    call = _attn_call(inp, dev)
+    call()
+    torch.cuda.synchronize()
+    time.sleep(0.5)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(chunks + 1)]
+    ev[0].record()
+    for c in range(chunks):
+        for _ in range(chunk):
+            call()
+        ev[c + 1].record()
+    torch.cuda.synchronize()
+    return [round(ev[c].elapsed_time(ev[c + 1]) * 1000 / chunk, 1) for c in range(chunks)]
+
+
+def cold_start(inp, dev):
+    """The first 20 back-to-back calls after 0.5 s idle (the default warmup
+    is what moves the headline past this transient)."""
+    s = call_series(inp, 2, dev)
+    us = sum(s) / len(s)
+    return {"calls": 20, "us_per_call": round(us, 1),
+            "gbs": round(attn_bytes(inp["lens_cpu"], 4) / us / 1e3, 1)}
+
+
 def cpu_info():
     """What the CPU legs ran on: nproc, the lscpu model name, torch threads."""
     model = None
@@ -408,8 +446,15 @@ def bench_decode_step(steps, warmup, dev, batch=64, out_tokens=64):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # Defaults reach the steady state: from idle, the first ~5-30 ms of
+    # back-to-back calls run up to 30 % slower while the GPU's power
+    # management settles (--series shows it); 400 warmup calls are ~50 ms.
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--density", type=float, default=0.2,
+                    help="spike density of the headline config-4 inputs (profiling the sweep)")
+    ap.add_argument("--series", type=int, default=0,
+                    help="print the config-4 per-call time of N chunks of 10 calls from idle, then exit")
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -437,11 +482,17 @@ def main():
         return
 
     print("config 4: generating inputs", file=sys.stderr, flush=True)
-    inp = make_attn_inputs(256, 4096, 32768, 0.2, 4000, dev)
+    inp = make_attn_inputs(256, 4096, 32768, args.density, 4000, dev)
+    if args.series:
+        print(json.dumps({"workload": "config4 from idle", "chunk_calls": 10,
+                          "us_per_call": call_series(inp, args.series, dev)}), flush=True)
+        return
+    cold = cold_start(inp, dev)
     ms, _ = bench_attention(inp, args.steps, args.warmup, dev)
     nbytes = attn_bytes(inp["lens_cpu"], 4)
     gbs = nbytes / ms / 1e6
     extras = {}
+    extras["config4_cold_start"] = cold
     if not args.skip_extras:
         extras["config4_density_sweep"] = density_sweep(inp, nbytes, args, dev)
         print("config 4 in a hipGraph", file=sys.stderr, flush=True)
@@ -476,8 +527,8 @@ def main():
         print("config 2", file=sys.stderr, flush=True)
         extras["config2_lif"] = bench_lif(args.steps, args.warmup, dev)
         print("config 5", file=sys.stderr, flush=True)
-        extras["config5_decode"] = bench_decode_step(args.steps, args.warmup, dev, out_tokens=64)
-        small = bench_decode_step(args.steps, args.warmup, dev, batch=8, out_tokens=64)
+        extras["config5_decode"] = bench_decode_step(args.steps, min(args.warmup, 20), dev, out_tokens=64)
+        small = bench_decode_step(args.steps, min(args.warmup, 20), dev, batch=8, out_tokens=64)
         extras["config5_decode_batch8"] = {k: small[k] for k in ("decode_tok_s", "ms_per_step")}
     if args.calib_copy_mib:
         src = torch.empty(args.calib_copy_mib << 18, dtype=torch.float32, device=dev).fill_(1.0)
@@ -506,7 +557,7 @@ def main():
         "data": "synthetic: Bernoulli(0.2) spike bits, shuffled block tables, seeded",
         "config": {"workload": "config4_paged_popcount_decode_attn", "batch": 256,
                    "ctx": "U[4096,32768]", "Hq": HQ, "Hkv": HKV, "head_dim": D, "T": T,
-                   "block_size": BS, "density": 0.2, "out_dtype": "f32",
+                   "block_size": BS, "density": args.density, "out_dtype": "f32",
                    "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),

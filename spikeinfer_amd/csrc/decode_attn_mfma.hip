@@ -165,14 +165,23 @@ __device__ __forceinline__ void wave_sync() {
 //   the all-ones B tile accumulates the softmax denominators.
 // With W64 = 2 the channel tiles of v word hv are acc[rt][4*hv + s]
 // (channel 64*hv + 4*(l%16) + s); the A operand is shared.
+// The contraction is split in read_ops (LDS -> registers) and mma_ops so
+// that a step's MFMAs can run while the next step is staged.
+
+// Operands of one staged step, held in registers so that the stage can take
+// the next step's rows while these MFMAs run.
+template <int W64>
+struct StepOps {
+  v8i A[2];          // digit rows of row tiles 0 and 1
+  uint32_t w[W64][4];  // transposed v words (nibble i = channels 4i..4i+3)
+};
+
 template <int RT, int W64>  // row tiles: heads 4rt..4rt+3 for rt < RT
-__device__ __forceinline__ void contract_step(const WaveStage<W64> &st, int lane,
-                                              v4f (&acc)[2][4 * W64], v4f (&accl)[2]) {
+__device__ __forceinline__ void read_ops(const WaveStage<W64> &st, int lane, StepOps<W64> &o) {
   const int q = lane >> 4;
   const int i16 = lane & 15;
   const int r0 = ((q & 1) ? 64 : 0) + 16 * (q >> 1);  // rows of A bytes 0..15; +32 for 16..31
   const int sub = (i16 >> 1) & 7, hb = (i16 & 1) * 8;
-  v8i A[2];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const SPK_LDS char *lds_a = (const SPK_LDS char *)&st.a[rt][0];
@@ -180,33 +189,43 @@ __device__ __forceinline__ void contract_step(const WaveStage<W64> &st, int lane
     for (int c = 0; c < 4; ++c) {
       const int row = r0 + 32 * (c >> 1) + 8 * (c & 1) + sub;
       const v2i r = tr_b8(lds_a + row * 16 + hb);
-      A[rt][2 * c] = r.x;
-      A[rt][2 * c + 1] = r.y;
+      o.A[rt][2 * c] = r.x;
+      o.A[rt][2 * c + 1] = r.y;
     }
   }
-  constexpr uint32_t kMask[4] = {0x11111111u, 0x22222222u, 0x44444444u, 0x44444444u};
 #pragma unroll
   for (int hv = 0; hv < W64; ++hv) {
     const SPK_LDS char *lds_v = (const SPK_LDS char *)st.v[hv];
     const v2i w0 = tr_b4(lds_v + (16 * q + i16) * 8);
     const v2i w1 = tr_b4(lds_v + (64 + 16 * q + i16) * 8);
-    const uint32_t w[4] = {static_cast<uint32_t>(w0.x), static_cast<uint32_t>(w0.y),
-                           static_cast<uint32_t>(w1.x), static_cast<uint32_t>(w1.y)};
+    o.w[hv][0] = static_cast<uint32_t>(w0.x);
+    o.w[hv][1] = static_cast<uint32_t>(w0.y);
+    o.w[hv][2] = static_cast<uint32_t>(w1.x);
+    o.w[hv][3] = static_cast<uint32_t>(w1.y);
+  }
+}
+
+template <int RT, int W64>
+__device__ __forceinline__ void mma_ops(const StepOps<W64> &o, v4f (&acc)[2][4 * W64], v4f (&accl)[2]) {
+  constexpr uint32_t kMask[4] = {0x11111111u, 0x22222222u, 0x44444444u, 0x44444444u};
+#pragma unroll
+  for (int hv = 0; hv < W64; ++hv) {
 #pragma unroll
     for (int ts = 0; ts < 4; ++ts) {
       v8i B = {};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) B[i] = static_cast<int>((ts == 3 ? w[i] >> 1 : w[i]) & kMask[ts]);
+      for (int i = 0; i < 4; ++i)
+        B[i] = static_cast<int>((ts == 3 ? o.w[hv][i] >> 1 : o.w[hv][i]) & kMask[ts]);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
         acc[rt][4 * hv + ts] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            A[rt], B, acc[rt][4 * hv + ts], 0, 4, 0, 127, 0, 127);
+            o.A[rt], B, acc[rt][4 * hv + ts], 0, 4, 0, 127, 0, 127);
     }
   }
   const v8i Bl = {0x11111111, 0x11111111, 0x11111111, 0x11111111, 0, 0, 0, 0};
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
-    accl[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[rt], Bl, accl[rt], 0, 4, 0, 127, 0, 127);
+    accl[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(o.A[rt], Bl, accl[rt], 0, 4, 0, 127, 0, 127);
 }
 
 // Longest-processing-time-first order of the (sequence, partition) items,
@@ -462,10 +481,13 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   // the loads stay unconditional; the staged block ids are inside the cache,
   // so every slot is.
   const int last_pair = (end - 1) & ~1;
-  auto load = [&](int j, uint64_t (&kw)[2][W64], uint64_t (&vw)[2][W64]) {
+  // Element offset (in u64 words / W64) of the pair's first slot.
+  auto slot_of = [&](int j) -> uint64_t {
     const int jj = min(j, last_pair);
     const uint32_t phys = static_cast<uint32_t>(blocks[(jj - start) >> p.bs_log2]);
-    const uint64_t slot = (static_cast<uint64_t>(phys) << p.bs_log2) | static_cast<uint64_t>(jj & bs_mask);
+    return (static_cast<uint64_t>(phys) << p.bs_log2) | static_cast<uint64_t>(jj & bs_mask);
+  };
+  auto issue = [&](uint64_t slot, uint64_t (&kw)[2][W64], uint64_t (&vw)[2][W64]) {
     typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
     const v2u64 *kp = reinterpret_cast<const v2u64 *>(kbase + slot * W64);
     const v2u64 *vp = reinterpret_cast<const v2u64 *>(vbase + slot * W64);
@@ -479,6 +501,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
       vw[(2 * i + 1) / W64][(2 * i + 1) % W64] = v2.y;
     }
   };
+  auto load = [&](int j, uint64_t (&kw)[2][W64], uint64_t (&vw)[2][W64]) { issue(slot_of(j), kw, vw); };
 
   v4f acc[2][4 * W64] = {}, accl[2] = {};
 
@@ -489,7 +512,10 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   const int ntotal = span > 0 ? (span + kStride - 1) / kStride : 0;
 
   const int cur_pair = (len - 1) & ~1, cur_e = (len - 1) & 1;
-  auto step = [&](const uint64_t (&kin)[2][W64], const uint64_t (&vin)[2][W64], bool masked, int j0) {
+  constexpr int kRT = NREP > 4 ? 2 : 1;
+  StepOps<W64> ops = {};  // zero before the first step: its MFMAs add nothing
+  auto step = [&](const uint64_t (&kin)[2][W64], const uint64_t (&vin)[2][W64], bool masked, int j0,
+                  auto &&after_stage) {
     // Nothing of this step moves ahead of the previous one: left free, the
     // scheduler hoists a later step's popcounts next to its just-issued loads
     // and the wait for them empties the prefetch ring (measured: -3.5 %).
@@ -515,14 +541,16 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
       const bool valid[2] = {j0 + 2 * lane < end, j0 + 2 * lane + 1 < end};
       stage_step<NREP, W64, true>(st, lane, kw, vw, valid, q, tab);
     }
+    after_stage();  // this step's words are consumed: the ring buffer takes new loads
+    // The previous step's MFMAs (operands already in registers) interleave
+    // with this step's popcounts and staging writes.
+    mma_ops<kRT, W64>(ops, acc, accl);
     wave_sync();
-    contract_step<(NREP > 4 ? 2 : 1), W64>(st, lane, acc, accl);
+    read_ops<kRT, W64>(st, lane, ops);
     wave_sync();
   };
 
-  // Three register buffers in a fixed ring, unrolled by three, so a load in
-  // flight is never copied (a copy would wait for it).
-  uint64_t k0[2][W64], v0[2][W64], k1[2][W64], v1[2][W64], k2[2][W64], v2[2][W64];
+  uint64_t k0[2][W64], v0[2][W64], k1[2][W64], v1[2][W64];
   const int lo = 2 * lane;
   // A wave with no tokens (short or empty partition) issues no loads: only
   // then is every pair index inside the staged block range [0, nblk).
@@ -559,46 +587,31 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
       }
     }
   }
+  // Two register buffers in a fixed ring: a step consumes its buffer, then
+  // refills it with the loads of the step after next, whose slot was read
+  // from the staged block table one step earlier (so the load address never
+  // waits behind this step's LDS traffic).
+  auto none = [] {};
   int i = 0;
-  if constexpr (W64 == 2) {  // two buffers: the wider words leave room for no third
-    for (; i + 2 <= nfull; i += 2) {
-      step(k0, v0, false, first + i * kStride);
-      load(first + (i + 2) * kStride + lo, k0, v0);
-      step(k1, v1, false, first + (i + 1) * kStride);
-      load(first + (i + 3) * kStride + lo, k1, v1);
-    }
-    if (i < nfull) step(k0, v0, false, first + i * kStride);
-    if (nfull < ntotal) {  // the partial last step: buffer nfull % 2
-      const int j0 = first + nfull * kStride;
-      if (nfull % 2 == 0) step(k0, v0, true, j0);
-      else step(k1, v1, true, j0);
-    }
-  } else {
-  for (; i + 3 <= nfull; i += 3) {
-    load(first + (i + 2) * kStride + lo, k2, v2);
-    step(k0, v0, false, first + i * kStride);
-    load(first + (i + 3) * kStride + lo, k0, v0);
-    step(k1, v1, false, first + (i + 1) * kStride);
-    load(first + (i + 4) * kStride + lo, k1, v1);
-    step(k2, v2, false, first + (i + 2) * kStride);
+  uint64_t snext = ntotal > 0 ? slot_of(first + 2 * kStride + lo) : 0;
+  for (; i + 2 <= nfull; i += 2) {
+    step(k0, v0, false, first + i * kStride, [&] {
+      issue(snext, k0, v0);
+      snext = slot_of(first + (i + 3) * kStride + lo);
+    });
+    step(k1, v1, false, first + (i + 1) * kStride, [&] {
+      issue(snext, k1, v1);
+      snext = slot_of(first + (i + 4) * kStride + lo);
+    });
   }
-  if (i < nfull) {
-    load(first + (i + 2) * kStride + lo, k2, v2);
-    step(k0, v0, false, first + i * kStride);
-    ++i;
-    if (i < nfull) {
-      step(k1, v1, false, first + i * kStride);
-      ++i;
-    }
-  }
-  if (nfull < ntotal) {  // the partial last step: buffer nfull % 3 of the ring
-    const int r = nfull % 3;
+  if (i < nfull) step(k0, v0, false, first + i * kStride, none);
+  if (nfull < ntotal) {  // the partial last step: buffer nfull % 2
     const int j0 = first + nfull * kStride;
-    if (r == 0) step(k0, v0, true, j0);
-    else if (r == 1) step(k1, v1, true, j0);
-    else step(k2, v2, true, j0);
+    if (nfull % 2 == 0) step(k0, v0, true, j0, none);
+    else step(k1, v1, true, j0, none);
   }
-  }
+
+  mma_ops<kRT, W64>(ops, acc, accl);  // the last staged step
 
   // Per lane: row tile rt holds head 4rt + lane/16 with its four digits in
   // acc[rt][c][d] (digit d carries 2^-(8+4d)); column lane%16 of channel
