@@ -235,6 +235,43 @@ int spk_lif_pack_write(const void *x, int x_dtype, const int64_t x_strides[4],
                        void *stream);
 
 /*
+ * One LIF site of spk_lif_pack_write_sites: the arguments of one
+ * spk_lif_pack_write call (x dtype and T shared by all sites of a launch).
+ *   x            [T, n_tok, H, D] at x_strides (elements)
+ *   beta, threshold  param_dtype [D]
+ *   out          int32 packed output at out_strides: [T, n_tok, H, W] when
+ *                scatter == 0, the paged cache [T, H, num_slots, W] when
+ *                scatter != 0 (token i -> slot slot_mapping[i]; slots outside
+ *                [0, num_slots) skip the token)
+ */
+typedef struct SpkLifSite {
+  const void *x;
+  int64_t x_strides[4];
+  const void *beta;
+  const void *threshold;
+  int param_dtype;
+  int scatter;
+  int32_t *out;
+  int64_t out_strides[3];
+  int64_t num_slots;
+  int64_t n_tok;
+  int H;
+  int D;
+} SpkLifSite;
+
+/*
+ * Several fused LIF + pack (+ cache scatter) sites in ONE launch, e.g. the
+ * q, k and v sites of an attention layer: the k/v sites scatter into their
+ * caches by slot_mapping (int64 [n_tok]), the q site writes the packed-query
+ * buffer.  Same results as one spk_lif_pack_write per site; one launch
+ * instead of three keeps the small k/v sites from running alone on a mostly
+ * idle GPU.  Replaces attention.py:138-149 with modeling_fast.py:132-134
+ * (three lif_multistep, pack_spikes, two index_copy_).  1 <= nsites <= 4.
+ */
+int spk_lif_pack_write_sites(const SpkLifSite *sites, int nsites, int x_dtype, int T,
+                             const int64_t *slot_mapping, void *stream);
+
+/*
  * Bit-pack rows: x [rows, C] (row stride x_row_stride elements, channel
  * stride 1) of any supported dtype -> int32 [rows, W] contiguous, nonzero ->
  * 1.  Replaces _pack_kernel (spikeinfer/kernels/packing.py:57-81, 114-133).

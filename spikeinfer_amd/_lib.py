@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 
 import torch
 
@@ -34,6 +35,27 @@ DECODE_ATTN_SCRATCH_BYTES = 16 << 20  # SPK_DECODE_ATTN_SCRATCH_BYTES
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _vp = ctypes.c_void_p
 _i32, _i64, _f32, _sz = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
+
+class SpkLifSite(ctypes.Structure):
+    """struct SpkLifSite of include/spikeinfer_amd.h (one LIF-pack site)."""
+
+    _fields_ = [
+        ("x", _vp), ("x_strides", _i64 * 4), ("beta", _vp), ("threshold", _vp),
+        ("param_dtype", _i32), ("scatter", _i32), ("out", _vp), ("out_strides", _i64 * 3),
+        ("num_slots", _i64), ("n_tok", _i64), ("H", _i32), ("D", _i32),
+    ]
+
+
+_SITE_FORMAT = struct.Struct("<Q4qQQiiQ3qqqii")  # SpkLifSite, field by field (no padding)
+
+
+def pack_lif_site(x, x_strides, beta, threshold, param_dtype, scatter, out, out_strides,
+                  num_slots, n_tok, H, D) -> bytes:
+    """The bytes of one SpkLifSite (struct.pack is ~10x cheaper per launch
+    than building the ctypes Structure)."""
+    return _SITE_FORMAT.pack(x, *x_strides, beta, threshold, param_dtype, scatter, out,
+                             *out_strides, num_slots, n_tok, H, D)
+
 
 # name -> (restype, argtypes); mirrors include/spikeinfer_amd.h
 _SIGNATURES = {
@@ -65,6 +87,7 @@ _SIGNATURES = {
     "spk_lif_pack_write": (_i32, [
         _vp, _i32, _i64p, _vp, _vp, _i32, _vp, _i64p, _vp, _i64, _vp, _i32, _i32, _i64,
         _i32, _i32, _vp]),
+    "spk_lif_pack_write_sites": (_i32, [ctypes.c_char_p, _i32, _i32, _i32, _vp, _vp]),
     "spk_pack": (_i32, [_vp, _i32, _i64, _vp, _i64, _i32, _vp]),
     "spk_unpack": (_i32, [_vp, _i64, _i32, _vp, _i32, _vp]),
     "spk_add_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _f32, _vp]),

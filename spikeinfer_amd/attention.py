@@ -19,7 +19,7 @@ from dataclasses import dataclass, field
 import torch
 import torch.nn.functional as F
 
-from .kernels.lif import lif_multistep, lif_pack_write
+from .kernels.lif import lif_multistep, lif_pack_write_sites
 from .kernels.packing import pack_spikes, packed_width
 from .kernels.spike_attention import gather_kv_unpacked_pair, paged_spike_attn_decode
 
@@ -151,16 +151,19 @@ def paged_attention_fused(
     """
     T, n_tok = q_cur.shape[0], q_cur.shape[1]
     dtype, device = q_cur.dtype, q_cur.device
-    lif_pack_write(k_cur, lif_k[0], lif_k[1], k_cache, slot_mapping=meta.slot_mapping)
-    lif_pack_write(v_cur, lif_v[0], lif_v[1], v_cache, slot_mapping=meta.slot_mapping)
     if out is None:
         out = torch.empty((T, n_tok, num_q_heads, head_dim), device=device, dtype=dtype)
     n_dec = meta.num_decode_tokens
+    # One launch for the three LIF sites: k and v into their cache slots, the
+    # decode tokens' q into the packed-query buffer.
+    sites = [(k_cur, lif_k[0], lif_k[1], k_cache, True), (v_cur, lif_v[0], lif_v[1], v_cache, True)]
     if n_dec:
         if q_packed is None:
             q_packed = torch.empty((T, n_dec, num_q_heads, packed_width(head_dim)),
                                    dtype=torch.int32, device=device)
-        lif_pack_write(q_cur[:, :n_dec], lif_q[0], lif_q[1], q_packed)
+        sites.append((q_cur[:, :n_dec], lif_q[0], lif_q[1], q_packed, False))
+    lif_pack_write_sites(sites, meta.slot_mapping)
+    if n_dec:
         paged_spike_attn_decode(
             q_packed, k_cache, v_cache, meta.block_tables, meta.seq_lens,
             head_dim=head_dim, block_size=meta.block_size, num_q_heads=num_q_heads,

@@ -371,6 +371,106 @@ inline unsigned grid_for(int64_t items, int per_block) {
   return static_cast<unsigned>(g);
 }
 
+// ---- several LIF-pack sites in one launch -----------------------------------
+// The 64-channel groups of all sites are numbered one after the other, each
+// site starting at a multiple of 8 groups (one wave's worth), so the site is
+// uniform over a wave and its fields stay in scalar registers.  An 8-lane group
+// then does exactly what lif_pack_vec_kernel does for that site.
+constexpr int kMaxSites = 4;
+static_assert(sizeof(SpkLifSite) == 120, "SpkLifSite layout (the Python binding packs it field by field)");
+constexpr int kGroupsPerWave = 8;
+struct MultiSites {
+  SpkLifSite s[kMaxSites];
+  int64_t gstart[kMaxSites + 1];  // first group of each site (multiples of 8), then the end
+  int64_t gcount[kMaxSites];      // groups of each site
+  int nsites;
+  int T;
+  const int64_t *slots;
+};
+
+// OR of v over the 8 lanes of each aligned lane octet (DPP: swap neighbours,
+// swap pairs, then mirror within the half row -- each step pairs lanes of the
+// octet that hold disjoint partial results).
+__device__ __forceinline__ uint32_t or_octet(uint32_t v) {
+  v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false));
+  v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false));
+  v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+
+// The x loads of a group are issued before its parameter and slot loads (they
+// do not depend on them), so a wave waits for one memory round trip, not two.
+template <int DT>
+__global__ __launch_bounds__(256) void lif_pack_sites_kernel(MultiSites m) {
+  typedef typename Elem<DT>::T E;
+  typedef E Vec __attribute__((ext_vector_type(8)));
+  const int lane = threadIdx.x & 63;
+  const int sub = lane & 7;
+  const int64_t groups = m.gstart[m.nsites];
+  const int64_t gstride = (int64_t)gridDim.x * (blockDim.x >> 3);  // a multiple of 8
+  for (int64_t gw = blockIdx.x * (int64_t)(blockDim.x >> 3) + (threadIdx.x >> 6) * kGroupsPerWave;
+       gw < groups; gw += gstride) {
+    int si = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxSites; ++k) si += (k < m.nsites && gw >= m.gstart[k]) ? 1 : 0;
+    si = __builtin_amdgcn_readfirstlane(si);  // wave-uniform: the wave's groups share a site
+    const SpkLifSite &st = m.s[si];
+    const int64_t li = gw - m.gstart[si] + (lane >> 3);
+    if (li >= m.gcount[si]) continue;  // the padding after a site (whole octets)
+    const int gpr = st.D >> 6;
+    const int64_t row = li / gpr;
+    const int grp = static_cast<int>(li - row * gpr);
+    const int64_t tok = row / st.H;
+    const int h = static_cast<int>(row - tok * st.H);
+    const int c0 = grp * 64 + sub * 8;
+    const E *xrow = static_cast<const E *>(st.x) + tok * st.x_strides[1] + h * st.x_strides[2] + c0;
+    const int64_t xs0 = st.x_strides[0];
+    // Unconditional loads (timesteps past T re-read the last one): a branch
+    // per load would make the compiler wait for each before the next.
+    Vec xv[kTBatch];
+#pragma unroll
+    for (int k = 0; k < kTBatch; ++k)
+      xv[k] = __builtin_nontemporal_load(reinterpret_cast<const Vec *>(xrow + min(k, m.T - 1) * xs0));
+    float beta[8], th[8], u[8];
+    load_params(st.beta, st.param_dtype, c0, beta);
+    load_params(st.threshold, st.param_dtype, c0, th);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      beta[i] = clamp01(beta[i]);
+      u[i] = 0.f;
+    }
+    bool write = true;
+    int64_t dst;
+    if (st.scatter) {
+      const int64_t slot = m.slots[tok];
+      write = slot >= 0 && slot < st.num_slots;
+      dst = h * st.out_strides[1] + slot * st.out_strides[2];
+    } else {
+      dst = tok * st.out_strides[1] + h * st.out_strides[2];
+    }
+    uint64_t *out = reinterpret_cast<uint64_t *>(st.out) + dst / 2 + grp;
+    const int64_t os0 = st.out_strides[0] / 2;
+    for (int t0 = 0; t0 < m.T; t0 += kTBatch) {
+      if (t0 > 0) {
+#pragma unroll
+        for (int k = 0; k < kTBatch; ++k)
+          xv[k] = __builtin_nontemporal_load(reinterpret_cast<const Vec *>(xrow + min(t0 + k, m.T - 1) * xs0));
+      }
+#pragma unroll
+      for (int k = 0; k < kTBatch; ++k) {
+        if (t0 + k >= m.T) break;
+        const Vec x = xv[k];
+        uint32_t byte = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) byte |= lif_step(u[i], elem_to_f32<DT>(x[i]), beta[i], th[i]) ? (1u << i) : 0u;
+        const uint32_t lo = or_octet(sub < 4 ? byte << (8 * sub) : 0u);
+        const uint32_t hi = or_octet(sub < 4 ? 0u : byte << (8 * (sub - 4)));
+        if (write && sub == 0) out[(t0 + k) * os0] = (static_cast<uint64_t>(hi) << 32) | lo;
+      }
+    }
+  }
+}
+
 }  // namespace spk
 
 using namespace spk;
@@ -446,6 +546,54 @@ extern "C" int spk_lif_pack_write(const void *x, int x_dtype, const int64_t x_st
                                             packed_strides[0], packed_strides[1], packed_strides[2],
                                             slot_mapping, num_slots, spikes, spike_dtype, n_tok, H, D);
   return check_launch("lif_pack_write");
+}
+
+extern "C" int spk_lif_pack_write_sites(const SpkLifSite *sites, int nsites, int x_dtype, int T,
+                                        const int64_t *slot_mapping, void *stream) {
+  if (!sites || nsites < 1 || nsites > kMaxSites)
+    return fail(SPK_EINVAL, "nsites must be 1..%d, got %d", kMaxSites, nsites);
+  if (T <= 0) return fail(SPK_EINVAL, "bad T=%d", T);
+  if (!valid_float_dtype(x_dtype)) return fail(SPK_EINVAL, "unsupported x dtype %d", x_dtype);
+  MultiSites m{};
+  m.nsites = nsites;
+  m.T = T;
+  m.slots = slot_mapping;
+  bool vec_ok = x_dtype == SPK_BF16 || x_dtype == SPK_F16;
+  int64_t g = 0;
+  for (int i = 0; i < nsites; ++i) {
+    const SpkLifSite &s = sites[i];
+    if (s.n_tok < 0 || s.H <= 0 || s.D <= 0)
+      return fail(SPK_EINVAL, "site %d: bad sizes n_tok=%lld H=%d D=%d", i, (long long)s.n_tok, s.H, s.D);
+    if (s.D > 128) return fail(SPK_EUNSUPPORTED, "fused LIF-pack supports D <= 128, got %d", s.D);
+    if (!valid_float_dtype(s.param_dtype)) return fail(SPK_EINVAL, "site %d: param dtype %d", i, s.param_dtype);
+    if (s.scatter && !slot_mapping) return fail(SPK_EINVAL, "site %d scatters but slot_mapping is NULL", i);
+    vec_ok = vec_ok && s.D % 64 == 0 && s.x_strides[3] == 1 && (s.x_strides[0] % 8) == 0 &&
+             (s.x_strides[1] % 8) == 0 && (s.x_strides[2] % 8) == 0 &&
+             (reinterpret_cast<uintptr_t>(s.x) & 15) == 0 && (s.out_strides[0] % 2) == 0 &&
+             (s.out_strides[1] % 2) == 0 && (s.out_strides[2] % 2) == 0 &&
+             (reinterpret_cast<uintptr_t>(s.out) & 7) == 0;
+    m.s[i] = s;
+    m.gstart[i] = g;
+    m.gcount[i] = s.n_tok * s.H * (s.D / 64);
+    g += (m.gcount[i] + kGroupsPerWave - 1) / kGroupsPerWave * kGroupsPerWave;
+  }
+  m.gstart[nsites] = g;
+  if (!vec_ok) {  // the general kernels, one launch per site
+    for (int i = 0; i < nsites; ++i) {
+      const SpkLifSite &s = sites[i];
+      const int rc = spk_lif_pack_write(s.x, x_dtype, s.x_strides, s.beta, s.threshold, s.param_dtype,
+                                        s.out, s.out_strides, s.scatter ? slot_mapping : nullptr,
+                                        s.num_slots, nullptr, 0, T, s.n_tok, s.H, s.D, stream);
+      if (rc != SPK_OK) return rc;
+    }
+    return SPK_OK;
+  }
+  if (g == 0) return SPK_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned grid = grid_for(g, 32);
+  if (x_dtype == SPK_BF16) lif_pack_sites_kernel<SPK_BF16><<<grid, 256, 0, st>>>(m);
+  else lif_pack_sites_kernel<SPK_F16><<<grid, 256, 0, st>>>(m);
+  return check_launch("lif_pack_write_sites");
 }
 
 extern "C" int spk_pack(const void *x, int x_dtype, int64_t x_row_stride, int32_t *out, int64_t rows,

@@ -5,7 +5,7 @@ include/spikeinfer_amd.h and have no CPU fallback.  The ``*_ref`` /
 ``*_cpu`` names (reference_paths.py) are the reference's eager-torch paths,
 restated; the operators never call them.
 """
-from .lif import lif_multistep, lif_pack_write, validate_thresholds
+from .lif import lif_multistep, lif_pack_write, lif_pack_write_sites, validate_thresholds
 from .packing import (
     BITS_PER_WORD,
     pack_spikes,
@@ -36,6 +36,7 @@ __all__ = [
     "paged_spike_attn_decode_cpu",
     "unpack_spikes_torch",
     "lif_pack_write",
+    "lif_pack_write_sites",
     "validate_thresholds",
     "pack_spikes",
     "unpack_spikes",

@@ -18,6 +18,8 @@ _FLOATS = (torch.float32, torch.float16, torch.bfloat16)
 
 
 def _param(p: torch.Tensor, n: int, dev) -> torch.Tensor:
+    if p.dtype in _FLOATS and p.dim() == 1 and p.shape[0] == n and p.is_contiguous() and p.device == dev:
+        return p  # the usual case, without the reshape/copy calls (host time per launch)
     if p.device != dev:
         raise ValueError(f"LIF parameter on {p.device}, input on {dev}")
     p = p.reshape(n)
@@ -100,10 +102,39 @@ def lif_pack_write(
 
     Returns ``out``.
     """
+    if slot_mapping is not None:
+        if slot_mapping.dtype != torch.int64:
+            slot_mapping = slot_mapping.to(torch.int64)
+        slot_mapping = slot_mapping.contiguous()
+    if spikes_out is not None:
+        site = _site(x, beta, threshold, out, slot_mapping)
+        T, n_tok, H, D = x.shape
+        if tuple(spikes_out.shape) != (T, n_tok, H, D) or not spikes_out.is_contiguous():
+            raise ValueError("spikes_out must be a contiguous [T, n_tok, H, D] tensor")
+        _lib.require_gpu(spikes_out)
+        sd = torch.uint8 if spikes_out.dtype == torch.bool else spikes_out.dtype
+        st = _lib.SpkLifSite.from_buffer_copy(site["struct"])
+        _lib.check(
+            _lib.load().spk_lif_pack_write(
+                x.data_ptr(), _lib.dtype_code(x.dtype), st.x_strides, st.beta, st.threshold,
+                st.param_dtype, out.data_ptr(), st.out_strides, _lib.ptr(site["slots"]),
+                st.num_slots, spikes_out.data_ptr(), _lib.dtype_code(sd), T, n_tok, H, D,
+                _lib.stream_of(x.device),
+            ),
+            "lif_pack_write",
+        )
+        return out
+    lif_pack_write_sites([(x, beta, threshold, out, slot_mapping is not None)], slot_mapping)
+    return out
+
+
+def _site(x, beta, threshold, out, slot_mapping):
+    """Validates one LIF-pack site and returns its SpkLifSite (plus the
+    tensors it points into, kept alive by the caller until the launch)."""
     if x.ndim != 4:
         raise ValueError(f"expected x as [T, n_tok, H, D], got shape {tuple(x.shape)}")
     T, n_tok, H, D = x.shape
-    dev = _lib.require_gpu(x, out, slot_mapping, spikes_out)
+    dev = _lib.require_gpu(x, out, slot_mapping)
     if x.dtype not in _FLOATS:
         raise ValueError(f"lif_pack_write input must be a float tensor, got {x.dtype}")
     W = packed_width(D)
@@ -112,38 +143,64 @@ def lif_pack_write(
     if slot_mapping is None:
         if tuple(out.shape[:3]) != (T, n_tok, H):
             raise ValueError(f"packed buffer shape {tuple(out.shape)} != {(T, n_tok, H, W)}")
-        pstr = (out.stride(0), out.stride(1), out.stride(2))
-        num_slots, slots_ptr = 0, None
+        num_slots = 0
     else:
         if out.shape[0] != T or out.shape[1] != H:
             raise ValueError(f"cache shape {tuple(out.shape)} does not match T={T}, H={H}")
         if slot_mapping.numel() < n_tok:
             raise ValueError(f"slot_mapping has {slot_mapping.numel()} entries for {n_tok} tokens")
-        if slot_mapping.dtype != torch.int64:
-            slot_mapping = slot_mapping.to(torch.int64)
-        slot_mapping = slot_mapping.contiguous()
-        pstr = (out.stride(0), out.stride(1), out.stride(2))
-        num_slots, slots_ptr = out.shape[2], slot_mapping.data_ptr()
-    spike_dtype = 0
-    if spikes_out is not None:
-        if tuple(spikes_out.shape) != (T, n_tok, H, D) or not spikes_out.is_contiguous():
-            raise ValueError("spikes_out must be a contiguous [T, n_tok, H, D] tensor")
-        sd = torch.uint8 if spikes_out.dtype == torch.bool else spikes_out.dtype
-        spike_dtype = _lib.dtype_code(sd)
+        num_slots = out.shape[2]
     beta_c = _param(beta, D, dev)
     th_c = _param(threshold, D, dev)
     if beta_c.dtype != th_c.dtype:  # mixed dtypes: both to fp32 (exact), as the reference loads them
         beta_c, th_c = beta_c.float(), th_c.float()
+    os_ = out.stride()
+    st = _lib.pack_lif_site(x.data_ptr(), x.stride(), beta_c.data_ptr(), th_c.data_ptr(),
+                            _lib.dtype_code(beta_c.dtype), 0 if slot_mapping is None else 1,
+                            out.data_ptr(), os_[:3], num_slots, n_tok, H, D)
+    return {"struct": st, "keep": (beta_c, th_c), "slots": slot_mapping, "T": T, "dev": dev}
+
+
+def lif_pack_write_sites(sites, slot_mapping: torch.Tensor | None = None) -> None:
+    """Several :func:`lif_pack_write` sites in one launch (1 to 4), e.g. an
+    attention layer's k and v (scattered into their caches by
+    ``slot_mapping``) and its decode queries (into the packed buffer).
+
+    Args:
+        sites: sequence of ``(x, beta, threshold, out, scatter)``; ``scatter``
+            True sends token ``i`` to cache slot ``slot_mapping[i]`` (the cache
+            form of ``out``), False writes the packed buffer form.  All ``x``
+            share one dtype and T.
+        slot_mapping: int64 ``[n_tok]``, needed when any site scatters.
+
+    Same bits as one :func:`lif_pack_write` per site; replaces the three LIF
+    sites of attention.py:138-149 / modeling_fast.py:132-134.
+    """
+    sites = list(sites)
+    if not 1 <= len(sites) <= 4:
+        raise ValueError(f"lif_pack_write_sites takes 1 to 4 sites, got {len(sites)}")
+    if slot_mapping is not None:
+        if slot_mapping.dtype != torch.int64:
+            slot_mapping = slot_mapping.to(torch.int64)
+        slot_mapping = slot_mapping.contiguous()
+    built = []
+    for x, beta, th, out, scatter in sites:
+        if scatter and slot_mapping is None:
+            raise ValueError("a scattering site needs slot_mapping")
+        built.append(_site(x, beta, th, out, slot_mapping if scatter else None))
+    x_dtype = sites[0][0].dtype
+    T = built[0]["T"]
+    dev = built[0]["dev"]
+    for (x, *_), b in zip(sites, built):
+        if x.dtype != x_dtype or b["T"] != T or b["dev"] != dev:
+            raise ValueError("lif_pack_write_sites: every site needs the same x dtype, T and device")
+    arr = b"".join(b["struct"] for b in built)
     _lib.check(
-        _lib.load().spk_lif_pack_write(
-            x.data_ptr(), _lib.dtype_code(x.dtype), _lib.strides(x),
-            beta_c.data_ptr(), th_c.data_ptr(), _lib.dtype_code(beta_c.dtype),
-            out.data_ptr(), (_lib.ctypes.c_int64 * 3)(*pstr), slots_ptr, num_slots,
-            _lib.ptr(spikes_out), spike_dtype, T, n_tok, H, D, _lib.stream_of(dev),
-        ),
-        "lif_pack_write",
+        _lib.load().spk_lif_pack_write_sites(
+            arr, len(built), _lib.dtype_code(x_dtype), T, _lib.ptr(slot_mapping),
+            _lib.stream_of(dev)),
+        "lif_pack_write_sites",
     )
-    return out
 
 
 def validate_thresholds(model):

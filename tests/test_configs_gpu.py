@@ -195,8 +195,11 @@ def test_config3_bf16_all_layers(gpu):
         assert (np.abs(got - want) <= np.abs(want) * 2.0 ** -8 + 1e-6).all(), f"layer {layer}"
 
 
-def test_config2_full_size_bit_exact(gpu):
-    from spikeinfer_amd.kernels import lif_multistep, lif_pack_write
+@pytest.mark.parametrize("one_launch", [True, False])
+def test_config2_full_size_bit_exact(one_launch, gpu):
+    """Both q/k/v forms: one spk_lif_pack_write_sites launch (what the bench
+    times) and one spk_lif_pack_write per site."""
+    from spikeinfer_amd.kernels import lif_multistep, lif_pack_write, lif_pack_write_sites
 
     n_tok, S = 4096, 16 * 257 * 2
     g = torch.Generator(device=gpu).manual_seed(2000)
@@ -210,9 +213,13 @@ def test_config2_full_size_bit_exact(gpu):
     qbuf = torch.empty((T, n_tok, HQ, 2), dtype=torch.int32, device=gpu)
     kc = torch.zeros((T, HKV, S, 2), dtype=torch.int32, device=gpu)
     vc = torch.zeros_like(kc)
-    lif_pack_write(xq, beta, th, qbuf)
-    lif_pack_write(xk, beta, th, kc, slot_mapping=slots)
-    lif_pack_write(xv, beta, th, vc, slot_mapping=slots)
+    if one_launch:
+        lif_pack_write_sites([(xq, beta, th, qbuf, False), (xk, beta, th, kc, True),
+                              (xv, beta, th, vc, True)], slots)
+    else:
+        lif_pack_write(xq, beta, th, qbuf)
+        lif_pack_write(xk, beta, th, kc, slot_mapping=slots)
+        lif_pack_write(xv, beta, th, vc, slot_mapping=slots)
     gate = lif_multistep(xg, bg, tg, out_dtype=torch.bfloat16)
     torch.cuda.synchronize()
     b, t_ = beta.cpu().numpy(), th.cpu().numpy()

@@ -58,6 +58,23 @@ def test_host_side_validation_without_a_gpu():
     assert lib.spk_lif_pack_write(None, 2, _i64(0, 0, 0, 1), None, None, 0, None, _i64(0, 0, 0),
                                   None, 0, None, 0, 4, 4, 2, 256, None) == _lib.SPK_EUNSUPPORTED
     assert lib.spk_pack(None, 9, 1, None, 4, 4, None) == _lib.SPK_EINVAL
+    sites = bytes(ctypes.sizeof(_lib.SpkLifSite) * 5)
+    assert lib.spk_lif_pack_write_sites(sites, 5, 2, 4, None, None) == _lib.SPK_EINVAL
+    assert lib.spk_lif_pack_write_sites(sites, 0, 2, 4, None, None) == _lib.SPK_EINVAL
+    one = _lib.pack_lif_site(0, (0, 0, 0, 1), 0, 0, 0, 1, 0, (0, 0, 1), 0, 3, 2, 64)
+    assert lib.spk_lif_pack_write_sites(one, 1, 2, 4, None, None) == _lib.SPK_EINVAL
+    assert b"slot_mapping" in lib.spk_last_error()
+
+
+def test_packed_site_bytes_match_the_c_struct():
+    """pack_lif_site's bytes are the SpkLifSite layout of the header (as
+    ctypes lays it out under the platform ABI)."""
+    raw = _lib.pack_lif_site(1, (2, 3, 4, 5), 6, 7, 8, 9, 10, (11, 12, 13), 14, 15, 16, 17)
+    assert len(raw) == ctypes.sizeof(_lib.SpkLifSite) == 120
+    st = _lib.SpkLifSite.from_buffer_copy(raw)
+    assert (st.x, list(st.x_strides), st.beta, st.threshold, st.param_dtype, st.scatter, st.out,
+            list(st.out_strides), st.num_slots, st.n_tok, st.H, st.D) == (
+        1, [2, 3, 4, 5], 6, 7, 8, 9, 10, [11, 12, 13], 14, 15, 16, 17)
 
 
 def test_decode_gemm_entry_points_validate_on_the_host():

@@ -207,6 +207,54 @@ def test_lif_pack_write_matches_reference_composition(gpu):
     assert torch.equal(fused, comp)
 
 
+@pytest.mark.parametrize("D", [64, 128, 32])
+@pytest.mark.parametrize("in_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_lif_pack_write_sites_one_launch(D, in_dtype, gpu):
+    """q (packed buffer, first n_dec tokens), k and v (cache scatter) with their
+    own parameters in one spk_lif_pack_write_sites call: bit-exact against the
+    oracle per site.  D = 32 and fp32 inputs take the per-site fallback."""
+    from spikeinfer_amd.kernels import lif_pack_write_sites
+
+    rng = np.random.default_rng(300 + D)
+    T, n_tok, n_dec, Hq, Hkv, S = 4, 203, 150, 14, 2, 16 * 40
+    W = (D + 31) // 32
+    proj = rng.standard_normal((T, n_tok, (Hq + 2 * Hkv) * D)).astype(np.float32)
+    x = torch.from_numpy(proj).to(gpu).to(in_dtype)
+    xq = x[..., : Hq * D].view(T, n_tok, Hq, D)  # strided views of one projection output
+    xk = x[..., Hq * D:(Hq + Hkv) * D].view(T, n_tok, Hkv, D)
+    xv = x[..., (Hq + Hkv) * D:].view(T, n_tok, Hkv, D)
+    params = [(_rand_beta(rng, D), _rand_th(rng, D)) for _ in range(3)]
+    slots = rng.permutation(S)[:n_tok].astype(np.int64)
+    slots[5] = -1  # pad token: skipped
+    qbuf = torch.full((T, n_dec, Hq, W), 7, dtype=torch.int32, device=gpu)
+    kc = torch.full((T, Hkv, S, W), 9, dtype=torch.int32, device=gpu)
+    vc = torch.full_like(kc, 11)
+    tp = [tuple(torch.from_numpy(a).to(gpu) for a in pr) for pr in params]
+    lif_pack_write_sites([(xq[:, :n_dec], *tp[0], qbuf, False), (xk, *tp[1], kc, True),
+                          (xv, *tp[2], vc, True)], torch.from_numpy(slots).to(gpu))
+    want_q = np.full((T, n_dec, Hq, W), 7, np.int32)
+    orc.lif_pack_write(xq[:, :n_dec].float().cpu().numpy(), *params[0], want_q)
+    assert np.array_equal(qbuf.cpu().numpy(), want_q), "q"
+    for xs, c, pr, fill, name in ((xk, kc, params[1], 9, "k"), (xv, vc, params[2], 11, "v")):
+        want = np.full((T, Hkv, S, W), fill, np.int32)
+        orc.lif_pack_write(xs.float().cpu().numpy(), *pr, want, slots)
+        assert np.array_equal(c.cpu().numpy(), want), name
+
+
+def test_lif_pack_write_sites_rejects_bad_arguments(gpu):
+    from spikeinfer_amd.kernels import lif_pack_write_sites
+
+    x = torch.zeros((4, 3, 2, 64), dtype=torch.bfloat16, device=gpu)
+    b = torch.full((64,), 0.9, device=gpu)
+    out = torch.zeros((4, 3, 2, 2), dtype=torch.int32, device=gpu)
+    with pytest.raises(ValueError, match="1 to 4"):
+        lif_pack_write_sites([])
+    with pytest.raises(ValueError, match="slot_mapping"):
+        lif_pack_write_sites([(x, b, b, out, True)])
+    with pytest.raises(ValueError, match="same x dtype"):
+        lif_pack_write_sites([(x, b, b, out, False), (x.half(), b, b, out, False)])
+
+
 @pytest.mark.parametrize("in_dtype", [torch.bfloat16, torch.float16])
 def test_lif_gate_vector_path(in_dtype, gpu):
     """Config-2 MLP-gate shape, reduced: [T, tokens, 4864] half-precision in and
