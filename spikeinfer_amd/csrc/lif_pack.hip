@@ -158,78 +158,6 @@ __global__ __launch_bounds__(256) void lif_dense_vec_kernel(LifParams p, int64_t
   }
 }
 
-// Fused LIF + pack for D % 64 == 0 with 16-byte aligned, channel-contiguous
-// rows: each lane owns 8 channels of a (token, head) row (bf16/f16 input),
-// 8 lanes cover 64 channels; per timestep their 8 spike bytes are OR-reduced
-// into the 64-bit word by three xor-shuffles and one lane stores it.
-template <int DT>
-__global__ __launch_bounds__(256) void lif_pack_vec_kernel(LifParams p, int64_t xs0, int64_t xs1,
-                                                           int64_t xs2, uint64_t *packed,
-                                                           int64_t ps0, int64_t ps1, int64_t ps2,
-                                                           const int64_t *slots, int64_t num_slots,
-                                                           int64_t n_tok, int H, int D) {
-  typedef typename Elem<DT>::T E;
-  typedef E Vec __attribute__((ext_vector_type(8)));
-  const int lane = threadIdx.x & 63;
-  const int sub = lane & 7;                  // lane within its 64-channel group
-  const int groups_per_row = D >> 6;
-  const int64_t groups = n_tok * H * groups_per_row;  // 64-channel groups
-  const int64_t gstride = (int64_t)gridDim.x * (blockDim.x >> 3);
-  for (int64_t gi = blockIdx.x * (int64_t)(blockDim.x >> 3) + (threadIdx.x >> 3); gi < groups;
-       gi += gstride) {
-    const int64_t row = gi / groups_per_row;
-    const int grp = static_cast<int>(gi - row * groups_per_row);
-    const int64_t tok = row / H;
-    const int h = static_cast<int>(row - tok * H);
-    const int c0 = grp * 64 + sub * 8;
-    float beta[8], th[8], u[8];
-    load_params(p.beta, p.param_dtype, c0, beta);
-    load_params(p.th, p.param_dtype, c0, th);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      beta[i] = clamp01(beta[i]);
-      u[i] = 0.f;
-    }
-    bool write = true;
-    int64_t dst;
-    if (slots) {
-      const int64_t slot = slots[tok];
-      write = slot >= 0 && slot < num_slots;
-      dst = h * ps1 + slot * ps2;
-    } else {
-      dst = tok * ps1 + h * ps2;
-    }
-    dst = dst / 2 + grp;  // in uint64 words
-    const E *xrow = static_cast<const E *>(p.x) + tok * xs1 + h * xs2 + c0;
-    for (int t0 = 0; t0 < p.T; t0 += kTBatch) {
-      // All loads of up to kTBatch timesteps in flight before the recurrence.
-      Vec xv[kTBatch];
-#pragma unroll
-      for (int k = 0; k < kTBatch; ++k)
-        if (t0 + k < p.T)
-          xv[k] = __builtin_nontemporal_load(reinterpret_cast<const Vec *>(xrow + (t0 + k) * xs0));
-#pragma unroll
-      for (int k = 0; k < kTBatch; ++k) {
-      if (t0 + k >= p.T) break;
-      const int t = t0 + k;
-      const Vec x = xv[k];
-      uint32_t byte = 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) byte |= lif_step(u[i], elem_to_f32<DT>(x[i]), beta[i], th[i]) ? (1u << i) : 0u;
-      // bits of lane `sub` land at channel offsets 8*sub .. 8*sub+7
-      uint32_t lo = sub < 4 ? byte << (8 * sub) : 0u;
-      uint32_t hi = sub < 4 ? 0u : byte << (8 * (sub - 4));
-#pragma unroll
-      for (int off = 1; off < 8; off <<= 1) {
-        lo |= __shfl_xor(lo, off);
-        hi |= __shfl_xor(hi, off);
-      }
-      if (write && sub == 0) packed[t * (ps0 / 2) + dst] = (static_cast<uint64_t>(hi) << 32) | lo;
-      }
-    }
-  }
-}
-
 // ---- pack / unpack ---------------------------------------------------------
 // One wave per row; each 64-channel chunk is one __ballot.
 __global__ __launch_bounds__(256) void pack_kernel(const void *x, int x_dtype, int64_t row_stride,
@@ -375,7 +303,7 @@ inline unsigned grid_for(int64_t items, int per_block) {
 // The 64-channel groups of all sites are numbered one after the other, each
 // site starting at a multiple of 8 groups (one wave's worth), so the site is
 // uniform over a wave and its fields stay in scalar registers.  An 8-lane group
-// then does exactly what lif_pack_vec_kernel does for that site.
+// then packs its 64 channels for every timestep (8 per lane).
 constexpr int kMaxSites = 4;
 static_assert(sizeof(SpkLifSite) == 120, "SpkLifSite layout (the Python binding packs it field by field)");
 constexpr int kGroupsPerWave = 8;
@@ -528,15 +456,21 @@ extern "C" int spk_lif_pack_write(const void *x, int x_dtype, const int64_t x_st
                       (x_strides[2] % 8) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
                       (packed_strides[0] % 2) == 0 && (packed_strides[1] % 2) == 0 &&
                       (packed_strides[2] % 2) == 0 && (reinterpret_cast<uintptr_t>(packed) & 7) == 0;
-  if (vec_ok) {
-    const unsigned vgrid = grid_for(n_tok * H * (D / 64), 32);
-    uint64_t *pk64 = reinterpret_cast<uint64_t *>(packed);
-    if (x_dtype == SPK_BF16)
-      lif_pack_vec_kernel<SPK_BF16><<<vgrid, 256, 0, s>>>(p, x_strides[0], x_strides[1], x_strides[2], pk64,
-          packed_strides[0], packed_strides[1], packed_strides[2], slot_mapping, num_slots, n_tok, H, D);
-    else
-      lif_pack_vec_kernel<SPK_F16><<<vgrid, 256, 0, s>>>(p, x_strides[0], x_strides[1], x_strides[2], pk64,
-          packed_strides[0], packed_strides[1], packed_strides[2], slot_mapping, num_slots, n_tok, H, D);
+  if (vec_ok) {  // the one-site form of the several-sites kernel
+    SpkLifSite site{};
+    site.x = x;
+    for (int i = 0; i < 4; ++i) site.x_strides[i] = x_strides[i];
+    site.beta = beta;
+    site.threshold = threshold;
+    site.param_dtype = param_dtype;
+    site.scatter = slot_mapping != nullptr;
+    site.out = packed;
+    for (int i = 0; i < 3; ++i) site.out_strides[i] = packed_strides[i];
+    site.num_slots = num_slots;
+    site.n_tok = n_tok;
+    site.H = H;
+    site.D = D;
+    return spk_lif_pack_write_sites(&site, 1, x_dtype, T, slot_mapping, stream);
   } else if (D <= 64)
     lif_pack_kernel<1><<<grid, 256, 0, s>>>(p, x_strides[0], x_strides[1], x_strides[2], x_strides[3], pk,
                                             packed_strides[0], packed_strides[1], packed_strides[2],
