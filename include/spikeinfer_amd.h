@@ -303,7 +303,8 @@ int spk_unpack(const int32_t *words, int64_t rows, int C, void *out,
  *   x        x_dtype (BF16/F16) [T, N, (Hq + 2*Hkv) * 64], channel stride 1,
  *            strides {t, token} in elements (the q/k/v projection output)
  *   cos, sin x_dtype [table_rows, 64] tables; token i uses row positions[i]
- *   beta, threshold  param_dtype [3, 64]: q, k and v sites
+ *   beta, threshold  param_dtype [3, 64]: q, k and v sites; param_dtype
+ *            must be SPK_F32 (convert other dtypes first: it is exact)
  *   slot_mapping int64 [N]: cache slot of each token's k/v words (outside
  *            [0, num_slots): not written)
  *   k_cache, v_cache int32 [T, Hkv, num_slots, 2] at cache_strides
@@ -407,7 +408,8 @@ int spk_lif_gate_mul(const void *x, int dtype, const int64_t x_strides[2],
  * contiguous) into the kernel's operand order, spk_mlp_gate_packed_bytes(hidden,
  * I) bytes at w_packed; done once per weight.
  * spk_mlp_gate_lif: x [T, n_tok, hidden] bf16 contiguous -> y [T, n_tok, I] bf16
- * contiguous.  Supports T <= 4, hidden a multiple of 128 in [512, 1024] (and
+ * contiguous; beta, threshold [I] with param_dtype SPK_F32 (other dtypes:
+ * convert first, exactly).  Supports T <= 4, hidden a multiple of 128 in [512, 1024] (and
  * T * 16 * hidden * 2 <= 160 KiB), I / 16 in [64, 512]; returns SPK_EUNSUPPORTED
  * otherwise (the caller then runs the GEMM and spk_lif_gate_mul).  The GEMM sums
  * are fp32 in a fixed order, rounded to bf16 before the LIF, as the two-launch

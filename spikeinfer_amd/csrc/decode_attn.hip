@@ -500,6 +500,9 @@ extern "C" int spk_qkv_decode_attn(const void *x, int x_dtype, const int64_t x_s
     return fail(SPK_EUNSUPPORTED, "qkv_decode_attn: input dtype %d (bf16 or f16 only)", x_dtype);
   if (!valid_float_dtype(param_dtype))
     return fail(SPK_EINVAL, "qkv_decode_attn: parameter dtype %d is not a float type", param_dtype);
+  if (param_dtype != SPK_F32)
+    return fail(SPK_EUNSUPPORTED, "qkv_decode_attn: LIF parameters must be fp32 (dtype %d given)",
+                param_dtype);
   if (T < 1 || T > kMaxFusedT)
     return fail(SPK_EUNSUPPORTED, "qkv_decode_attn: T=%d (1..%d)", T, kMaxFusedT);
   if (head_dim != 64)

@@ -331,6 +331,10 @@ struct FusedIn {
   float clo[kRounds], chi[kRounds], slo[kRounds], shi[kRounds];
 };
 
+// Every load is unconditional (lanes of a round past the last head read the
+// last head's currents, timesteps past t re-read timestep t; both are
+// dropped): with a branch per load the compiler waited for each in turn.
+// beta / th are fp32 (the host converts other dtypes, exactly).
 template <int NREP, int XDT>
 __device__ __forceinline__ void fused_load(const AttnParams &p, int n, int t, int kvh, int wave,
                                            int lane, FusedIn<XDT> &in) {
@@ -342,30 +346,26 @@ __device__ __forceinline__ void fused_load(const AttnParams &p, int n, int t, in
   const E *cosr = static_cast<const E *>(f.cos) + prow * 64;
   const E *sinr = static_cast<const E *>(f.sin) + prow * 64;
   const E *xtok = static_cast<const E *>(f.x) + n * f.xs1;
+  const float *beta = static_cast<const float *>(f.beta);
+  const float *th = static_cast<const float *>(f.th);
 #pragma unroll
   for (int r = 0; r < (NREP + 2 + 7) / 8; ++r) {
-    const int hi = r * 8 + wave * 2 + (lane >> 5);
-    const bool act = hi < NREP + 2;
+    const int hi = min(r * 8 + wave * 2 + (lane >> 5), NREP + 1);
     const int site = hi < NREP ? 0 : (hi == NREP ? 1 : 2);
     const int col = (hi < NREP ? kvh * NREP + hi : (hi == NREP ? p.Hq + kvh : p.Hq + p.Hkv + kvh)) * 64;
-    float v[1];
-    load_params(f.beta, f.param_dtype, site * 64 + c, v);
-    in.blo[r] = clamp01(v[0]);
-    load_params(f.beta, f.param_dtype, site * 64 + c + 32, v);
-    in.bhi[r] = clamp01(v[0]);
-    load_params(f.th, f.param_dtype, site * 64 + c, v);
-    in.tlo[r] = v[0];
-    load_params(f.th, f.param_dtype, site * 64 + c + 32, v);
-    in.thi[r] = v[0];
+#pragma unroll
+    for (int k = 0; k < kMaxFusedT; ++k) {
+      in.xl[r][k] = xtok[min(k, t) * f.xs0 + col + c];
+      in.xh[r][k] = xtok[min(k, t) * f.xs0 + col + c + 32];
+    }
+    in.blo[r] = clamp01(beta[site * 64 + c]);
+    in.bhi[r] = clamp01(beta[site * 64 + c + 32]);
+    in.tlo[r] = th[site * 64 + c];
+    in.thi[r] = th[site * 64 + c + 32];
     in.clo[r] = elem_to_f32<XDT>(cosr[c]);
     in.chi[r] = elem_to_f32<XDT>(cosr[c + 32]);
     in.slo[r] = elem_to_f32<XDT>(sinr[c]);
     in.shi[r] = elem_to_f32<XDT>(sinr[c + 32]);
-#pragma unroll
-    for (int k = 0; k < kMaxFusedT; ++k) {
-      in.xl[r][k] = act && k <= t ? xtok[k * f.xs0 + col + c] : E{};
-      in.xh[r][k] = act && k <= t ? xtok[k * f.xs0 + col + c + 32] : E{};
-    }
   }
 }
 

@@ -59,8 +59,8 @@ constexpr int kSlotFloats = 2 * kMaxT * 4 * 64;  // one partial: 2 tiles x T row
 // between the MFMAs (and the accumulator copies they bring cost registers).
 template <int KQ, int T>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void mlp_gate_lif_kernel(
-    const uint16_t *x, const v4u *wp, const void *beta_p, const void *th_p, int param_dtype,
-    uint16_t *y, int n, int I, int MG) {
+    const uint16_t *x, const v4u *wp, const float *beta_p, const float *th_p, uint16_t *y, int n,
+    int I, int MG) {
   constexpr int KS = 4 * KQ;       // k-steps of 32 (H = 32 KS)
   constexpr int H = 32 * KS;
   constexpr int kChunks = 4 * KS;  // 16-byte chunks per x row
@@ -71,6 +71,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int P = I / 16;
   const int p0 = r * P / kRanges, np = (r + 1) * P / kRanges - p0;
   if (np <= 0) return;  // uniform over the workgroup
+  // The LIF parameters of the pair this wave finishes (wave e < np: pair
+  // p0 + e), loaded first so their latency hides under the whole K loop.
+  const int ch = 16 * (p0 + min(wave, np - 1)) + (lane & 15);
+  const float beta = clamp01(beta_p[ch]);
+  const float th = th_p[ch];
 
   // Units (pair, K-quarter): wave w takes [u0, u1), at most 4 of them, over at
   // most two pairs.
@@ -207,11 +212,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         su[t][j] += d[((1 * kMaxT + t) * 4 + j) * 64 + lane];
       }
   }
-  const int ch = 16 * (p0 + pp) + r16;
-  float bt[1], th[1];
-  load_params(beta_p, param_dtype, ch, bt);
-  load_params(th_p, param_dtype, ch, th);
-  const float beta = clamp01(bt[0]);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int tok = m * kTok + 4 * kq + j;
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     for (int t = 0; t < T; ++t) {
       const float g = round_to<SPK_BF16>(sg[t][j]);
       const float up = round_to<SPK_BF16>(su[t][j]);
-      const bool spike = lif_step(u, g, beta, th[0]);
+      const bool spike = lif_step(u, g, beta, th);
       y[(static_cast<int64_t>(t) * n + tok) * I + ch] = f32_to_elem<SPK_BF16>((spike ? 1.f : 0.f) * up);
     }
   }
@@ -277,6 +277,9 @@ extern "C" int spk_mlp_gate_lif(const void *x, const void *w_packed, const void 
   if (dtype != SPK_BF16) return fail(SPK_EUNSUPPORTED, "mlp_gate_lif: bf16 only");
   if (!valid_float_dtype(param_dtype))
     return fail(SPK_EINVAL, "mlp_gate_lif: parameter dtype %d is not a float type", param_dtype);
+  if (param_dtype != SPK_F32)
+    return fail(SPK_EUNSUPPORTED, "mlp_gate_lif: LIF parameters must be fp32 (dtype %d given)",
+                param_dtype);
   if (!mlp_shape_ok(T, n_tok, hidden, inter))
     return fail(SPK_EUNSUPPORTED, "mlp_gate_lif: T=%d n_tok=%d hidden=%d inter=%d not supported", T,
                 n_tok, hidden, inter);
@@ -298,7 +301,8 @@ extern "C" int spk_mlp_gate_lif(const void *x, const void *w_packed, const void 
       attr = true;                                                                                 \
     }                                                                                              \
     mlp::mlp_gate_lif_kernel<KQ, TT><<<grid, mlp::kThreads, mlp::kLdsBytes, s>>>(                   \
-        xp, wp, beta, threshold, param_dtype, yp, n_tok, inter, MG);                               \
+        xp, wp, static_cast<const float *>(beta), static_cast<const float *>(threshold), yp, n_tok,  \
+        inter, MG);                                                                                \
   }
 #define SPK_MLP_CASE(KQ)                                                                             \
   case KQ:                                                                                         \

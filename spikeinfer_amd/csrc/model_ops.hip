@@ -108,6 +108,90 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(typename Elem<DT>::T *
   for (int v = lane; v < nv; v += 64) norm(hr[v], wr[v], v, r);
 }
 
+// Sum over the wave, the same value in every lane: DPP adds within each row of
+// 16 lanes (pairs, quads, half rows, rows), then the four row sums by readlane.
+__device__ __forceinline__ float wave_sum(float v) {
+  auto dpp = [](float x, int ctrl) -> float {
+    switch (ctrl) {  // the control must be a constant: one instantiation each
+      case 0xB1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+      case 0x4E: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+      case 0x141: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));
+      default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));
+    }
+  };
+  v += dpp(v, 0xB1);   // quad_perm [1,0,3,2]
+  v += dpp(v, 0x4E);   // quad_perm [2,3,0,1]
+  v += dpp(v, 0x141);  // row_half_mirror
+  v += dpp(v, 0x140);  // row_mirror
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// add_rmsnorm for rows of at most 64 * kNormRegVecs vectors (hidden 896 at
+// bf16 is 112): every load of the row -- weights, h, delta -- is issued at once
+// (lanes past the row re-read its last vector and drop it), so a wave waits
+// for one memory round trip; with a branch per load the compiler waited for
+// each in turn.
+template <int DT, bool ADD>
+__global__ __launch_bounds__(64) void add_rmsnorm_reg_kernel(typename Elem<DT>::T *h,
+                                                             const typename Elem<DT>::T *delta,
+                                                             const typename Elem<DT>::T *weight,
+                                                             typename Elem<DT>::T *out, int hidden,
+                                                             float eps) {
+  typedef typename Elem<DT>::T E;
+  constexpr int V = Elem<DT>::kVec;
+  typedef E Vec __attribute__((ext_vector_type(V)));
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  Vec *hr = reinterpret_cast<Vec *>(h + row * hidden);
+  const Vec *dr = reinterpret_cast<const Vec *>(delta + (ADD ? row * hidden : 0));
+  const Vec *wr = reinterpret_cast<const Vec *>(weight);
+  Vec *orow = reinterpret_cast<Vec *>(out + row * hidden);
+  const int nv = hidden / V;
+  Vec xs[kNormRegVecs], ds[kNormRegVecs], ws[kNormRegVecs];
+#pragma unroll
+  for (int k = 0; k < kNormRegVecs; ++k) {
+    const int v = min(lane + 64 * k, nv - 1);
+    ws[k] = wr[v];
+    xs[k] = hr[v];
+    if (ADD) ds[k] = dr[v];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kNormRegVecs; ++k) {
+    const int v = lane + 64 * k;
+    const bool mine = v < nv;
+    if (ADD) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) xs[k][i] = f32_to_elem<DT>(elem_to_f32<DT>(xs[k][i]) + elem_to_f32<DT>(ds[k][i]));
+      if (mine) hr[v] = xs[k];
+    }
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float f = elem_to_f32<DT>(xs[k][i]);
+      part += f * f;
+    }
+    ss += mine ? part : 0.f;
+  }
+  const float r = rsqrtf(wave_sum(ss) * (1.f / static_cast<float>(hidden)) + eps);
+#pragma unroll
+  for (int k = 0; k < kNormRegVecs; ++k) {
+    const int v = lane + 64 * k;
+    if (v >= nv) continue;
+    Vec y;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float n = round_to<DT>(elem_to_f32<DT>(xs[k][i]) * r);
+      y[i] = f32_to_elem<DT>(elem_to_f32<DT>(ws[k][i]) * n);
+    }
+    orow[v] = y;
+  }
+}
+
 // ---- embedding + first RMSNorm ------------------------------------------------
 // One wave per token: e = embed[clamp(ids[i], 0, vocab - 1)], then for every
 // timestep t: h[t, i] = e and out[t, i] = round(weight * round(e * r)) with
@@ -612,13 +696,24 @@ extern "C" int spk_add_rmsnorm(void *h, const void *delta, const void *weight, v
   // 4-wave workgroups, and the decode step runs ~20 us faster (47 calls).
   const dim3 grid(static_cast<unsigned>(rows));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool reg = hidden / vec_of(dtype) <= 64 * kNormRegVecs;
   switch (dtype) {
 #define SPK_CASE(DT)                                                                          \
   case DT:                                                                                    \
-    add_rmsnorm_kernel<DT><<<grid, 64, 0, s>>>(                                              \
-        static_cast<Elem<DT>::T *>(h), static_cast<const Elem<DT>::T *>(delta),              \
-        static_cast<const Elem<DT>::T *>(weight), static_cast<Elem<DT>::T *>(out), rows,      \
-        hidden, eps);                                                                         \
+    if (reg && delta)                                                                         \
+      add_rmsnorm_reg_kernel<DT, true><<<grid, 64, 0, s>>>(                                   \
+          static_cast<Elem<DT>::T *>(h), static_cast<const Elem<DT>::T *>(delta),            \
+          static_cast<const Elem<DT>::T *>(weight), static_cast<Elem<DT>::T *>(out), hidden,  \
+          eps);                                                                               \
+    else if (reg)                                                                             \
+      add_rmsnorm_reg_kernel<DT, false><<<grid, 64, 0, s>>>(                                  \
+          static_cast<Elem<DT>::T *>(h), nullptr, static_cast<const Elem<DT>::T *>(weight),  \
+          static_cast<Elem<DT>::T *>(out), hidden, eps);                                      \
+    else                                                                                      \
+      add_rmsnorm_kernel<DT><<<grid, 64, 0, s>>>(                                            \
+          static_cast<Elem<DT>::T *>(h), static_cast<const Elem<DT>::T *>(delta),            \
+          static_cast<const Elem<DT>::T *>(weight), static_cast<Elem<DT>::T *>(out), rows,    \
+          hidden, eps);                                                                       \
     break;
     SPK_CASE(SPK_F32) SPK_CASE(SPK_F16) SPK_CASE(SPK_BF16)
 #undef SPK_CASE

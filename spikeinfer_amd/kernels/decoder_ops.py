@@ -230,8 +230,10 @@ def qkv_decode_attention(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor
         raise ValueError("k and v caches must have the same shape and strides")
     if tuple(out.shape) != (T, n, num_q_heads, D):
         raise ValueError(f"out must be [{T}, {n}, {num_q_heads}, {D}]")
-    beta = beta.reshape(3, D).contiguous()
-    threshold = threshold.reshape(3, D).to(beta.dtype).contiguous()
+    # the fused kernel reads fp32 parameters: the upcast is exact (bf16/f16 -> fp32),
+    # and a model that keeps them in fp32 (SpikingDecoder does) pays no copy here
+    beta = beta.reshape(3, D).float().contiguous()
+    threshold = threshold.reshape(3, D).float().contiguous()
     slot_mapping = slot_mapping.to(torch.int64).contiguous()
     block_tables = block_tables.to(torch.int32)
     seq_lens = seq_lens.to(torch.int32).contiguous()
@@ -365,8 +367,9 @@ def mlp_gate_lif(x: torch.Tensor, w_packed: torch.Tensor, beta: torch.Tensor,
         out = torch.empty((T, n, I), dtype=x.dtype, device=dev)
     elif tuple(out.shape) != (T, n, I) or not out.is_contiguous() or out.dtype != x.dtype:
         raise ValueError(f"out must be contiguous bf16 [{T}, {n}, {I}]")
-    beta = beta.contiguous()
-    threshold = threshold.to(beta.dtype).contiguous()
+    # fp32 parameters (exact upcast; SpikingDecoder keeps them in fp32, so no copy)
+    beta = beta.float().contiguous()
+    threshold = threshold.float().contiguous()
     rc = _lib.load().spk_mlp_gate_lif(
         x.data_ptr(), w_packed.data_ptr(), beta.data_ptr(), threshold.data_ptr(),
         _lib.dtype_code(beta.dtype), out.data_ptr(), T, n, hidden, I, _lib.dtype_code(x.dtype),

@@ -92,12 +92,14 @@ class SpikingDecoder:
             L.post_norm = const(1.0, H)
             L.w_qkv = normal(C, H)
             L.b_qkv = normal(C)
-            L.lif_qkv_beta = const(c.beta_init, 3, self.D)
-            L.lif_qkv_th = const(c.threshold_init, 3, self.D)
+            # q/k/v LIF parameters: the model-dtype values, kept in fp32 (exact) because
+            # the fused decode kernel reads fp32
+            L.lif_qkv_beta = const(c.beta_init, 3, self.D).float()
+            L.lif_qkv_th = const(c.threshold_init, 3, self.D).float()
             L.w_o = normal(H, self.Hq * self.D)
             L.w_gu = normal(2 * I, H)
-            L.lif_gate_beta = const(c.beta_init, I)
-            L.lif_gate_th = const(c.threshold_init, I)
+            L.lif_gate_beta = const(c.beta_init, I).float()  # model-dtype values in fp32
+            L.lif_gate_th = const(c.threshold_init, I).float()
             L.w_down = normal(H, I)
             self.layers.append(L)
         # Decode-only batches run q/k/v spikes and attention as one launch
@@ -140,12 +142,12 @@ class SpikingDecoder:
             L.post_norm = cast(sd[p + "post_attention_layernorm.weight"])
             L.w_qkv = cast(torch.cat([sd[a + f"{s}_proj.weight"] for s in "qkv"]))
             L.b_qkv = cast(torch.cat([sd[a + f"{s}_proj.bias"] for s in "qkv"]))
-            L.lif_qkv_beta = cast(torch.stack([sd[a + f"lif_{s}.lif.beta"] for s in "qkv"]))
-            L.lif_qkv_th = cast(torch.stack([sd[a + f"lif_{s}.lif.threshold"] for s in "qkv"]))
+            L.lif_qkv_beta = cast(torch.stack([sd[a + f"lif_{s}.lif.beta"] for s in "qkv"])).float()
+            L.lif_qkv_th = cast(torch.stack([sd[a + f"lif_{s}.lif.threshold"] for s in "qkv"])).float()
             L.w_o = cast(sd[a + "o_proj.weight"])
             L.w_gu = cast(torch.cat([sd[m + "gate_proj.weight"], sd[m + "up_proj.weight"]]))
-            L.lif_gate_beta = cast(sd[m + "lif_gate.lif.beta"])
-            L.lif_gate_th = cast(sd[m + "lif_gate.lif.threshold"])
+            L.lif_gate_beta = cast(sd[m + "lif_gate.lif.beta"]).float()
+            L.lif_gate_th = cast(sd[m + "lif_gate.lif.threshold"]).float()
             L.w_down = cast(sd[m + "down_proj.weight"])
         self._pack_mlp()
 
