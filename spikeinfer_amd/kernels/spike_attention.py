@@ -8,6 +8,7 @@ contexts split into partitions whose partial sums simply add.
 """
 from __future__ import annotations
 
+import functools
 import math
 
 import torch
@@ -27,11 +28,13 @@ def _check_packed(name: str, t: torch.Tensor) -> None:
         raise ValueError(f"{name} must be 4-D with a contiguous word axis")
 
 
+@functools.lru_cache(maxsize=256)
 def decode_attn_workspace_bytes(
     T: int, n_seqs: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
     block_size: int, max_blocks: int,
 ) -> int:
-    """Scratch bytes :func:`paged_spike_attn_decode` needs for this shape."""
+    """Scratch bytes :func:`paged_spike_attn_decode` needs for this shape
+    (a pure function of the shape: cached, so eager calls skip the query)."""
     return int(
         _lib.load().spk_decode_attn_workspace_bytes(
             T, n_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks
