@@ -274,6 +274,7 @@ def cpu_baseline(inp, dev, budget_s=15.0, threads=16):
                        "layers": layers,
                        "torch_ms_per_step": round(ms_t * layers, 3),
                        "c_oracle_ms_per_step": round(ms_c * layers, 3)}
+    small["config2"] = cpu_config2(dev)
     return {
         "value": round(torch_gbs, 3),
         "unit": "GB/s",
@@ -291,6 +292,62 @@ def cpu_baseline(inp, dev, budget_s=15.0, threads=16):
         "configs_1_3": small,
         "host": cpu_info(),
     }
+
+
+def cpu_config2(dev, iters=3):
+    """Config 2 (LIF + pack + cache write for q/k/v, dense gate mask) on the
+    host: the reference's CPU strategy restated in torch (lif_multistep_ref,
+    the tensor-op pack, index_copy_) and the C oracle (OpenMP).  Inputs are
+    the bench's own config-2 tensors copied to the host (bf16 -> fp32)."""
+    import numpy as np
+
+    from oracle import oracle as orc
+    from spikeinfer_amd.kernels import lif_multistep_ref, pack_spikes_torch
+
+    g = torch.Generator(device=dev).manual_seed(2000)
+    n_tok, S = 4096, 16 * 257 * 2
+    xq = torch.randn((T, n_tok, HQ, D), generator=g, device=dev).bfloat16().cpu()
+    xk = torch.randn((T, n_tok, HKV, D), generator=g, device=dev).bfloat16().cpu()
+    xv = torch.randn((T, n_tok, HKV, D), generator=g, device=dev).bfloat16().cpu()
+    xg = torch.randn((T, n_tok, 4864), generator=g, device=dev).bfloat16().cpu()
+    slots = torch.randperm(S)[:n_tok]
+    beta, th = torch.full((D,), 0.9), torch.full((D,), 1.0)
+    bg, tg = torch.full((4864,), 0.9), torch.full((4864,), 1.0)
+    kc = torch.zeros((T, HKV, S, 2), dtype=torch.int32)
+    vc = torch.zeros_like(kc)
+
+    def torch_qkv():
+        pack_spikes_torch(lif_multistep_ref(xq, beta, th)[0])
+        for x, c in ((xk, kc), (xv, vc)):
+            words = pack_spikes_torch(lif_multistep_ref(x, beta, th)[0])  # [T, n_tok, Hkv, 2]
+            c.index_copy_(2, slots, words.permute(0, 2, 1, 3))
+
+    def torch_gate():
+        lif_multistep_ref(xg, bg, tg)
+
+    fq, fk, fv, fg = (x.float().numpy() for x in (xq, xk, xv, xg))
+    b, t_, bgn, tgn = beta.numpy(), th.numpy(), bg.numpy(), tg.numpy()
+    qbuf = np.zeros((T, n_tok, HQ, 2), np.int32)
+    kcn, vcn, sl = kc.numpy().copy(), vc.numpy().copy(), slots.numpy()
+
+    def c_qkv():
+        orc.lif_pack_write(fq, b, t_, qbuf)
+        orc.lif_pack_write(fk, b, t_, kcn, sl)
+        orc.lif_pack_write(fv, b, t_, vcn, sl)
+
+    def c_gate():
+        orc.lif(fg, bgn, tgn)
+
+    bytes_qkv = T * n_tok * (HQ + 2 * HKV) * D * 2 + T * n_tok * (HQ + 2 * HKV) * 8 + 2 * 8 * n_tok
+    bytes_gate = T * n_tok * 4864 * 2 * 2
+    out = {}
+    for name, fq_, fg_ in (("torch_reference_strategy", torch_qkv, torch_gate),
+                           ("c_oracle", c_qkv, c_gate)):
+        ms_q = _median_ms(fq_, iters, warm=1)
+        ms_g = _median_ms(fg_, iters, warm=1)
+        out[name] = {"qkv_ms": round(ms_q, 2), "gate_ms": round(ms_g, 2),
+                     "gbs": round((bytes_qkv + bytes_gate) / (ms_q + ms_g) / 1e6, 3)}
+    return out
 
 
 def density_sweep(inp, nbytes, args, dev, repeats=3):

@@ -15,6 +15,7 @@ from .packing import (
 )
 from .reference_paths import (
     lif_multistep_ref,
+    pack_spikes_torch,
     paged_spike_attn_decode_cpu,
     paged_spike_attn_decode_ref,
     unpack_spikes_torch,
@@ -35,6 +36,7 @@ __all__ = [
     "paged_spike_attn_decode_ref",
     "paged_spike_attn_decode_cpu",
     "unpack_spikes_torch",
+    "pack_spikes_torch",
     "lif_pack_write",
     "lif_pack_write_sites",
     "validate_thresholds",

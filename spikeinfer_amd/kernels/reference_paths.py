@@ -7,7 +7,8 @@ unpack + SDPA, ``spike_attention.py:247-282``) and
 ``paged_spike_attn_decode_cpu`` (the grouped CPU strategy,
 ``spike_attention_cpu.py:66-222``).  This module gives the same three, written
 for this package in plain torch so they run on any device, and with them a
-torch unpack (``unpack_spikes_torch``) that does not need the HIP library.
+torch pack and unpack (``pack_spikes_torch``, ``unpack_spikes_torch``, the
+reference's CPU packing) that do not need the HIP library.
 
 They are separate, explicitly named entry points.  The HIP operators in
 ``spike_attention.py`` and ``lif.py`` never call into this module: a CPU
@@ -39,6 +40,23 @@ def unpack_spikes_torch(words: torch.Tensor, num_channels: int,
     bits = (words.to(torch.int32).unsqueeze(-1) >> shifts) & 1  # [..., W, 32]
     bits = bits.reshape(*words.shape[:-1], W * BITS_PER_WORD)[..., :num_channels]
     return bits.to(dtype)
+
+
+def pack_spikes_torch(x: torch.Tensor) -> torch.Tensor:
+    """``[..., C]`` (nonzero = spike) -> ``int32 [..., ceil(C/32)]`` with tensor
+    ops, the reference's CPU packing (packing.py:97-111): bits shifted into
+    place and summed per 32-channel word, values >= 2^31 wrapped to negative
+    int32; tail bits zero."""
+    C = x.shape[-1]
+    W = packed_width(C)
+    bits = (x != 0).to(torch.int64)
+    if W * BITS_PER_WORD != C:
+        bits = F.pad(bits, (0, W * BITS_PER_WORD - C))
+    bits = bits.reshape(*bits.shape[:-1], W, BITS_PER_WORD)
+    shifts = torch.arange(BITS_PER_WORD, device=x.device, dtype=torch.int64)
+    acc = (bits << shifts).sum(dim=-1)
+    acc = torch.where(acc >= 2 ** 31, acc - 2 ** 32, acc)
+    return acc.to(torch.int32)
 
 
 def lif_multistep_ref(x, beta, threshold, mem0=None, out_dtype=None):

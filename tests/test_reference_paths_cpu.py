@@ -103,3 +103,40 @@ def test_unpack_spikes_torch_matches_packbits():
     assert np.array_equal(got, bits)
     with pytest.raises(ValueError, match="words"):
         unpack_spikes_torch(torch.from_numpy(words), 100)
+
+
+@pytest.mark.parametrize("channels", [1, 31, 32, 33, 64, 128, 4864])
+def test_pack_spikes_torch_matches_packbits(channels):
+    """The reference's CPU packing restated: equal to the numpy packbits twin,
+    any nonzero (negative, NaN) packs as 1, all-ones words wrap to -1."""
+    from spikeinfer_amd.kernels import pack_spikes_torch
+
+    rng = np.random.default_rng(channels)
+    bits = (rng.random((3, 5, channels)) < 0.3).astype(np.uint8)
+    x = torch.from_numpy(bits.astype(np.float32))
+    x[x != 0] = torch.tensor([-2.0, float("nan"), 0.5]).repeat(int((x != 0).sum()) // 3 + 1)[: int((x != 0).sum())]
+    got = pack_spikes_torch(x).numpy()
+    assert got.dtype == np.int32
+    assert np.array_equal(got, orc.np_pack(bits))
+    ones = pack_spikes_torch(torch.ones(2, 64))
+    assert (ones == -1).all()
+
+
+def test_reference_cpu_lif_pack_write_matches_oracle():
+    """The torch CPU form of the k/v cache write the bench times
+    (lif_multistep_ref -> pack_spikes_torch -> index_copy_, attention.py:138-139)
+    writes the same cache bytes as the C oracle's fused restatement."""
+    from spikeinfer_amd.kernels import lif_multistep_ref, pack_spikes_torch
+
+    rng = np.random.default_rng(4)
+    T, n_tok, H, D, S = 4, 50, 2, 64, 16 * 8
+    x = torch.from_numpy(rng.standard_normal((T, n_tok, H, D)).astype(np.float32)).bfloat16()
+    beta = torch.from_numpy((rng.random(D) * 1.2).astype(np.float32))
+    th = torch.from_numpy((rng.random(D) * 0.9 + 0.1).astype(np.float32))
+    slots = torch.from_numpy(rng.permutation(S)[:n_tok].astype(np.int64))
+    cache = torch.zeros((T, H, S, 2), dtype=torch.int32)
+    words = pack_spikes_torch(lif_multistep_ref(x, beta, th)[0])
+    cache.index_copy_(2, slots, words.permute(0, 2, 1, 3))
+    want = np.zeros((T, H, S, 2), np.int32)
+    orc.lif_pack_write(x.float().numpy(), beta.numpy(), th.numpy(), want, slots.numpy())
+    assert np.array_equal(cache.numpy(), want)
