@@ -337,6 +337,81 @@ __global__ __launch_bounds__(256) void rmsnorm_mean_t_kernel(const typename Elem
   }
 }
 
+// The same for rows of at most 2 * 64 vectors and T <= 4 (hidden 896 at bf16):
+// one wave per row with every load of the row -- all timesteps of h and delta,
+// the weights -- issued at once (lanes past the row re-read its last vector),
+// DPP sums; the same roundings and t order as rmsnorm_mean_t_kernel.
+constexpr int kMeanRegVecs = 2;
+constexpr int kMeanRegT = 4;
+template <int DT, bool ADD>
+__global__ __launch_bounds__(64) void rmsnorm_mean_t_reg_kernel(const typename Elem<DT>::T *h,
+                                                                const typename Elem<DT>::T *delta,
+                                                                const typename Elem<DT>::T *weight,
+                                                                typename Elem<DT>::T *out, int T,
+                                                                int64_t rows, int hidden, float eps) {
+  typedef typename Elem<DT>::T E;
+  constexpr int V = Elem<DT>::kVec;
+  typedef E Vec __attribute__((ext_vector_type(V)));
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int nv = hidden / V;
+  Vec x[kMeanRegT][kMeanRegVecs], d[kMeanRegT][kMeanRegVecs], w[kMeanRegVecs];
+#pragma unroll
+  for (int k = 0; k < kMeanRegVecs; ++k) {
+    const int v = min(lane + 64 * k, nv - 1);
+    w[k] = reinterpret_cast<const Vec *>(weight)[v];
+#pragma unroll
+    for (int t = 0; t < kMeanRegT; ++t) {
+      const int64_t off = (min(t, T - 1) * rows + row) * hidden;
+      x[t][k] = reinterpret_cast<const Vec *>(h + off)[v];
+      if (ADD) d[t][k] = reinterpret_cast<const Vec *>(delta + off)[v];
+    }
+  }
+  float rs[kMeanRegT];
+#pragma unroll
+  for (int t = 0; t < kMeanRegT; ++t) {
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMeanRegVecs; ++k) {
+      if (ADD) {
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+          x[t][k][i] = f32_to_elem<DT>(elem_to_f32<DT>(x[t][k][i]) + elem_to_f32<DT>(d[t][k][i]));
+      }
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float f = elem_to_f32<DT>(x[t][k][i]);
+        part += f * f;
+      }
+      ss += lane + 64 * k < nv ? part : 0.f;
+    }
+    rs[t] = rsqrtf(wave_sum(ss) * (1.f / static_cast<float>(hidden)) + eps);
+  }
+  Vec *orow = reinterpret_cast<Vec *>(out + row * hidden);
+#pragma unroll
+  for (int k = 0; k < kMeanRegVecs; ++k) {
+    const int v = lane + 64 * k;
+    if (v >= nv) continue;
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int t = 0; t < kMeanRegT; ++t) {
+      if (t >= T) break;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float n = round_to<DT>(elem_to_f32<DT>(x[t][k][i]) * rs[t]);
+        acc[i] += round_to<DT>(elem_to_f32<DT>(w[k][i]) * n);
+      }
+    }
+    Vec y;
+#pragma unroll
+    for (int i = 0; i < V; ++i) y[i] = f32_to_elem<DT>(acc[i] * (1.f / static_cast<float>(T)));
+    orow[v] = y;
+  }
+}
+
 // ---- fused q/k/v: RoPE -> LIF -> pack -> packed q / cache slots -------------------
 struct QkvParams {
   const void *x;           // [T, n_tok, (Hq + 2 Hkv) * D], channel stride 1
@@ -763,6 +838,27 @@ extern "C" int spk_rmsnorm_mean_t(const void *h, const void *delta, const void *
   if (rows == 0) return SPK_OK;
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (hidden / vec_of(dtype) <= 64 * kMeanRegVecs && T <= kMeanRegT) {
+    const dim3 g1(static_cast<unsigned>(rows));
+    switch (dtype) {
+#define SPK_CASE(DT)                                                                          \
+  case DT:                                                                                    \
+    if (delta)                                                                                \
+      rmsnorm_mean_t_reg_kernel<DT, true><<<g1, 64, 0, s>>>(                                  \
+          static_cast<const Elem<DT>::T *>(h), static_cast<const Elem<DT>::T *>(delta),       \
+          static_cast<const Elem<DT>::T *>(weight), static_cast<Elem<DT>::T *>(out), T, rows, \
+          hidden, eps);                                                                       \
+    else                                                                                      \
+      rmsnorm_mean_t_reg_kernel<DT, false><<<g1, 64, 0, s>>>(                                 \
+          static_cast<const Elem<DT>::T *>(h), nullptr,                                       \
+          static_cast<const Elem<DT>::T *>(weight), static_cast<Elem<DT>::T *>(out), T, rows, \
+          hidden, eps);                                                                       \
+    break;
+      SPK_CASE(SPK_F32) SPK_CASE(SPK_F16) SPK_CASE(SPK_BF16)
+#undef SPK_CASE
+    }
+    return check_launch("rmsnorm_mean_t");
+  }
   switch (dtype) {
 #define SPK_CASE(DT)                                                                          \
   case DT:                                                                                    \
