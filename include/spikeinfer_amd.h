@@ -49,7 +49,7 @@ enum spk_dtype {
 /* Message of the last failing call on this thread ("" if none). */
 const char *spk_last_error(void);
 
-/* ABI version, bumped on any signature change. */
+/* ABI version, bumped on any signature change (2: spk_decode_advance draws). */
 int spk_abi_version(void);
 
 /*
@@ -454,14 +454,20 @@ int spk_mlp_gate_lif(const void *x, const void *w_packed, const void *beta,
  * (spikeinfer/engine/model_runner.py:89-100, block_manager.py:71-77).  A row
  * whose next position is past its table stays put.  When history != NULL,
  * next_tokens[i] is also stored at history[i * hist_cap + *step] and *step is
- * incremented.  No reference counterpart as a kernel: the reference rebuilds
- * these tensors on the host every step.
+ * incremented.  When uniforms != NULL (rng_seeds and step required), every row
+ * i < n_rows also gets the next step's sampling draw uniforms[i] =
+ * u(rng_seeds[i], *step after the increment): SplitMix64's output function on
+ * seed + (step + 1) * 0x9E3779B97F4A7C15, top 24 bits / 2^24 -- a captured
+ * step then needs no torch RNG (whose per-replay seed/offset fills are two
+ * extra launches).  No reference counterpart as a kernel: the reference
+ * rebuilds these tensors on the host every step.
  */
 int spk_decode_advance(const int64_t *next_tokens, int64_t *input_ids, int64_t *positions,
                        int32_t *seq_lens, int64_t *slot_mapping, const int32_t *block_tables,
                        int64_t bt_stride0, int64_t bt_stride1, int max_blocks,
                        int block_size, int n_rows, const int32_t *live, int64_t *history,
-                       int32_t *step, int hist_cap, void *stream);
+                       int32_t *step, int hist_cap, const int64_t *rng_seeds,
+                       float *uniforms, void *stream);
 
 /*
  * Batched sampler, one workgroup per row (spikeinfer/engine/sampler.py:48-177):

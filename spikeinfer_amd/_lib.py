@@ -29,7 +29,7 @@ _DTYPE_CODES = {
     torch.int32: SPK_I32,
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DECODE_ATTN_SCRATCH_BYTES = 16 << 20  # SPK_DECODE_ATTN_SCRATCH_BYTES
 
 _i64p = ctypes.POINTER(ctypes.c_int64)
@@ -103,7 +103,8 @@ _SIGNATURES = {
     "spk_mlp_gate_pack": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
     "spk_mlp_gate_lif": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "spk_decode_advance": (_i32, [
-        _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i32, _vp]),
+        _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp,
+        _vp]),
     "spk_sample": (_i32, [
         _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
         _vp, _vp, _vp]),

@@ -725,12 +725,27 @@ __global__ __launch_bounds__(256) void lif_gate_mul_kernel(const typename Elem<D
 // (slot from its block table, seq_len p + 2).  A row whose next position falls
 // outside its table stays where it is.  n_live is min(n_rows, *live) when
 // `live` is given (a device count a captured graph can change).  One workgroup.
+// Uniform in [0, 1) for (seed, step): SplitMix64's output function (Steele,
+// Lea, Flood, "Fast splittable pseudorandom number generators", OOPSLA 2014)
+// on seed + (step + 1) * golden gamma, top 24 bits.
+__device__ __forceinline__ float step_uniform(uint64_t seed, uint32_t step) {
+  uint64_t z = seed + (static_cast<uint64_t>(step) + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return static_cast<float>(z >> 40) * (1.f / 16777216.f);
+}
+
 __global__ __launch_bounds__(1024) void decode_advance_kernel(
     const int64_t *next, int64_t *input_ids, int64_t *positions, int32_t *seq_lens,
     int64_t *slot_mapping, const int32_t *tables, int64_t ts0, int64_t ts1, int max_blocks,
     int block_size, int n_rows, const int32_t *live, int64_t *history, int32_t *step,
-    int hist_cap) {
+    int hist_cap, const int64_t *rng_seeds, float *uniforms) {
   const int s = step ? *step : 0;
+  // the next step's draws (every row: a parked row's value is never used)
+  if (uniforms)
+    for (int i = threadIdx.x; i < n_rows; i += blockDim.x)
+      uniforms[i] = step_uniform(static_cast<uint64_t>(rng_seeds[i]), static_cast<uint32_t>(s + 1));
   const int n_live = live ? min(n_rows, max(0, *live)) : n_rows;
   for (int i = threadIdx.x; i < n_live; i += blockDim.x) {
     const int64_t tok = next[i];
@@ -991,9 +1006,12 @@ extern "C" int spk_decode_advance(const int64_t *next_tokens, int64_t *input_ids
                                   const int32_t *block_tables, int64_t bt_stride0,
                                   int64_t bt_stride1, int max_blocks, int block_size, int n_rows,
                                   const int32_t *live, int64_t *history, int32_t *step,
-                                  int hist_cap, void *stream) {
+                                  int hist_cap, const int64_t *rng_seeds, float *uniforms,
+                                  void *stream) {
   if (!next_tokens || !input_ids || !positions || !seq_lens || !slot_mapping || !block_tables)
     return fail(SPK_EINVAL, "decode_advance: null pointer");
+  if (uniforms && (!rng_seeds || !step))
+    return fail(SPK_EINVAL, "decode_advance: uniforms need rng_seeds and a step counter");
   if (n_rows < 0 || max_blocks < 1 || !is_pow2(block_size))
     return fail(SPK_EINVAL, "decode_advance: bad shape n_rows=%d max_blocks=%d block_size=%d",
                 n_rows, max_blocks, block_size);
@@ -1002,6 +1020,7 @@ extern "C" int spk_decode_advance(const int64_t *next_tokens, int64_t *input_ids
   if (n_rows == 0) return SPK_OK;
   decode_advance_kernel<<<1, 1024, 0, static_cast<hipStream_t>(stream)>>>(
       next_tokens, input_ids, positions, seq_lens, slot_mapping, block_tables, bt_stride0,
-      bt_stride1, max_blocks, block_size, n_rows, live, history, step, hist_cap);
+      bt_stride1, max_blocks, block_size, n_rows, live, history, step, hist_cap, rng_seeds,
+      uniforms);
   return check_launch("decode_advance");
 }

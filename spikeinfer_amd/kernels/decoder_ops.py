@@ -381,12 +381,15 @@ def mlp_gate_lif(x: torch.Tensor, w_packed: torch.Tensor, beta: torch.Tensor,
 
 
 def decode_advance(next_tokens, input_ids, positions, seq_lens, slot_mapping, block_tables,
-                   block_size: int, n_rows: int, live=None, history=None, step=None) -> None:
+                   block_size: int, n_rows: int, live=None, history=None, step=None,
+                   rng_seeds=None, uniforms=None) -> None:
     """Moves rows ``[0, n_live)`` of a decode batch to their next token on the
     device (no host sync); ``n_live = min(n_rows, live[0])`` when the int32
-    device count ``live`` is given, else ``n_rows``."""
+    device count ``live`` is given, else ``n_rows``.  With ``rng_seeds`` (int64
+    ``[n_rows]``) and ``uniforms`` (fp32 ``[n_rows]``) it also writes each
+    row's draw for the next step (a function of its seed and the step count)."""
     dev = _lib.require_gpu(next_tokens, input_ids, positions, seq_lens, slot_mapping, block_tables,
-                           live, history, step)
+                           live, history, step, rng_seeds, uniforms)
     if live is not None and live.dtype != torch.int32:
         raise ValueError("live must be an int32 device count")
     for name, t, dt in (("next_tokens", next_tokens, torch.int64), ("input_ids", input_ids, torch.int64),
@@ -397,6 +400,13 @@ def decode_advance(next_tokens, input_ids, positions, seq_lens, slot_mapping, bl
             raise ValueError(f"{name} must be {dt}")
         if t.ndim == 1 and not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous")
+    if uniforms is not None:
+        if (rng_seeds is None or step is None or rng_seeds.dtype != torch.int64
+                or uniforms.dtype != torch.float32 or rng_seeds.numel() < n_rows
+                or uniforms.numel() < n_rows or not rng_seeds.is_contiguous()
+                or not uniforms.is_contiguous()):
+            raise ValueError("uniforms need contiguous int64 rng_seeds and fp32 uniforms of n_rows "
+                             "entries and a step counter")
     hist_cap = 0
     if history is not None:
         if step is None or history.dtype != torch.int64 or not history.is_contiguous():
@@ -407,7 +417,8 @@ def decode_advance(next_tokens, input_ids, positions, seq_lens, slot_mapping, bl
             next_tokens.data_ptr(), input_ids.data_ptr(), positions.data_ptr(), seq_lens.data_ptr(),
             slot_mapping.data_ptr(), block_tables.data_ptr(), block_tables.stride(0),
             block_tables.stride(1), block_tables.shape[1], block_size, n_rows,
-            _lib.ptr(live), _lib.ptr(history), _lib.ptr(step), hist_cap, _lib.stream_of(dev),
+            _lib.ptr(live), _lib.ptr(history), _lib.ptr(step), hist_cap, _lib.ptr(rng_seeds),
+            _lib.ptr(uniforms), _lib.stream_of(dev),
         ),
         "decode_advance",
     )

@@ -86,12 +86,14 @@ class DecodeRunner:
                                  self._bufs[b])
         logits = self.logits[:b]
         m.compute_logits(hidden, out=logits)
-        s.uniforms[:b].uniform_()
+        # s.uniforms holds this step's draws: written by the previous step's
+        # decode_advance (no torch RNG in the captured step)
         sample_tokens(logits, s.temperature[:b], s.top_k[:b], s.top_p[:b], s.min_p[:b],
                       s.repetition_penalty[:b], s.presence_penalty[:b], s.frequency_penalty[:b],
                       self.history, self.step_count, s.uniforms[:b], s.tokens[:b])
         decode_advance(s.tokens, self.input_ids, self.positions, self.seq_lens, self.slot_mapping,
-                       self.block_tables, self.bs, b, self.live, self.history, self.step_count)
+                       self.block_tables, self.bs, b, self.live, self.history, self.step_count,
+                       s.rng_seeds, s.uniforms)
 
     # -- prefill -------------------------------------------------------------
     @torch.no_grad()
@@ -149,7 +151,8 @@ class DecodeRunner:
                       s.repetition_penalty[:n], s.presence_penalty[:n], s.frequency_penalty[:n],
                       self.history, self.step_count, s.uniforms[:n], s.tokens[:n])
         decode_advance(s.tokens, self.input_ids, self.positions, self.seq_lens, self.slot_mapping,
-                       self.block_tables, self.bs, self.B, self.live, self.history, self.step_count)
+                       self.block_tables, self.bs, self.B, self.live, self.history, self.step_count,
+                       s.rng_seeds, s.uniforms)
 
     # -- capture and replay --------------------------------------------------------
     @torch.no_grad()
@@ -163,7 +166,8 @@ class DecodeRunner:
             if b not in self.buckets:
                 raise ValueError(f"{b} is not one of the buckets {self.buckets}")
         parked = (self.input_ids, self.positions, self.seq_lens, self.slot_mapping,
-                  self.step_count, self.history, self.live, self.sampler.tokens)
+                  self.step_count, self.history, self.live, self.sampler.tokens,
+                  self.sampler.uniforms)
         saved = [t.clone() for t in parked]
         self.live.zero_()
         bt = self.block_tables.clone()

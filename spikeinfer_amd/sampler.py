@@ -148,6 +148,8 @@ class BatchSampler:
         self.history = torch.zeros((max_rows, history_cap), dtype=torch.int64, device=self.device)
         self.history_len = torch.zeros(max_rows, dtype=torch.int32, device=self.device)
         self.uniforms = torch.zeros(max_rows, **f32)
+        # per-row seeds of the device-side draws of captured steps (decode_advance)
+        self.rng_seeds = torch.zeros(max_rows, dtype=torch.int64, device=self.device)
         self.tokens = torch.zeros(max_rows, dtype=torch.int64, device=self.device)
         self.params: list[SamplingParams] = []
         self._generators: dict[int, torch.Generator] = {}
@@ -165,6 +167,11 @@ class BatchSampler:
         self.repetition_penalty[:n] = host([p.repetition_penalty for p in params], torch.float32)
         self.presence_penalty[:n] = host([p.presence_penalty for p in params], torch.float32)
         self.frequency_penalty[:n] = host([p.frequency_penalty for p in params], torch.float32)
+        # seeded rows draw the same sequence whatever else is in the batch; the
+        # others take seeds from torch's host generator
+        fresh = torch.randint(0, 2 ** 62, (n,), dtype=torch.int64).tolist()
+        self.rng_seeds[:n] = host([int(p.seed) if p.seed is not None else fresh[i]
+                                   for i, p in enumerate(params)], torch.int64)
         self.history_len.zero_()
         self._generators = {}
 

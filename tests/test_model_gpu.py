@@ -371,6 +371,43 @@ def test_decode_advance_moves_live_rows_only(gpu):
     assert hist[:, 2].tolist() == [11, 12, 13, 14, 0] and int(step) == 3
 
 
+def _splitmix_uniform(seed: int, step: int) -> float:
+    """SplitMix64's output function (Steele, Lea, Flood 2014) on
+    seed + (step + 1) * golden gamma, top 24 bits."""
+    m = (1 << 64) - 1
+    z = (seed + (step + 1) * 0x9E3779B97F4A7C15) & m
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+    z ^= z >> 31
+    return (z >> 40) / float(1 << 24)
+
+
+def test_decode_advance_draws_next_uniforms(gpu):
+    """Every row's draw for the next step is the SplitMix64 value of its seed
+    and the incremented step: deterministic, distinct across rows and steps."""
+    B, bs = 300, 16
+    tables = torch.zeros((B, 4), dtype=torch.int32, device=gpu)
+    pos = torch.zeros(B, dtype=torch.int64, device=gpu)
+    ids, slots = torch.zeros_like(pos), torch.zeros_like(pos)
+    lens = torch.ones(B, dtype=torch.int32, device=gpu)
+    hist = torch.zeros((B, 8), dtype=torch.int64, device=gpu)
+    step = torch.tensor([5], dtype=torch.int32, device=gpu)
+    seeds = torch.randint(0, 2 ** 62, (B,), dtype=torch.int64)
+    seeds[0], seeds[1] = 0, 2 ** 62 + 12345
+    u = torch.full((B,), -1.0, device=gpu)
+    decode_advance(pos.clone(), ids, pos, lens, slots, tables, bs, B, None, hist, step,
+                   seeds.to(gpu), u)
+    got = u.cpu().tolist()
+    want = [_splitmix_uniform(int(sd), 6) for sd in seeds.tolist()]
+    assert got == pytest.approx(want, abs=0, rel=0)
+    assert all(0.0 <= x < 1.0 for x in got) and len(set(got)) > B - 3
+    assert abs(sum(got) / B - 0.5) < 0.1
+    decode_advance(pos.clone(), ids, pos, lens, slots, tables, bs, B, None, hist, step,
+                   seeds.to(gpu), u)
+    assert u.cpu().tolist() == pytest.approx([_splitmix_uniform(int(sd), 7) for sd in seeds.tolist()],
+                                             abs=0, rel=0)
+
+
 def _small_model(gpu, layers=2, seed=0):
     cfg = SpikingQwenConfig(vocab_size=1024, hidden_size=256, intermediate_size=512,
                             num_hidden_layers=layers, num_attention_heads=4, num_key_value_heads=2,
