@@ -235,30 +235,64 @@ __device__ __forceinline__ void mma_ops(const StepOps<W64> &o, v4f (&acc)[2][4 *
 // scanned largest first, and the slot's item found by a block-wide prefix
 // count of that bucket's members.  Returns -1 past the last existing item
 // (uniform over the block).  Needs N * num_parts <= kInlinePlanItems; `sh`
-// holds kMaxBuckets + 8 ints and is free again after the call.
+// holds kMaxBuckets + 8 ints and is free again after the call.  *len_out gets
+// the chosen item's sequence length (as seq_len computes it).  When every
+// sequence has the same length and one partition, the order is the item order
+// and is returned after one vote.
 constexpr int kMaxBuckets = 130;  // part_len <= 32768 tokens, 256 per bucket
+constexpr int kPlanKeys = 8;      // per-thread item keys kept in registers between the passes
 template <int KW>
-__device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh) {
+__device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh, int *len_out) {
   constexpr int kThreads = KW * 64;
   int *count = sh, *wsum = sh + kMaxBuckets, *res = wsum + KW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int M = p.N * p.num_parts;
   const int nb = ((p.part_len + 255) >> 8) + 2;  // bucket of a full partition + 1
-  // Bucket of item i, -1 when the sequence has no such partition.
-  auto key = [&](int i) {
+  // Bucket of item i, -1 when the sequence has no such partition; `len` gets
+  // the sequence's length.
+  auto key = [&](int i, int &len) {
     const int n = i % p.N, part = i / p.N;
-    const int len = seq_len(p, n);
+    len = seq_len(p, n);
     const int nparts = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
     if (part >= nparts) return -1;
     const int size = min(p.part_len, len - part * p.part_len);
     return size <= 0 ? 0 : ((size + 255) >> 8) + 1;
   };
-  for (int b = tid; b < nb; b += kThreads) count[b] = 0;
-  __syncthreads();
   const int per = (M + kThreads - 1) / kThreads;
   const int i0 = min(M, tid * per), i1 = min(M, i0 + per);
+  // The thread's first kPlanKeys keys and lengths are loaded once, before the
+  // first barrier, and reused by the second pass (one dependent memory round
+  // trip fewer in the prologue of every workgroup).
+  int kc[kPlanKeys], lc[kPlanKeys];
+#pragma unroll
+  for (int k = 0; k < kPlanKeys; ++k) kc[k] = i0 + k < i1 ? key(i0 + k, lc[k]) : -1;
+  // Equal lengths (one partition each): the order is the item order, known
+  // after one vote -- the histogram passes and their barriers are skipped.
+  if (p.num_parts == 1) {
+    const int l0 = seq_len(p, 0);
+    bool same = per <= kPlanKeys;
+#pragma unroll
+    for (int k = 0; k < kPlanKeys; ++k) same = same && (i0 + k >= i1 || lc[k] == l0);
+    if (__syncthreads_and(same)) {
+      *len_out = l0;
+      return q < M ? q : -1;
+    }
+  }
+  auto key_at = [&](int i, int &len) {
+    const int k = i - i0;
+#pragma unroll
+    for (int c = 0; c < kPlanKeys; ++c)
+      if (c == k) {
+        len = lc[c];
+        return kc[c];
+      }
+    return key(i, len);
+  };
+  for (int b = tid; b < nb; b += kThreads) count[b] = 0;
+  __syncthreads();
   for (int i = i0; i < i1; ++i) {
-    const int k = key(i);
+    int len;
+    const int k = key_at(i, len);
     if (k >= 0) atomicAdd(&count[k], 1);
   }
   __syncthreads();
@@ -291,7 +325,10 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh) {
   const int sel = res[0], j = res[1];
   if (sel < 0) return -1;
   int mine = 0;
-  for (int i = i0; i < i1; ++i) mine += key(i) == sel;
+  for (int i = i0; i < i1; ++i) {
+    int len;
+    mine += key_at(i, len) == sel;
+  }
   int incl = mine;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -304,10 +341,16 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh) {
   for (int w = 0; w < wave; ++w) before += wsum[w];
   if (before <= j && j < before + mine) {
     int r = j - before;
-    for (int i = i0; i < i1; ++i)
-      if (key(i) == sel && r-- == 0) res[2] = i;
+    for (int i = i0; i < i1; ++i) {
+      int len;
+      if (key_at(i, len) == sel && r-- == 0) {
+        res[2] = i;
+        res[3] = len;  // the slot's sequence length: no reload after the plan
+      }
+    }
   }
   __syncthreads();
+  *len_out = res[3];
   return res[2];
 }
 
@@ -412,10 +455,11 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   // sibling units of equal length.
   const int units = p.N * p.T * p.Hkv;
   int unit = blockIdx.x, part = blockIdx.y;
+  int planned_len = 0;  // planned launch: the chosen item's sequence length
   __shared__ __align__(16) char smem[kSmemBytes<W64, KW>];
   if (p.plan_inline) {  // planned launch: longest work items first
     const int ups = p.T * p.Hkv;
-    const int i = plan_slot<KW>(p, (int)blockIdx.x / ups, reinterpret_cast<int *>(smem));
+    const int i = plan_slot<KW>(p, (int)blockIdx.x / ups, reinterpret_cast<int *>(smem), &planned_len);
     if (i < 0) return;
     unit = (i % p.N) * ups + (int)blockIdx.x % ups;
     part = i / p.N;
@@ -433,7 +477,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  const int len = seq_len(p, n);
+  const int len = p.plan_inline ? planned_len : seq_len(p, n);
   const int nparts_seq = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
   if (part >= nparts_seq) return;
   const int start = part * p.part_len;

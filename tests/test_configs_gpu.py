@@ -160,6 +160,35 @@ def test_config4_deterministic_and_paths_agree(config4_inputs, gpu, monkeypatch)
     assert float((a - c).abs().max()) < 1e-5, "matrix-core and general paths disagree"
 
 
+@pytest.mark.parametrize("waves", ["2", "4"])
+def test_fixed_8k_batch_equal_and_unequal_lengths(waves, gpu, monkeypatch):
+    """The north_star shape, batch 256 x 8,192 tokens (one partition each, the
+    in-kernel launch order): with every length equal the order is decided by
+    one vote; with one sequence a token shorter the full histogram order runs.
+    Both against the oracle on a subset, and the sequences the two batches
+    share bit-identical (an item computes the same sums wherever it runs)."""
+    from spikeinfer_amd.kernels import decode_attn_workspace_bytes, paged_spike_attn_decode
+
+    monkeypatch.delenv("SPIKEINFER_AMD_ATTN_PATH", raising=False)
+    monkeypatch.setenv("SPIKEINFER_AMD_ATTN_WAVES", waves)
+    q, ((k, v),), tables, lens = _paged_inputs(gpu, 256, 8192, 8192, 0.2, 8000)
+    assert decode_attn_workspace_bytes(T, 256, HQ, HKV, D, BS, tables.shape[1]) == 0
+    print(f"fixed 8k waves={waves}", flush=True)
+    tg = tables.to(gpu)
+    eq = paged_spike_attn_decode(q, k, v, tg, lens.to(gpu), D, BS, HQ, HKV).cpu().numpy()
+    lens2 = lens.clone()
+    lens2[100] = 8191
+    uneq = paged_spike_attn_decode(q, k, v, tg, lens2.to(gpu), D, BS, HQ, HKV).cpu().numpy()
+    torch.cuda.synchronize()
+    keep = np.array([i for i in range(256) if i != 100])
+    assert np.array_equal(eq[:, keep], uneq[:, keep])
+    kn, vn = k.cpu().numpy(), v.cpu().numpy()
+    idx = np.array([0, 100, 255])
+    _check(eq[:, idx].astype(np.float64), _oracle_subset(q, kn, vn, tables, lens, idx), "fixed 8k")
+    _check(uneq[:, idx].astype(np.float64), _oracle_subset(q, kn, vn, tables, lens2, idx),
+           "8k, one shorter")
+
+
 def test_config3_bf16_all_layers(gpu):
     """Batch 64, U[128, 192], 24 layers of cache, bf16 out: every layer's
     output within one bf16 rounding of the oracle (checked on 3 layers and
