@@ -207,16 +207,19 @@ def test_lif_pack_write_matches_reference_composition(gpu):
     assert torch.equal(fused, comp)
 
 
+@pytest.mark.parametrize("T", [4, 1, 3, 8])
 @pytest.mark.parametrize("D", [64, 128, 32])
 @pytest.mark.parametrize("in_dtype", [torch.bfloat16, torch.float16, torch.float32])
-def test_lif_pack_write_sites_one_launch(D, in_dtype, gpu):
+def test_lif_pack_write_sites_one_launch(D, in_dtype, T, gpu):
     """q (packed buffer, first n_dec tokens), k and v (cache scatter) with their
     own parameters in one spk_lif_pack_write_sites call: bit-exact against the
-    oracle per site.  D = 32 and fp32 inputs take the per-site fallback."""
+    oracle per site.  D = 32 and fp32 inputs take the per-site fallback; T = 1
+    and 3 re-read the last timestep for the unused loads of the 4-step batch,
+    T = 8 runs a second batch."""
     from spikeinfer_amd.kernels import lif_pack_write_sites
 
-    rng = np.random.default_rng(300 + D)
-    T, n_tok, n_dec, Hq, Hkv, S = 4, 203, 150, 14, 2, 16 * 40
+    rng = np.random.default_rng(300 + D + T)
+    n_tok, n_dec, Hq, Hkv, S = 203, 150, 14, 2, 16 * 40
     W = (D + 31) // 32
     proj = rng.standard_normal((T, n_tok, (Hq + 2 * Hkv) * D)).astype(np.float32)
     x = torch.from_numpy(proj).to(gpu).to(in_dtype)
