@@ -35,19 +35,28 @@ def _ulps(a, b):
     return int((ai - bi).abs().max())
 
 
+@pytest.mark.parametrize("hidden,dtype", [(896, torch.bfloat16), (64, torch.bfloat16),
+                                          (2048, torch.bfloat16), (2056, torch.bfloat16),
+                                          (896, torch.float32), (1028, torch.float32)])
 @pytest.mark.parametrize("with_delta", [False, True])
-def test_add_rmsnorm_matches_qwen2_rmsnorm(gpu, with_delta):
+def test_add_rmsnorm_matches_qwen2_rmsnorm(gpu, with_delta, hidden, dtype):
+    """Rows of <= 256 vectors take the register kernel (hidden 64: lanes past
+    the row re-read its last vector; 2048 bf16: exactly 256), longer rows the
+    looping one (2056 bf16, 1028 fp32)."""
     g = torch.Generator(device=gpu).manual_seed(1)
-    h = torch.randn((4, 37, 896), generator=g, device=gpu).to(torch.bfloat16)
-    d = torch.randn((4, 37, 896), generator=g, device=gpu).to(torch.bfloat16)
-    w = (1 + 0.1 * torch.randn(896, generator=g, device=gpu)).to(torch.bfloat16)
+    h = torch.randn((4, 37, hidden), generator=g, device=gpu).to(dtype)
+    d = torch.randn((4, 37, hidden), generator=g, device=gpu).to(dtype)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g, device=gpu)).to(dtype)
     h_ref = h + d if with_delta else h.clone()
     want = rms_norm(h_ref, w, 1e-6)
     hk = h.clone()
     got = add_rmsnorm(hk, d if with_delta else None, w, 1e-6)
     assert torch.equal(hk, h_ref)  # the residual add is bit-exact
-    assert _ulps(got, want) <= 1
-    assert (got != want).float().mean() < 1e-3
+    if dtype == torch.bfloat16:
+        assert _ulps(got, want) <= 1
+        assert (got != want).float().mean() < 1e-3
+    else:
+        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-6)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -72,12 +81,16 @@ def test_embed_rmsnorm_matches_embedding_then_norm(gpu, dtype):
     assert torch.equal(x[0], x[T - 1])
 
 
+@pytest.mark.parametrize("T,hidden", [(4, 896), (1, 896), (3, 64), (6, 896), (4, 1032)])
 @pytest.mark.parametrize("with_delta", [False, True])
-def test_rmsnorm_mean_t_matches_norm_then_mean(gpu, with_delta):
+def test_rmsnorm_mean_t_matches_norm_then_mean(gpu, with_delta, T, hidden):
+    """T <= 4 and rows of <= 128 vectors take the register kernel (T = 1 and 3
+    re-read the last timestep; hidden 64 re-reads the last vector); T = 6 and
+    hidden 1032 the looping one."""
     g = torch.Generator(device=gpu).manual_seed(2)
-    h = torch.randn((4, 29, 896), generator=g, device=gpu).to(torch.bfloat16)
-    d = torch.randn((4, 29, 896), generator=g, device=gpu).to(torch.bfloat16)
-    w = (1 + 0.1 * torch.randn(896, generator=g, device=gpu)).to(torch.bfloat16)
+    h = torch.randn((T, 29, hidden), generator=g, device=gpu).to(torch.bfloat16)
+    d = torch.randn((T, 29, hidden), generator=g, device=gpu).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g, device=gpu)).to(torch.bfloat16)
     want = rms_norm(h + d if with_delta else h, w, 1e-6).mean(dim=0)
     h0 = h.clone()
     got = rmsnorm_mean_t(h, w, 1e-6, delta=d if with_delta else None)
