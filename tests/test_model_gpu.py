@@ -155,7 +155,8 @@ def test_qkv_rope_lif_pack_bit_exact(gpu, D, Hq, Hkv, n, dtype, tables):
 
 @pytest.mark.parametrize("Hq,Hkv,dtype", [(14, 2, torch.bfloat16), (4, 2, torch.bfloat16),
                                           (14, 2, torch.float16)])
-def test_qkv_decode_attention_matches_two_launches(gpu, Hq, Hkv, dtype):
+@pytest.mark.parametrize("T", [4, 1])
+def test_qkv_decode_attention_matches_two_launches(gpu, Hq, Hkv, dtype, T):
     """The fused launch gives the same attention output and the same cache
     bytes as qkv_rope_lif_pack + paged_spike_attn_decode, bit for bit: ragged
     lengths (one long enough to split into partitions), a pad row whose slot
@@ -163,8 +164,8 @@ def test_qkv_decode_attention_matches_two_launches(gpu, Hq, Hkv, dtype):
     from spikeinfer_amd.kernels import paged_spike_attn_decode
     from spikeinfer_amd.kernels.decoder_ops import qkv_decode_attention
 
-    T, D, bs = 4, 64, 16
-    g = torch.Generator(device=gpu).manual_seed(Hq * 7 + (dtype == torch.float16))
+    D, bs = 64, 16
+    g = torch.Generator(device=gpu).manual_seed(Hq * 7 + (dtype == torch.float16) + T)
     lens = torch.randint(1, 300, (37,), generator=g, device=gpu).to(torch.int32)
     lens[5] = 9001
     n = lens.numel()
