@@ -495,6 +495,24 @@ int spk_sample(const void *logits, int logits_dtype, int64_t row_stride, int row
 /* LDS bytes one spk_sample workgroup uses (for occupancy planning). */
 size_t spk_sample_shared_bytes(void);
 
+/*
+ * spk_sample with a device workspace (spk_sample_workspace_bytes(rows) bytes,
+ * 16-byte aligned; no counterpart in the reference, whose sampler is torch
+ * ops).  Rows with a top-k cut (0 < top_k <= 256, temperature >= 1e-5) are
+ * first cut into 8 slices of the vocabulary, one workgroup each, which hand
+ * the row workgroup a candidate set holding the row's top_k largest; the
+ * tokens are those spk_sample returns.  A NULL workspace is spk_sample.
+ * Calls sharing a workspace must be ordered (one stream).
+ */
+size_t spk_sample_workspace_bytes(int rows);
+int spk_sample_ws(const void *logits, int logits_dtype, int64_t row_stride, int rows, int vocab,
+                  const float *temperature, const int32_t *top_k, const float *top_p,
+                  const float *min_p, const float *repetition_penalty,
+                  const float *presence_penalty, const float *frequency_penalty,
+                  const int64_t *history, int64_t history_stride, const int32_t *history_len,
+                  int64_t history_len_stride, const float *uniforms, int64_t *out_tokens,
+                  void *workspace, size_t workspace_bytes, void *stream);
+
 
 
 #ifdef __cplusplus

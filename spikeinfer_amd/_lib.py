@@ -109,6 +109,10 @@ _SIGNATURES = {
         _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
         _vp, _vp, _vp]),
     "spk_sample_shared_bytes": (_sz, []),
+    "spk_sample_workspace_bytes": (_sz, [_i32]),
+    "spk_sample_ws": (_i32, [
+        _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
+        _vp, _vp, _vp, _sz, _vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -18,13 +18,15 @@ using namespace spk;
 
 extern "C" size_t spk_sample_shared_bytes(void) { return sizeof(smp::Shared); }
 
-extern "C" int spk_sample(const void *logits, int logits_dtype, int64_t row_stride, int rows,
-                          int vocab, const float *temperature, const int32_t *top_k,
-                          const float *top_p, const float *min_p, const float *repetition_penalty,
-                          const float *presence_penalty, const float *frequency_penalty,
-                          const int64_t *history, int64_t history_stride, const int32_t *history_len,
-                          int64_t history_len_stride, const float *uniforms, int64_t *out_tokens,
-                          void *stream) {
+extern "C" size_t spk_sample_workspace_bytes(int rows) { return rows > 0 ? smp::slice_ws_bytes(rows) : 0; }
+
+extern "C" int spk_sample_ws(const void *logits, int logits_dtype, int64_t row_stride, int rows,
+                             int vocab, const float *temperature, const int32_t *top_k,
+                             const float *top_p, const float *min_p, const float *repetition_penalty,
+                             const float *presence_penalty, const float *frequency_penalty,
+                             const int64_t *history, int64_t history_stride, const int32_t *history_len,
+                             int64_t history_len_stride, const float *uniforms, int64_t *out_tokens,
+                             void *workspace, size_t workspace_bytes, void *stream) {
   if (!valid_float_dtype(logits_dtype))
     return fail(SPK_EINVAL, "sample: logits dtype %d is not a float type", logits_dtype);
   if (!logits || !temperature || !out_tokens) return fail(SPK_EINVAL, "sample: null pointer");
@@ -34,9 +36,14 @@ extern "C" int spk_sample(const void *logits, int logits_dtype, int64_t row_stri
   if (history && (!history_len || history_stride < 1))
     return fail(SPK_EINVAL, "sample: history needs history_len and a row stride >= 1");
   if (rows == 0) return SPK_OK;
+  if (workspace && workspace_bytes < smp::slice_ws_bytes(rows))
+    return fail(SPK_EINVAL, "sample: workspace of %zu bytes, %zu needed for %d rows", workspace_bytes,
+                smp::slice_ws_bytes(rows), rows);
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15))
+    return fail(SPK_EINVAL, "sample: workspace must be 16-byte aligned");
   smp::Args a{logits, row_stride, vocab, temperature, top_k, top_p, min_p, repetition_penalty,
               presence_penalty, frequency_penalty, history, history_stride, history_len,
-              history_len_stride, uniforms, out_tokens};
+              history_len_stride, uniforms, out_tokens, workspace};
   const size_t esz = logits_dtype == SPK_F32 ? 4 : 2;
   const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (row_stride * esz) % 16 == 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -45,4 +52,16 @@ extern "C" int spk_sample(const void *logits, int logits_dtype, int64_t row_stri
     case SPK_F16: return vec ? smp::launch<SPK_F16, true>(a, rows, s) : smp::launch<SPK_F16, false>(a, rows, s);
     default: return vec ? smp::launch<SPK_BF16, true>(a, rows, s) : smp::launch<SPK_BF16, false>(a, rows, s);
   }
+}
+
+extern "C" int spk_sample(const void *logits, int logits_dtype, int64_t row_stride, int rows,
+                          int vocab, const float *temperature, const int32_t *top_k,
+                          const float *top_p, const float *min_p, const float *repetition_penalty,
+                          const float *presence_penalty, const float *frequency_penalty,
+                          const int64_t *history, int64_t history_stride, const int32_t *history_len,
+                          int64_t history_len_stride, const float *uniforms, int64_t *out_tokens,
+                          void *stream) {
+  return spk_sample_ws(logits, logits_dtype, row_stride, rows, vocab, temperature, top_k, top_p, min_p,
+                       repetition_penalty, presence_penalty, frequency_penalty, history, history_stride,
+                       history_len, history_len_stride, uniforms, out_tokens, nullptr, 0, stream);
 }

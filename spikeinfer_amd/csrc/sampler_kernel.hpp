@@ -81,7 +81,8 @@ __device__ __forceinline__ int hash_slot(int tok) {
 // Penalised logit (sampler.py:98-119): repetition first, then presence and
 // frequency, for tokens generated so far.
 // Penalty of a token known to be in the history.
-__device__ __forceinline__ float penalise_seen(const Params &P, const Shared &sh, int i, float v) {
+template <class SH>
+__device__ __forceinline__ float penalise_seen(const Params &P, const SH &sh, int i, float v) {
   if (P.rep != 1.f) v = v > 0.f ? v / P.rep : v * P.rep;
   if (P.presence != 0.f || P.frequency != 0.f) {
     float cnt = 1.f;
@@ -107,7 +108,8 @@ __device__ __forceinline__ unsigned long long shfl_up_u64(unsigned long long v, 
 }
 
 // Exclusive prefix sum over the workgroup in thread order; *total gets the sum.
-__device__ __forceinline__ unsigned long long block_exclusive_scan(unsigned long long v, Shared &sh,
+template <class SH>
+__device__ __forceinline__ unsigned long long block_exclusive_scan(unsigned long long v, SH &sh,
                                                    unsigned long long *total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   unsigned long long inc = v;
@@ -480,12 +482,526 @@ __device__ __forceinline__ int64_t filter_and_draw(const Src src, Shared &sh, co
       index_rank(src, sh, jt + 1, [&](int i, float x) { return kept(i, x) && fkey(x) == K; }));
 }
 
+
+// ---- sliced candidate stage (rows with a top-k cut) ------------------------------
+// The two sweeps over a row are most of the one-workgroup path's time.  For
+// rows with 0 < top_k <= kFastMaxK a first launch splits each row into
+// kSlices slices, one workgroup each (sample_slices_kernel):
+//   * the slice goes into registers once, with the penalties, as keys of the
+//     penalised values v; every kSampleStride-th one is a sample;
+//   * the r-th largest sample (r = k / kSampleStride + 2, doubled while the
+//     candidates fall short) fixes a bound x_B on x = v / temperature, turned
+//     once into the smallest v key whose x reaches x_B (a bisection over keys,
+//     x monotone in v), so the passes compare keys and divide only the
+//     candidates {x >= x_B}, a prefix of the slice in the total order (x
+//     descending, index ascending);
+//   * with at least k of them (or the whole slice) they hold the slice's k
+//     largest: each candidate's rank among them is counted, and the first
+//     min(k, n) go to the workspace in order.
+// sample_finish_kernel merges a row's lists (ranks by binary search), which
+// gives the row's top-k in order, and finishes with prefix sums over it:
+// min_p, top_p and the draw are the same cuts as filter_and_draw's, computed
+// from the same fixed-point masses with the same comparisons.  A slice that
+// cannot certify its list (more than kSliceCand candidates) marks itself -1,
+// and sample_kernel takes its row on the one-workgroup path.
+constexpr int kSlices = 8;
+constexpr int kSliceThreads = 512;
+constexpr int kSliceCand = 1024;
+constexpr int kFastMaxK = 256;
+static_assert(kFastMaxK < kThreads, "the finish takes one thread per kept position");
+constexpr int kSliceMaxLen = ((kMaxVocab + kSlices - 1) / kSlices + 255) & ~255;
+constexpr int kSliceSamples = kSliceMaxLen / kSampleStride;
+constexpr int kSampleRegs = kSliceSamples / 64;  // samples a lane of wave 0 reads
+
+__host__ __device__ inline int slice_len(int V) { return ((V + kSlices - 1) / kSlices + 255) & ~255; }
+
+// k of a row's top-k cut, or -1 (no cut).
+__device__ __forceinline__ long long k_request(int top_k, int V) {
+  return (top_k < 0 || top_k >= V) ? -1 : top_k;
+}
+__device__ __forceinline__ bool sliced_row(float temp, long long k_req) {
+  return !(temp < kGreedyTemp) && k_req > 0 && k_req <= kFastMaxK;
+}
+
+// The total order as one integer: larger = earlier (x descending, index ascending).
+__device__ __forceinline__ unsigned long long order_key(float x, int i) {
+  return (static_cast<unsigned long long>(fkey(x)) << 32) | (0xffffffffu - static_cast<uint32_t>(i));
+}
+
+// Workspace: x [rows][kSlices][kFastMaxK] float, index the same in int32,
+// then count [rows][kSlices] int32 and maximum v [rows][kSlices] float.
+struct SliceWs {
+  float *x;
+  int32_t *idx;
+  int32_t *count;
+  float *vmax;
+};
+__host__ __device__ inline size_t slice_ws_bytes(int rows) {
+  return static_cast<size_t>(rows) * kSlices * (2 * kFastMaxK * 4 + 8);
+}
+__host__ __device__ inline SliceWs slice_ws(void *base, int rows) {
+  char *b = static_cast<char *>(base);
+  const size_t n = static_cast<size_t>(rows) * kSlices;
+  SliceWs w;
+  w.x = reinterpret_cast<float *>(b);
+  w.idx = reinterpret_cast<int32_t *>(b + n * kFastMaxK * 4);
+  w.count = reinterpret_cast<int32_t *>(b + 2 * n * kFastMaxK * 4);
+  w.vmax = reinterpret_cast<float *>(b + 2 * n * kFastMaxK * 4 + n * 4);
+  return w;
+}
+
+// Maximum over the wave (DPP within rows of 16, then the four rows).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  auto dpp = [](uint32_t x, int ctrl) -> uint32_t {
+    switch (ctrl) {
+      case 0xB1: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0xB1, 0xF, 0xF, false));
+      case 0x4E: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x4E, 0xF, 0xF, false));
+      case 0x141: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x141, 0xF, 0xF, false));
+      default: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x140, 0xF, 0xF, false));
+    }
+  };
+  v = max(v, dpp(v, 0xB1));   // quad_perm [1,0,3,2]
+  v = max(v, dpp(v, 0x4E));   // quad_perm [2,3,0,1]
+  v = max(v, dpp(v, 0x141));  // row_half_mirror
+  v = max(v, dpp(v, 0x140));  // row_mirror
+  const uint32_t r0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 0));
+  const uint32_t r1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 16));
+  const uint32_t r2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 32));
+  const uint32_t r3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 48));
+  return max(max(r0, r1), max(r2, r3));
+}
+
+struct SliceShared {
+  uint32_t seen[kSliceMaxLen / 32];  // the slice's generated-token bits
+  int32_t hkey[kHashSlots];          // token + 1 -> count, tokens of the slice
+  int32_t hcnt[kHashSlots];
+  uint32_t samp[kSliceSamples];      // sample keys (of v)
+  unsigned long long cand[kSliceCand + 16];  // candidates' order keys (+ a zero batch)
+  float fmax[kSliceThreads / 64];
+  uint32_t wcount[kSliceThreads / 64];
+  uint32_t bound;
+};
+
+// A thread's share of a slice: vectors v = threadIdx.x + q * kSliceThreads
+// of the slice's whole vectors (elements v * W ..), every load issued at once
+// (vectors past them re-read the first and are dropped), plus one of the < W
+// trailing elements.  After pass A it holds the keys of the penalised
+// logits, so later passes only compare keys.  Needs 16-byte aligned rows (the
+// host checks).
+template <int DT>
+struct SliceRegs {
+  typedef typename Elem<DT>::T E;
+  static constexpr int W = Elem<DT>::kVec;
+  static constexpr int kVecs = kSliceMaxLen / (W * kSliceThreads);
+  typedef E Vec __attribute__((ext_vector_type(W)));
+  Vec a[kVecs];
+  E tail;
+  uint32_t key[kVecs * W + 1];  // slot q * W + j; the last one the trailing element
+  int nv;                       // whole vectors of the slice
+  bool tail_valid;
+
+  __device__ __forceinline__ void load(const E *row, int c0, int n) {
+    const Vec *pv = reinterpret_cast<const Vec *>(row + c0);
+    nv = n / W;
+#pragma unroll
+    for (int q = 0; q < kVecs; ++q) {
+      const int v = threadIdx.x + q * kSliceThreads;
+      a[q] = pv[v < nv ? v : 0];
+    }
+    const int t = nv * W + static_cast<int>(threadIdx.x);
+    tail_valid = t < n;
+    tail = row[c0 + (tail_valid ? t : 0)];
+  }
+  __device__ __forceinline__ bool valid(int slot) const {
+    return slot == kVecs * W ? tail_valid : static_cast<int>(threadIdx.x) + (slot / W) * kSliceThreads < nv;
+  }
+  __device__ __forceinline__ int elem(int slot) const {  // offset in the slice
+    return slot == kVecs * W ? nv * W + static_cast<int>(threadIdx.x)
+                             : (static_cast<int>(threadIdx.x) + (slot / W) * kSliceThreads) * W + slot % W;
+  }
+  // Pass A: key of every penalised logit; f(b, v) for each valid element.
+  template <class F>
+  __device__ __forceinline__ void penalise_all(int c0, const Params &P, const SliceShared &sh, bool has_hist, F f) {
+#pragma unroll
+    for (int q = 0; q < kVecs; ++q) {
+      const int v = threadIdx.x + q * kSliceThreads;
+      const int b = v * W;
+      const bool ok = v < nv;
+      const uint32_t bits = has_hist && ok ? ((sh.seen[b >> 5] >> (b & 31)) & ((1u << W) - 1u)) : 0u;
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        float x = elem_to_f32<DT>(a[q][j]);
+        if ((bits >> j) & 1u) x = penalise_seen(P, sh, c0 + b + j, x);
+        key[q * W + j] = fkey(x);
+        if (ok) f(b + j, x);
+      }
+    }
+    const int b = nv * W + static_cast<int>(threadIdx.x);
+    float x = elem_to_f32<DT>(tail);
+    if (tail_valid && has_hist && ((sh.seen[b >> 5] >> (b & 31)) & 1u)) x = penalise_seen(P, sh, c0 + b, x);
+    key[kVecs * W] = fkey(x);
+    if (tail_valid) f(b, x);
+  }
+};
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kSliceThreads) void sample_slices_kernel(
+    const void *logits, int64_t row_stride, int V, const float *temperature, const int32_t *top_k,
+    const float *rep, const float *presence, const float *frequency, const int64_t *history,
+    int64_t hist_stride, const int32_t *hist_len, int64_t hist_len_stride, SliceWs ws) {
+  typedef typename Elem<DT>::T E;
+  __shared__ SliceShared sh;
+  const int row = blockIdx.x / kSlices, sl = blockIdx.x % kSlices;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  Params P;
+  P.temp = temperature[row];
+  P.top_k = top_k ? top_k[row] : -1;
+  P.rep = rep ? rep[row] : 1.f;
+  P.presence = presence ? presence[row] : 0.f;
+  P.frequency = frequency ? frequency[row] : 0.f;
+  P.use_hash = P.frequency != 0.f;
+  P.top_p = 1.f;
+  P.min_p = 0.f;
+  const long long k_req = k_request(P.top_k, V);
+  if (!sliced_row(P.temp, k_req)) return;  // the row workgroup does not read this slice
+  const int64_t ws_i = static_cast<int64_t>(row) * kSlices + sl;
+  const int L = slice_len(V), c0 = sl * L, c1 = min(V, c0 + L);
+  if (c0 >= c1) {
+    if (tid == 0) {
+      ws.count[ws_i] = 0;
+      ws.vmax[ws_i] = -INFINITY;
+    }
+    return;
+  }
+  SliceRegs<DT> rg;  // the slice's logits, loaded while the history is read
+  rg.load(reinterpret_cast<const E *>(logits) + row * row_stride, c0, c1 - c0);
+  // ---- history -> the slice's bits (+ counts) ----
+  for (int w = tid; w < (c1 - c0 + 31) / 32; w += kSliceThreads) sh.seen[w] = 0u;
+  if (P.use_hash)
+    for (int s2 = tid; s2 < kHashSlots; s2 += kSliceThreads) sh.hkey[s2] = 0, sh.hcnt[s2] = 0;
+  __syncthreads();
+  int nh = 0;
+  if (history && hist_len) {
+    nh = hist_len[row * hist_len_stride];
+    const int64_t cap = hist_stride < kMaxHist ? hist_stride : kMaxHist;
+    nh = nh < 0 ? 0 : (nh > cap ? static_cast<int>(cap) : nh);
+    for (int j = tid; j < nh; j += kSliceThreads) {
+      const int64_t tok = history[row * hist_stride + j];
+      if (tok < c0 || tok >= c1) continue;
+      const int t32 = static_cast<int>(tok);
+      atomicOr(&sh.seen[(t32 - c0) >> 5], 1u << ((t32 - c0) & 31));
+      if (P.use_hash) {
+        int h = hash_slot(t32);
+        while (true) {
+          const int prev = atomicCAS(&sh.hkey[h], 0, t32 + 1);
+          if (prev == 0 || prev == t32 + 1) break;
+          h = (h + 1) % kHashSlots;
+        }
+        atomicAdd(&sh.hcnt[h], 1);
+      }
+    }
+  }
+  __syncthreads();
+  const bool has_hist = nh > 0;
+
+  // ---- maximum and samples (keys of v) ----
+  float mv = -INFINITY;
+  rg.penalise_all(c0, P, sh, has_hist, [&](int b, float v) {
+    mv = fmaxf(mv, v);
+    if ((b % kSampleStride) == 0) sh.samp[b / kSampleStride] = fkey(v);
+  });
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) mv = fmaxf(mv, __shfl_xor(mv, d));
+  if (lane == 0) sh.fmax[wave] = mv;
+  __syncthreads();
+
+  // ---- bound and candidates.  Wave 0 takes the r-th largest sample, then
+  // the smallest v key whose x reaches that sample's x; every thread counts
+  // its elements at or above it.  Too few candidates (fewer than k, the
+  // slice not exhausted): r doubles and the registers are counted again. ----
+  const int n_s = (c1 - c0 + kSampleStride - 1) / kSampleStride;
+  const long long kk = (k_req + kSampleStride - 1) / kSampleStride;
+  int r = static_cast<int>(min<long long>(n_s, kk + 2));
+  uint32_t n = 0, mine = 0, incl = 0, bound = 0;
+  while (true) {
+    if (wave == 0) {
+      uint32_t key[kSampleRegs];  // sample keys; 0 (a NaN's key) past the samples
+#pragma unroll
+      for (int q = 0; q < kSampleRegs; ++q) {
+        const int j = q * 64 + lane;
+        key[q] = j < n_s ? sh.samp[j] : 0u;
+      }
+      uint32_t best = 0;
+      for (int it = 0; it < min(r, n_s); ++it) {  // remove the largest r - 1 times, one copy each
+        uint32_t m = 0;
+#pragma unroll
+        for (int q = 0; q < kSampleRegs; ++q) m = key[q] > m ? key[q] : m;
+        best = wave_max_u32(m);
+        const unsigned long long holders = __ballot(m == best);
+        if (lane == static_cast<int>(__builtin_ctzll(holders))) {
+          bool done = false;
+#pragma unroll
+          for (int q = 0; q < kSampleRegs; ++q)
+            if (!done && key[q] == best) {
+              key[q] = 0u;
+              done = true;
+            }
+        }
+      }
+      // The smallest key k in (0, best] with unkey(k) / temp >= unkey(best) /
+      // temp (key 0 is a NaN's: never).
+      const float xb = unkey(best) / P.temp;
+      uint32_t lo = 0, hi = best;
+      while (hi - lo > 1) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (unkey(mid) / P.temp >= xb) hi = mid;
+        else lo = mid;
+      }
+      if (lane == 0) sh.bound = r > n_s ? 0u : hi;  // r past the samples: every element
+    }
+    __syncthreads();
+    bound = sh.bound;
+    mine = 0;
+#pragma unroll
+    for (int q = 0; q <= SliceRegs<DT>::kVecs * SliceRegs<DT>::W; ++q)
+      mine += rg.valid(q) && rg.key[q] >= bound ? 1u : 0u;
+    incl = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t o = __shfl_up(incl, d);
+      if (lane >= d) incl += o;
+    }
+    if (lane == 63) sh.wcount[wave] = incl;
+    __syncthreads();
+    n = 0;
+#pragma unroll
+    for (int w = 0; w < kSliceThreads / 64; ++w) n += sh.wcount[w];
+    __syncthreads();  // wcount and bound are rewritten by a retry
+    if (static_cast<long long>(n) >= k_req || static_cast<int>(n) == c1 - c0 || r > n_s) break;
+    r = r == n_s ? n_s + 1 : min(n_s, 2 * r);
+  }
+  uint32_t off = incl - mine;
+#pragma unroll
+  for (int w = 0; w < kSliceThreads / 64; ++w) off += w < wave ? sh.wcount[w] : 0u;
+  if (mine) {
+#pragma unroll
+    for (int q = 0; q <= SliceRegs<DT>::kVecs * SliceRegs<DT>::W; ++q) {
+      if (!(rg.valid(q) && rg.key[q] >= bound)) continue;
+      if (off < static_cast<uint32_t>(kSliceCand)) sh.cand[off] = order_key(unkey(rg.key[q]) / P.temp, c0 + rg.elem(q));
+      ++off;
+    }
+  }
+  if (n <= static_cast<uint32_t>(kSliceCand) && tid < 16) sh.cand[n + tid] = 0ull;
+  __syncthreads();
+  const bool ok = n <= static_cast<uint32_t>(kSliceCand) &&
+                  (static_cast<long long>(n) >= k_req || static_cast<int>(n) == c1 - c0);
+  const int nk = static_cast<int>(min<long long>(n, k_req));
+  if (ok) {
+    // The first nk candidates in order, each placed by its rank among them.
+    float *xo = ws.x + ws_i * kFastMaxK;
+    int32_t *io = ws.idx + ws_i * kFastMaxK;
+    for (int c = tid; c < static_cast<int>(n); c += kSliceThreads) {
+      const unsigned long long kc = sh.cand[c];
+      int rank = 0;
+      // 16 keys a batch, loads first (keys past n are zero: never greater).
+      for (int d0 = 0; d0 < static_cast<int>(n); d0 += 16) {
+        unsigned long long kd[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) kd[q] = sh.cand[d0 + q];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) rank += kd[q] > kc ? 1 : 0;
+      }
+      if (rank < nk) {
+        xo[rank] = unkey(static_cast<uint32_t>(kc >> 32));
+        io[rank] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(kc));
+      }
+    }
+  }
+  if (tid == 0) {
+    ws.count[ws_i] = ok ? nk : -1;
+    float m = sh.fmax[0];
+    for (int w = 1; w < kSliceThreads / 64; ++w) m = fmaxf(m, sh.fmax[w]);
+    ws.vmax[ws_i] = m;
+  }
+}
+
+struct FinishShared {
+  unsigned long long lists[kSlices * kFastMaxK];  // the slices' lists as order keys
+  float cx[kFastMaxK];                            // the merged top-k, in order
+  int32_t ci[kFastMaxK];
+  unsigned long long cums[kFastMaxK + 1];         // kept mass before each position
+  unsigned long long wsum[kWaves];
+  unsigned long long bcast[4];
+};
+
+// Whether the slices certified row `row`'s lists (every count >= 0); n gets
+// the counts and *vmax the row's largest penalised logit.
+__device__ __forceinline__ bool sliced_lists(const SliceWs &ws, int row, int (&n)[kSlices], float *vmax) {
+  bool ok = true;
+  float mv = -INFINITY;
+#pragma unroll
+  for (int sl = 0; sl < kSlices; ++sl) {
+    // Vector loads (not the scalar cache): the slices kernel wrote these.
+    n[sl] = __hip_atomic_load(ws.count + static_cast<int64_t>(row) * kSlices + sl, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+    ok = ok && n[sl] >= 0;
+    mv = fmaxf(mv, __hip_atomic_load(ws.vmax + static_cast<int64_t>(row) * kSlices + sl, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT));
+  }
+  *vmax = mv;
+  return ok;
+}
+
+// The row's sliced finish (see above): the merged top-k in sh.cx / sh.ci, in
+// order, then min_p, top_p and the draw as filter_and_draw makes them.
+__device__ __forceinline__ int64_t sliced_finish(FinishShared &sh, const SliceWs &ws, int row, const Params &P,
+                                                 long long k_req, float u, const int (&n)[kSlices], float m) {
+  const int tid = threadIdx.x;
+  // Merge: element j of slice s goes to position j + (number of elements of
+  // the other slices earlier in the order), found by binary search in each
+  // (sorted) list, staged in LDS as order keys.  Positions >= k are dropped.
+  const int64_t base = static_cast<int64_t>(row) * kSlices * kFastMaxK;
+  unsigned long long *lists = sh.lists;
+  int total = 0;
+#pragma unroll
+  for (int s = 0; s < kSlices; ++s) {
+    for (int j = tid; j < n[s]; j += kThreads)
+      lists[s * kFastMaxK + j] = order_key(ws.x[base + s * kFastMaxK + j], ws.idx[base + s * kFastMaxK + j]);
+    total += n[s];
+  }
+  __syncthreads();
+  const int kept_k = static_cast<int>(min<long long>(k_req, total));
+  for (int e = tid; e < total; e += kThreads) {  // element e of the lists, concatenated
+    int s = 0, j = e, before = 0;  // (list, position) of e; n[] indexed by constants only
+#pragma unroll
+    for (int t = 0; t < kSlices; ++t) {
+      if (e >= before && e < before + n[t]) {
+        s = t;
+        j = e - before;
+      }
+      before += n[t];
+    }
+    const unsigned long long kj = lists[s * kFastMaxK + j];
+    int pos = j;
+#pragma unroll
+    for (int t = 0; t < kSlices; ++t) {
+      if (t == s) continue;
+      int lo = 0, hi = n[t];  // count of list t's elements earlier than kj
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (lists[t * kFastMaxK + mid] > kj) lo = mid + 1;
+        else hi = mid;
+      }
+      pos += lo;
+    }
+    if (pos < kept_k) {
+      sh.cx[pos] = unkey(static_cast<uint32_t>(kj >> 32));
+      sh.ci[pos] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(kj));
+    }
+  }
+  __syncthreads();
+  // Per position j < kept_k (one thread each; kept_k <= kFastMaxK < kThreads).
+  const int j = tid;
+  const bool live = j < kept_k;
+  const float x = live ? sh.cx[j] : 0.f;
+  const uint32_t key = fkey(x);
+  const bool alive = live && (P.min_p <= 0.f || expf(x - m) >= P.min_p);
+  // The alive elements are a prefix; the top-k cut keeps the first min(k, alive).
+  const int n1 = __syncthreads_count(alive);
+  const bool in1 = j < n1;
+  const unsigned long long w = in1 ? mass_of(x, m) : 0ull;
+  unsigned long long Z;
+  const unsigned long long cum = block_exclusive_scan(w, sh, &Z);  // mass before position j
+  // Group start of j (first position with j's key) = j - (earlier equal keys).
+  int gs = j;
+  if (in1)
+    while (gs > 0 && fkey(sh.cx[gs - 1]) == key) --gs;
+  // cum of each position, for the group lookups
+  unsigned long long *cums = sh.cums;
+  if (in1) cums[j] = cum;
+  if (tid == 0) cums[n1] = Z;
+  __syncthreads();
+  // top_p: the group K with mass(keys > K) < target <= mass(keys >= K) (the
+  // first element of each group tests its group), then j ties of it.
+  int n2 = n1;
+  if (P.top_p < 1.f) {
+    const double target = static_cast<double>(P.top_p) * static_cast<double>(Z);
+    if (tid == 0) sh.bcast[2] = 0;
+    __syncthreads();
+    if (in1 && gs == j) {
+      int ge = j + 1;
+      while (ge < n1 && fkey(sh.cx[ge]) == key) ++ge;
+      const unsigned long long before = cum, after = cums[ge];
+      if (static_cast<double>(before) < target && target <= static_cast<double>(after)) {
+        unsigned long long jt = w ? static_cast<unsigned long long>(ceil((target - static_cast<double>(before)) /
+                                                                         static_cast<double>(w)))
+                                  : 1;
+        if (jt < 1) jt = 1;
+        const unsigned long long c = static_cast<unsigned long long>(ge - j);
+        sh.bcast[0] = static_cast<unsigned long long>(j) + (jt >= c ? c : jt);
+        sh.bcast[2] = 1;
+      }
+    }
+    __syncthreads();
+    if (sh.bcast[2]) n2 = static_cast<int>(sh.bcast[0]);
+    __syncthreads();
+  }
+  // Draw: the element whose interval of the kept mass holds u * total.
+  const unsigned long long Wtot = cums[n2];
+  unsigned long long T = static_cast<unsigned long long>(static_cast<double>(u) * static_cast<double>(Wtot));
+  if (T >= Wtot) T = Wtot ? Wtot - 1 : 0;
+  const double target = static_cast<double>(T) + 1.0;
+  if (tid == 0) sh.bcast[2] = 0;
+  __syncthreads();
+  if (j < n2 && gs == j) {
+    int ge = j + 1;
+    while (ge < n2 && fkey(sh.cx[ge]) == key) ++ge;
+    const unsigned long long before = cum, after = cums[ge];
+    if (static_cast<double>(before) < target && target <= static_cast<double>(after)) {
+      const unsigned long long jt = w ? (T - before) / w : 0;
+      sh.bcast[0] = static_cast<unsigned long long>(sh.ci[j + static_cast<int>(jt)]);
+      sh.bcast[2] = 1;
+    }
+  }
+  __syncthreads();
+  if (sh.bcast[2]) return static_cast<int64_t>(sh.bcast[0]);
+  // No interval holds it (not reached: the first kept element weighs 2^40):
+  // the smallest kept index.
+  int best = 0x7fffffff;
+  for (int q = 0; q < n2; ++q) best = min(best, static_cast<int>(sh.ci[q]));
+  return best;
+}
+
+// One workgroup per sliced row whose slices certified their lists; the row
+// kernel leaves those rows alone.  (A template only so that each logits
+// dtype's translation unit may instantiate it.)
+template <int DT>
+__global__ __launch_bounds__(kThreads) void sample_finish_kernel(int V, const float *temperature,
+                                                                 const int32_t *top_k, const float *top_p,
+                                                                 const float *min_p, const float *uniforms,
+                                                                 int64_t *out, SliceWs ws) {
+  __shared__ FinishShared sh;
+  const int row = blockIdx.x;
+  Params P;
+  P.temp = temperature[row];
+  P.top_k = top_k ? top_k[row] : -1;
+  const long long k_req = k_request(P.top_k, V);
+  if (!sliced_row(P.temp, k_req)) return;
+  int n[kSlices];
+  float mv;
+  if (!sliced_lists(ws, row, n, &mv)) return;
+  P.top_p = top_p ? top_p[row] : 1.f;
+  P.min_p = min_p ? min_p[row] : 0.f;
+  const int64_t tok = sliced_finish(sh, ws, row, P, k_req, uniforms ? uniforms[row] : 0.f, n, mv / P.temp);
+  if (threadIdx.x == 0) out[row] = tok;
+}
+
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void sample_kernel(
     const void *logits, int64_t row_stride, int V, const float *temperature,
     const int32_t *top_k, const float *top_p, const float *min_p, const float *rep,
     const float *presence, const float *frequency, const int64_t *history, int64_t hist_stride,
-    const int32_t *hist_len, int64_t hist_len_stride, const float *uniforms, int64_t *out) {
+    const int32_t *hist_len, int64_t hist_len_stride, const float *uniforms, int64_t *out, SliceWs ws) {
   typedef typename Elem<DT>::T E;
   extern __shared__ __align__(16) char smem_raw[];
   Shared &sh = *reinterpret_cast<Shared *>(smem_raw);
@@ -500,6 +1016,13 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
   P.presence = presence ? presence[row] : 0.f;
   P.frequency = frequency ? frequency[row] : 0.f;
   P.use_hash = P.frequency != 0.f;
+
+  // ---- sliced rows whose slices certified their lists: sample_finish_kernel's
+  if (ws.count && sliced_row(P.temp, k_request(P.top_k, V))) {
+    int n[kSlices];
+    float mv;
+    if (sliced_lists(ws, row, n, &mv)) return;
+  }
 
   // ---- history -> seen bitmap (+ counts) ------------------------------------
   const int nwords = (V + 31) >> 5;
@@ -551,7 +1074,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
     return;
   }
 
-  const long long k_req = (P.top_k < 0 || P.top_k >= V) ? -1 : P.top_k;
+  const long long k_req = k_request(P.top_k, V);
   const float u = uniforms ? uniforms[row] : 0.f;
 
   // ---- pass A (on the penalised logits v; x = v / temperature preserves
@@ -636,6 +1159,7 @@ struct Args {
   int64_t hist_len_stride;
   const float *uniforms;
   int64_t *out;
+  void *workspace;  // slice_ws_bytes(rows), or null: one workgroup per row throughout
 };
 
 template <int DT, bool VEC>
@@ -649,9 +1173,19 @@ int launch(const Args &a, int rows, hipStream_t stream) {
     if (e != hipSuccess) return fail(SPK_EHIP, "sample: %s", hipGetErrorString(e));
     attr_set = true;
   }
+  SliceWs ws{nullptr, nullptr, nullptr, nullptr};
+  if (a.workspace && VEC) {  // the sliced stage reads whole 16-byte vectors
+    ws = slice_ws(a.workspace, rows);
+    sample_slices_kernel<DT, VEC><<<rows * kSlices, kSliceThreads, 0, stream>>>(
+        a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.rep, a.presence, a.frequency, a.history,
+        a.hist_stride, a.hist_len, a.hist_len_stride, ws);
+  }
+  if (ws.count)
+    sample_finish_kernel<DT><<<rows, kThreads, 0, stream>>>(a.V, a.temperature, a.top_k, a.top_p, a.min_p, a.uniforms,
+                                                        a.out, ws);
   sample_kernel<DT, VEC><<<rows, kThreads, shm, stream>>>(
       a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.top_p, a.min_p, a.rep, a.presence,
-      a.frequency, a.history, a.hist_stride, a.hist_len, a.hist_len_stride, a.uniforms, a.out);
+      a.frequency, a.history, a.hist_stride, a.hist_len, a.hist_len_stride, a.uniforms, a.out, ws);
   return check_launch("sample");
 }
 

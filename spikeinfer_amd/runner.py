@@ -90,7 +90,7 @@ class DecodeRunner:
         # decode_advance (no torch RNG in the captured step)
         sample_tokens(logits, s.temperature[:b], s.top_k[:b], s.top_p[:b], s.min_p[:b],
                       s.repetition_penalty[:b], s.presence_penalty[:b], s.frequency_penalty[:b],
-                      self.history, self.step_count, s.uniforms[:b], s.tokens[:b])
+                      self.history, self.step_count, s.uniforms[:b], s.tokens[:b], workspace=s.workspace)
         decode_advance(s.tokens, self.input_ids, self.positions, self.seq_lens, self.slot_mapping,
                        self.block_tables, self.bs, b, self.live, self.history, self.step_count,
                        s.rng_seeds, s.uniforms)
@@ -149,7 +149,7 @@ class DecodeRunner:
         s.draw_uniforms(n)
         sample_tokens(logits, s.temperature[:n], s.top_k[:n], s.top_p[:n], s.min_p[:n],
                       s.repetition_penalty[:n], s.presence_penalty[:n], s.frequency_penalty[:n],
-                      self.history, self.step_count, s.uniforms[:n], s.tokens[:n])
+                      self.history, self.step_count, s.uniforms[:n], s.tokens[:n], workspace=s.workspace)
         decode_advance(s.tokens, self.input_ids, self.positions, self.seq_lens, self.slot_mapping,
                        self.block_tables, self.bs, self.B, self.live, self.history, self.step_count,
                        s.rng_seeds, s.uniforms)

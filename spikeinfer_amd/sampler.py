@@ -73,6 +73,7 @@ def sample_tokens(
     history_len: torch.Tensor | None = None,
     uniforms: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """One token per row of ``logits [rows, vocab]`` (fp32/bf16/fp16, row
     stride free, vocab stride 1).
@@ -82,7 +83,9 @@ def sample_tokens(
     off).  ``history`` int64 ``[rows, cap]`` holds each row's generated tokens,
     ``history_len`` int32 ``[rows]`` (or ``[1]``: one count for all rows) how
     many.  ``uniforms`` float32 ``[rows]`` in [0, 1) drive the draw.  Returns
-    ``out`` int64 ``[rows]``.
+    ``out`` int64 ``[rows]``.  ``workspace`` (uint8, at least
+    :func:`sample_workspace_bytes` ``(rows)``) lets rows with a top-k cut
+    gather their candidates over several workgroups per row (same tokens).
     """
     dev = _lib.require_gpu(logits, temperature, top_k, top_p, min_p, repetition_penalty,
                            presence_penalty, frequency_penalty, history, history_len, uniforms, out)
@@ -109,17 +112,27 @@ def sample_tokens(
         len_stride = 0 if history_len.numel() == 1 else 1
     if out is None:
         out = torch.empty(rows, dtype=torch.int64, device=dev)
+    ws_bytes = 0
+    if workspace is not None:
+        ws_bytes = workspace.numel() * workspace.element_size()
+        if not workspace.is_contiguous() or workspace.device != dev:
+            raise ValueError("workspace must be a contiguous tensor on the logits' device")
     _lib.check(
-        _lib.load().spk_sample(
+        _lib.load().spk_sample_ws(
             logits.data_ptr(), _lib.dtype_code(logits.dtype), logits.stride(0), rows, vocab,
             temperature.data_ptr(), _lib.ptr(top_k), _lib.ptr(top_p), _lib.ptr(min_p),
             _lib.ptr(repetition_penalty), _lib.ptr(presence_penalty), _lib.ptr(frequency_penalty),
             _lib.ptr(history), hist_stride, _lib.ptr(history_len), len_stride, _lib.ptr(uniforms),
-            out.data_ptr(), _lib.stream_of(dev),
+            out.data_ptr(), _lib.ptr(workspace), ws_bytes, _lib.stream_of(dev),
         ),
         "sample",
     )
     return out
+
+
+def sample_workspace_bytes(rows: int) -> int:
+    """Bytes of the :func:`sample_tokens` workspace for ``rows`` rows."""
+    return int(_lib.load().spk_sample_workspace_bytes(rows))
 
 
 class BatchSampler:
@@ -151,6 +164,8 @@ class BatchSampler:
         # per-row seeds of the device-side draws of captured steps (decode_advance)
         self.rng_seeds = torch.zeros(max_rows, dtype=torch.int64, device=self.device)
         self.tokens = torch.zeros(max_rows, dtype=torch.int64, device=self.device)
+        # candidates of the sliced top-k stage (sample_tokens' workspace)
+        self.workspace = torch.empty(sample_workspace_bytes(max_rows), dtype=torch.uint8, device=self.device)
         self.params: list[SamplingParams] = []
         self._generators: dict[int, torch.Generator] = {}
 
@@ -218,6 +233,7 @@ class BatchSampler:
             logits, self.temperature[:n], self.top_k[:n], self.top_p[:n], self.min_p[:n],
             self.repetition_penalty[:n], self.presence_penalty[:n], self.frequency_penalty[:n],
             self.history[:n], self.history_len[:n], self.uniforms[:n], self.tokens[:n],
+            workspace=self.workspace,
         )
         if record:
             self.record(n)

@@ -134,3 +134,18 @@ def test_python_api_refuses_cpu_tensors():
     with pytest.raises(ValueError, match="expected 1"):
         paged_spike_attn_decode(q, kv, kv, torch.zeros(1, 2, dtype=torch.int32),
                                 torch.ones(1, dtype=torch.int32), 32, 16, 14, 2)
+
+
+def test_sampler_workspace_size_and_validation():
+    """The sliced sampler's workspace: per row, 8 slices of 256 candidates
+    (x and index) plus a count and a maximum each; a short or misaligned one
+    is refused before anything is launched."""
+    lib = _lib.load()
+    assert lib.spk_sample_workspace_bytes(64) == 64 * 8 * (2 * 256 * 4 + 8)
+    assert lib.spk_sample_workspace_bytes(0) == 0
+    args = lambda ws, nbytes: (16, 2, 151936, 4, 151936, 16, None, None, None, None, None, None, None, 0,
+                               None, 0, None, 32, ws, nbytes, None)
+    assert lib.spk_sample_ws(*args(64, 100)) == _lib.SPK_EINVAL
+    assert b"workspace" in lib.spk_last_error()
+    assert lib.spk_sample_ws(*args(8, lib.spk_sample_workspace_bytes(4))) == _lib.SPK_EINVAL
+    assert b"aligned" in lib.spk_last_error()

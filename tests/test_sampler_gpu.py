@@ -14,12 +14,12 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from spikeinfer_amd.sampler import BatchSampler, SamplingParams, sample_tokens
+from spikeinfer_amd.sampler import BatchSampler, SamplingParams, sample_tokens, sample_workspace_bytes
 
 pytestmark = pytest.mark.gpu
 
 
-def _run(gpu, logits, params, histories, uniforms, dtype=torch.float32):
+def _run(gpu, logits, params, histories, uniforms, dtype=torch.float32, sliced=False):
     n, V = logits.shape
     lg = torch.from_numpy(logits).to(gpu, dtype)
     f = lambda k, dflt: torch.tensor([p.get(k, dflt) for p in params], dtype=torch.float32, device=gpu)
@@ -33,7 +33,8 @@ def _run(gpu, logits, params, histories, uniforms, dtype=torch.float32):
         lg, f("temperature", 1.0),
         torch.tensor([p.get("top_k", -1) for p in params], dtype=torch.int32, device=gpu),
         f("top_p", 1.0), f("min_p", 0.0), f("rep", 1.0), f("presence", 0.0), f("frequency", 0.0),
-        hist, hlen, torch.tensor(uniforms, dtype=torch.float32, device=gpu))
+        hist, hlen, torch.tensor(uniforms, dtype=torch.float32, device=gpu),
+        workspace=torch.empty(sample_workspace_bytes(n), dtype=torch.uint8, device=gpu) if sliced else None)
     return out.cpu().tolist(), lg.float().cpu().numpy()
 
 
@@ -50,9 +51,10 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("sliced", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("case", range(len(CASES)))
-def test_sampler_matches_oracle(gpu, case, dtype):
+def test_sampler_matches_oracle(gpu, case, dtype, sliced):
     rng = np.random.default_rng(case)
     rows, V = 16, 151936
     logits = (rng.standard_normal((rows, V)) * 3).astype(np.float32)
@@ -63,7 +65,7 @@ def test_sampler_matches_oracle(gpu, case, dtype):
         for t in h[:3]:
             logits[i, t] = 12.0 + rng.standard_normal()
     us = rng.random(rows).astype(np.float32).tolist()
-    got, used = _run(gpu, logits, params, histories, us, dtype)
+    got, used = _run(gpu, logits, params, histories, us, dtype, sliced)
     skipped = 0
     for i in range(rows):
         p = params[i]
@@ -86,13 +88,47 @@ def test_sampler_matches_oracle(gpu, case, dtype):
     assert skipped <= 2
 
 
+SLICED_CASES = [
+    (151936, 3.0, dict(temperature=0.8, top_k=50, top_p=0.9, rep=1.1)),
+    (151936, 3.0, dict(temperature=1.0, top_k=256, min_p=0.02, presence=0.4, frequency=0.3)),
+    (151936, 3.0, dict(temperature=1.0, top_k=257)),             # above the sliced range
+    (151936, 0.0, dict(temperature=1.0, top_k=50)),              # every logit equal: slices overflow
+    (151936, 0.02, dict(temperature=0.7, top_k=8, top_p=0.5)),   # bf16: heavy ties
+    (1000, 3.0, dict(temperature=1.0, top_k=50)),                # slices past the vocabulary are empty
+    (100, 3.0, dict(temperature=1.0, top_k=60, rep=2.0)),        # one partial slice, k near the vocabulary
+    (262144, 3.0, dict(temperature=1.2, top_k=1)),               # the largest vocabulary
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", range(len(SLICED_CASES)))
+def test_sampler_sliced_candidates_give_the_same_tokens(gpu, case, dtype):
+    """With the workspace, rows with a top-k cut take their candidates from
+    the sliced stage (or fall back to the row sweeps when a slice cannot
+    certify its set): every token equals the one-workgroup path's."""
+    V, scale, p = SLICED_CASES[case]
+    print(f"sliced sampler case {case} V={V} dtype={dtype}", flush=True)
+    rng = np.random.default_rng(100 + case)
+    rows = 24
+    logits = (rng.standard_normal((rows, V)) * scale).astype(np.float32)
+    histories = [rng.integers(0, V, size=rng.integers(0, 60)).tolist() for _ in range(rows)]
+    for i, h in enumerate(histories):
+        for t in h[:3]:
+            logits[i, t] = 10.0 + rng.standard_normal()
+    us = rng.random(rows).astype(np.float32).tolist()
+    plain, _ = _run(gpu, logits, [p] * rows, histories, us, dtype)
+    sliced, _ = _run(gpu, logits, [p] * rows, histories, us, dtype, sliced=True)
+    assert sliced == plain
+
+
 def test_sampler_ties_and_tiny_vocab(gpu):
     """bf16-style ties at the top-k cut are kept in index order."""
     logits = np.array([[1.0, 3.0, 3.0, 3.0, 0.0, 3.0]] * 4, np.float32)
     params = [dict(temperature=1.0, top_k=2)] * 4
     us = [0.0, 0.49, 0.51, 0.999]
-    got, _ = _run(gpu, logits, params, [[]] * 4, us)
-    assert got == [1, 1, 2, 2]
+    for sliced in (False, True):
+        got, _ = _run(gpu, logits, params, [[]] * 4, us, sliced=sliced)
+        assert got == [1, 1, 2, 2]
 
 
 def test_sampler_uniform_sweep_follows_closed_form(gpu):
