@@ -498,7 +498,7 @@ __device__ __forceinline__ int64_t filter_and_draw(const Src src, Shared &sh, co
 //   * with at least k of them (or the whole slice) they hold the slice's k
 //     largest: each candidate's rank among them is counted, and the first
 //     min(k, n) go to the workspace in order.
-// sample_finish_kernel merges a row's lists (ranks by binary search), which
+// The row kernel then merges a row's lists (ranks by binary search), which
 // gives the row's top-k in order, and finishes with prefix sums over it:
 // min_p, top_p and the draw are the same cuts as filter_and_draw's, computed
 // from the same fixed-point masses with the same comparisons.  A slice that
@@ -972,30 +972,6 @@ __device__ __forceinline__ int64_t sliced_finish(FinishShared &sh, const SliceWs
   return best;
 }
 
-// One workgroup per sliced row whose slices certified their lists; the row
-// kernel leaves those rows alone.  (A template only so that each logits
-// dtype's translation unit may instantiate it.)
-template <int DT>
-__global__ __launch_bounds__(kThreads) void sample_finish_kernel(int V, const float *temperature,
-                                                                 const int32_t *top_k, const float *top_p,
-                                                                 const float *min_p, const float *uniforms,
-                                                                 int64_t *out, SliceWs ws) {
-  __shared__ FinishShared sh;
-  const int row = blockIdx.x;
-  Params P;
-  P.temp = temperature[row];
-  P.top_k = top_k ? top_k[row] : -1;
-  const long long k_req = k_request(P.top_k, V);
-  if (!sliced_row(P.temp, k_req)) return;
-  int n[kSlices];
-  float mv;
-  if (!sliced_lists(ws, row, n, &mv)) return;
-  P.top_p = top_p ? top_p[row] : 1.f;
-  P.min_p = min_p ? min_p[row] : 0.f;
-  const int64_t tok = sliced_finish(sh, ws, row, P, k_req, uniforms ? uniforms[row] : 0.f, n, mv / P.temp);
-  if (threadIdx.x == 0) out[row] = tok;
-}
-
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void sample_kernel(
     const void *logits, int64_t row_stride, int V, const float *temperature,
@@ -1017,11 +993,17 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
   P.frequency = frequency ? frequency[row] : 0.f;
   P.use_hash = P.frequency != 0.f;
 
-  // ---- sliced rows whose slices certified their lists: sample_finish_kernel's
+  // ---- sliced rows whose slices certified their lists: merge and finish ------
   if (ws.count && sliced_row(P.temp, k_request(P.top_k, V))) {
     int n[kSlices];
     float mv;
-    if (sliced_lists(ws, row, n, &mv)) return;
+    if (sliced_lists(ws, row, n, &mv)) {
+      static_assert(sizeof(FinishShared) <= sizeof(Shared), "the finish reuses the row kernel's LDS");
+      const int64_t tok = sliced_finish(*reinterpret_cast<FinishShared *>(smem_raw), ws, row, P,
+                                        k_request(P.top_k, V), uniforms ? uniforms[row] : 0.f, n, mv / P.temp);
+      if (tid == 0) out[row] = tok;
+      return;
+    }
   }
 
   // ---- history -> seen bitmap (+ counts) ------------------------------------
@@ -1180,9 +1162,6 @@ int launch(const Args &a, int rows, hipStream_t stream) {
         a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.rep, a.presence, a.frequency, a.history,
         a.hist_stride, a.hist_len, a.hist_len_stride, ws);
   }
-  if (ws.count)
-    sample_finish_kernel<DT><<<rows, kThreads, 0, stream>>>(a.V, a.temperature, a.top_k, a.top_p, a.min_p, a.uniforms,
-                                                        a.out, ws);
   sample_kernel<DT, VEC><<<rows, kThreads, shm, stream>>>(
       a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.top_p, a.min_p, a.rep, a.presence,
       a.frequency, a.history, a.hist_stride, a.hist_len, a.hist_len_stride, a.uniforms, a.out, ws);
