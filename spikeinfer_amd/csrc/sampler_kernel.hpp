@@ -644,7 +644,7 @@ struct SliceRegs {
   }
 };
 
-template <int DT, bool VEC>
+template <int DT>
 __global__ __launch_bounds__(kSliceThreads) void sample_slices_kernel(
     const void *logits, int64_t row_stride, int V, const float *temperature, const int32_t *top_k,
     const float *rep, const float *presence, const float *frequency, const int64_t *history,
@@ -1156,11 +1156,13 @@ int launch(const Args &a, int rows, hipStream_t stream) {
     attr_set = true;
   }
   SliceWs ws{nullptr, nullptr, nullptr, nullptr};
-  if (a.workspace && VEC) {  // the sliced stage reads whole 16-byte vectors
-    ws = slice_ws(a.workspace, rows);
-    sample_slices_kernel<DT, VEC><<<rows * kSlices, kSliceThreads, 0, stream>>>(
-        a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.rep, a.presence, a.frequency, a.history,
-        a.hist_stride, a.hist_len, a.hist_len_stride, ws);
+  if constexpr (VEC) {  // the sliced stage reads whole 16-byte vectors: aligned rows only
+    if (a.workspace) {
+      ws = slice_ws(a.workspace, rows);
+      sample_slices_kernel<DT><<<rows * kSlices, kSliceThreads, 0, stream>>>(
+          a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.rep, a.presence, a.frequency, a.history,
+          a.hist_stride, a.hist_len, a.hist_len_stride, ws);
+    }
   }
   sample_kernel<DT, VEC><<<rows, kThreads, shm, stream>>>(
       a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.top_p, a.min_p, a.rep, a.presence,

@@ -121,6 +121,22 @@ def test_sampler_sliced_candidates_give_the_same_tokens(gpu, case, dtype):
     assert sliced == plain
 
 
+def test_sampler_workspace_with_unaligned_rows_takes_the_row_path(gpu):
+    """Rows whose stride is not a whole number of 16-byte vectors cannot be
+    sliced: with a workspace they take the one-workgroup path, same tokens."""
+    g = torch.Generator(device=gpu).manual_seed(3)
+    wide = torch.randn((12, 1001), generator=g, device=gpu) * 2
+    lg = wide[:, :1000]  # row stride 1001 floats
+    rows = lg.shape[0]
+    t = torch.full((rows,), 0.9, device=gpu)
+    k = torch.full((rows,), 20, dtype=torch.int32, device=gpu)
+    u = torch.rand(rows, generator=g, device=gpu)
+    plain = sample_tokens(lg, t, k, uniforms=u)
+    ws = torch.empty(sample_workspace_bytes(rows), dtype=torch.uint8, device=gpu)
+    sliced = sample_tokens(lg, t, k, uniforms=u, workspace=ws)
+    assert torch.equal(plain, sliced)
+
+
 def test_sampler_ties_and_tiny_vocab(gpu):
     """bf16-style ties at the top-k cut are kept in index order."""
     logits = np.array([[1.0, 3.0, 3.0, 3.0, 0.0, 3.0]] * 4, np.float32)
