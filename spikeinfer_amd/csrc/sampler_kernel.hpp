@@ -489,7 +489,7 @@ __device__ __forceinline__ int64_t filter_and_draw(const Src src, Shared &sh, co
 // kSlices slices, one workgroup each (sample_slices_kernel):
 //   * the slice goes into registers once, with the penalties, as keys of the
 //     penalised values v; every kSampleStride-th one is a sample;
-//   * the r-th largest sample (r = k / kSampleStride + 2, doubled while the
+//   * the r-th largest sample (r = k / kSampleStride + 3, doubled while the
 //     candidates fall short) fixes a bound x_B on x = v / temperature, turned
 //     once into the smallest v key whose x reaches x_B (a bisection over keys,
 //     x monotone in v), so the passes compare keys and divide only the
@@ -721,7 +721,7 @@ __global__ __launch_bounds__(kSliceThreads) void sample_slices_kernel(
   // slice not exhausted): r doubles and the registers are counted again. ----
   const int n_s = (c1 - c0 + kSampleStride - 1) / kSampleStride;
   const long long kk = (k_req + kSampleStride - 1) / kSampleStride;
-  int r = static_cast<int>(min<long long>(n_s, kk + 2));
+  int r = static_cast<int>(min<long long>(n_s, kk + 3));
   uint32_t n = 0, mine = 0, incl = 0, bound = 0;
   while (true) {
     if (wave == 0) {
@@ -749,13 +749,17 @@ __global__ __launch_bounds__(kSliceThreads) void sample_slices_kernel(
         }
       }
       // The smallest key k in (0, best] with unkey(k) / temp >= unkey(best) /
-      // temp (key 0 is a NaN's: never).
+      // temp (key 0 is a NaN's: never): 64 keys tested a round, one a lane.
       const float xb = unkey(best) / P.temp;
       uint32_t lo = 0, hi = best;
       while (hi - lo > 1) {
-        const uint32_t mid = lo + (hi - lo) / 2;
-        if (unkey(mid) / P.temp >= xb) hi = mid;
-        else lo = mid;
+        const uint32_t step = (hi - lo + 63) / 64;
+        const uint32_t k = min(hi, lo + step * static_cast<uint32_t>(lane + 1));
+        const unsigned long long t = __ballot(unkey(k) / P.temp >= xb);  // lane 63 tests hi
+        if (t == 0) break;  // only with a NaN bound: keep hi
+        const int first = static_cast<int>(__builtin_ctzll(t));
+        hi = min(hi, lo + step * static_cast<uint32_t>(first + 1));
+        lo = first == 0 ? lo : lo + step * static_cast<uint32_t>(first);
       }
       if (lane == 0) sh.bound = r > n_s ? 0u : hi;  // r past the samples: every element
     }
