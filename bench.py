@@ -489,8 +489,10 @@ def bench_decode_step(steps, warmup, dev, batch=64, out_tokens=64):
     # The timed run: a fresh prefill (untimed, it samples output token 1),
     # then exactly out_tokens - 1 replays of the captured step for tokens
     # 2 .. out_tokens.
+    t0 = time.perf_counter()
     runner.start(prompts, params, shuffle_blocks=5002)
     torch.cuda.synchronize()
+    prefill_warm_s = time.perf_counter() - t0
     stream = torch.cuda.current_stream(dev)
     ms = time_calls(lambda: runner.replay(1), out_tokens - 1, 0, stream)
     toks = runner.history[:B, :out_tokens]
@@ -500,7 +502,8 @@ def bench_decode_step(steps, warmup, dev, batch=64, out_tokens=64):
         "ms_per_step": round(ms, 4),
         "weight_gbs": round(model.weight_bytes / ms / 1e6, 1),
         "weight_bytes_per_step": model.weight_bytes,
-        "prefill_s_eager": round(prefill_s, 3),
+        "prefill_s_eager": round(prefill_s, 3),  # first call: includes library warm-up
+        "prefill_s_eager_warm": round(prefill_warm_s, 4),
         "batch": B, "prompt_len": plen, "T": cfg.T,
         "sampling": "temperature 0.8, top_k 50, top_p 0.9, repetition 1.1 (on device)",
         "distinct_tokens": int(torch.unique(toks).numel()),
