@@ -586,8 +586,8 @@ struct SliceShared {
 // of the slice's whole vectors (elements v * W ..), every load issued at once
 // (vectors past them re-read the first and are dropped), plus one of the < W
 // trailing elements.  After pass A it holds the keys of the penalised
-// logits, so later passes only compare keys.  Needs 16-byte aligned rows (the
-// host checks).
+// logits, so later passes only compare keys.  No load leaves the slice.
+// Needs 16-byte aligned rows (the host checks).
 template <int DT>
 struct SliceRegs {
   typedef typename Elem<DT>::T E;
@@ -603,10 +603,12 @@ struct SliceRegs {
   __device__ __forceinline__ void load(const E *row, int c0, int n) {
     const Vec *pv = reinterpret_cast<const Vec *>(row + c0);
     nv = n / W;
+    if (nv > 0) {  // (a slice of fewer than W elements has no whole vector to re-read)
 #pragma unroll
-    for (int q = 0; q < kVecs; ++q) {
-      const int v = threadIdx.x + q * kSliceThreads;
-      a[q] = pv[v < nv ? v : 0];
+      for (int q = 0; q < kVecs; ++q) {
+        const int v = threadIdx.x + q * kSliceThreads;
+        a[q] = pv[v < nv ? v : 0];
+      }
     }
     const int t = nv * W + static_cast<int>(threadIdx.x);
     tail_valid = t < n;

@@ -137,6 +137,25 @@ def test_sampler_workspace_with_unaligned_rows_takes_the_row_path(gpu):
     assert torch.equal(plain, sliced)
 
 
+def test_sampler_slices_never_read_past_the_row(gpu):
+    """A last slice with fewer elements than one 16-byte vector (bf16 V = 515:
+    slices of 256, 256 and 3; fp32 V = 258: 256 and 2), aligned rows (so the
+    sliced path runs) and a last row that ends its allocation: the sliced and
+    one-workgroup paths agree."""
+    for V, stride, dt in ((515, 520, torch.bfloat16), (258, 260, torch.float32)):
+        g = torch.Generator(device=gpu).manual_seed(V)
+        rows = 6
+        flat = (torch.randn((rows - 1) * stride + V, generator=g, device=gpu) * 2).to(dt)
+        lg = flat.as_strided((rows, V), (stride, 1))
+        t = torch.full((rows,), 1.0, device=gpu)
+        k = torch.full((rows,), 5, dtype=torch.int32, device=gpu)
+        u = torch.rand(rows, generator=g, device=gpu)
+        plain = sample_tokens(lg, t, k, uniforms=u)
+        ws = torch.empty(sample_workspace_bytes(rows), dtype=torch.uint8, device=gpu)
+        sliced = sample_tokens(lg, t, k, uniforms=u, workspace=ws)
+        assert torch.equal(plain, sliced), (V, dt)
+
+
 def test_sampler_ties_and_tiny_vocab(gpu):
     """bf16-style ties at the top-k cut are kept in index order."""
     logits = np.array([[1.0, 3.0, 3.0, 3.0, 0.0, 3.0]] * 4, np.float32)
