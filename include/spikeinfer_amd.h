@@ -498,12 +498,25 @@ size_t spk_sample_shared_bytes(void);
 /*
  * spk_sample with a device workspace (spk_sample_workspace_bytes(rows) bytes,
  * 16-byte aligned; no counterpart in the reference, whose sampler is torch
- * ops).  Rows with a top-k cut (0 < top_k <= 256, temperature >= 1e-5) are
- * first cut into 8 slices of the vocabulary, one workgroup each, which hand
- * the row workgroup a candidate set holding the row's top_k largest; the
- * tokens are those spk_sample returns.  A NULL workspace is spk_sample.
- * Calls sharing a workspace must be ordered (one stream).
+ * ops).  `stages` picks the sliced stages, which cut a row into 8 slices of
+ * the vocabulary, one workgroup each:
+ *   SPK_SAMPLE_STAGE_TOPK: rows with a top-k cut (0 < top_k <= 256,
+ *     temperature >= 1e-5); the slices hand the row workgroup a candidate set
+ *     holding the row's top_k largest;
+ *   SPK_SAMPLE_STAGE_OPEN: rows with no top-k cut (top_k < 0 or >= vocab,
+ *     temperature >= 1e-5) and a top-p or min-p cut (top_p < 1 or
+ *     min_p > 0); two launches give the row maximum, then each slice's 64
+ *     largest and its exact share of the row's probability mass,
+ *     which decide the row when its top-p cut and draw fall inside the
+ *     certified prefix of the merged lists (else the row workgroup takes the
+ *     whole row).
+ * The tokens are those spk_sample returns whatever the stages; a stage only
+ * pays off when the batch holds rows of its kind (each costs launches).  A
+ * NULL workspace or stages 0 is spk_sample.  Calls sharing a workspace must
+ * be ordered (one stream).
  */
+#define SPK_SAMPLE_STAGE_TOPK 1
+#define SPK_SAMPLE_STAGE_OPEN 2
 size_t spk_sample_workspace_bytes(int rows);
 int spk_sample_ws(const void *logits, int logits_dtype, int64_t row_stride, int rows, int vocab,
                   const float *temperature, const int32_t *top_k, const float *top_p,
@@ -511,7 +524,7 @@ int spk_sample_ws(const void *logits, int logits_dtype, int64_t row_stride, int 
                   const float *presence_penalty, const float *frequency_penalty,
                   const int64_t *history, int64_t history_stride, const int32_t *history_len,
                   int64_t history_len_stride, const float *uniforms, int64_t *out_tokens,
-                  void *workspace, size_t workspace_bytes, void *stream);
+                  void *workspace, size_t workspace_bytes, int stages, void *stream);
 
 
 

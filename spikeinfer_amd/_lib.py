@@ -112,7 +112,7 @@ _SIGNATURES = {
     "spk_sample_workspace_bytes": (_sz, [_i32]),
     "spk_sample_ws": (_i32, [
         _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
-        _vp, _vp, _vp, _sz, _vp]),
+        _vp, _vp, _vp, _sz, _i32, _vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -26,7 +26,7 @@ extern "C" int spk_sample_ws(const void *logits, int logits_dtype, int64_t row_s
                              const float *presence_penalty, const float *frequency_penalty,
                              const int64_t *history, int64_t history_stride, const int32_t *history_len,
                              int64_t history_len_stride, const float *uniforms, int64_t *out_tokens,
-                             void *workspace, size_t workspace_bytes, void *stream) {
+                             void *workspace, size_t workspace_bytes, int stages, void *stream) {
   if (!valid_float_dtype(logits_dtype))
     return fail(SPK_EINVAL, "sample: logits dtype %d is not a float type", logits_dtype);
   if (!logits || !temperature || !out_tokens) return fail(SPK_EINVAL, "sample: null pointer");
@@ -35,6 +35,8 @@ extern "C" int spk_sample_ws(const void *logits, int logits_dtype, int64_t row_s
                 smp::kMaxVocab);
   if (history && (!history_len || history_stride < 1))
     return fail(SPK_EINVAL, "sample: history needs history_len and a row stride >= 1");
+  if (stages & ~(SPK_SAMPLE_STAGE_TOPK | SPK_SAMPLE_STAGE_OPEN))
+    return fail(SPK_EINVAL, "sample: unknown stage bits %d", stages);
   if (rows == 0) return SPK_OK;
   if (workspace && workspace_bytes < smp::slice_ws_bytes(rows))
     return fail(SPK_EINVAL, "sample: workspace of %zu bytes, %zu needed for %d rows", workspace_bytes,
@@ -43,7 +45,7 @@ extern "C" int spk_sample_ws(const void *logits, int logits_dtype, int64_t row_s
     return fail(SPK_EINVAL, "sample: workspace must be 16-byte aligned");
   smp::Args a{logits, row_stride, vocab, temperature, top_k, top_p, min_p, repetition_penalty,
               presence_penalty, frequency_penalty, history, history_stride, history_len,
-              history_len_stride, uniforms, out_tokens, workspace};
+              history_len_stride, uniforms, out_tokens, workspace, stages};
   const size_t esz = logits_dtype == SPK_F32 ? 4 : 2;
   const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (row_stride * esz) % 16 == 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -63,5 +65,5 @@ extern "C" int spk_sample(const void *logits, int logits_dtype, int64_t row_stri
                           void *stream) {
   return spk_sample_ws(logits, logits_dtype, row_stride, rows, vocab, temperature, top_k, top_p, min_p,
                        repetition_penalty, presence_penalty, frequency_penalty, history, history_stride,
-                       history_len, history_len_stride, uniforms, out_tokens, nullptr, 0, stream);
+                       history_len, history_len_stride, uniforms, out_tokens, nullptr, 0, 0, stream);
 }

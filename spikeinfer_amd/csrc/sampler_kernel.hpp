@@ -185,9 +185,11 @@ __device__ __forceinline__ void select_bin(Shared &sh, unsigned long long base, 
   __syncthreads();
 }
 
-__device__ __forceinline__ unsigned long long mass_of(float x, float m) {
-  return static_cast<unsigned long long>(static_cast<double>(expf(x - m)) * kMassScale);
+// Fixed-point mass of a weight e = exp(x - m): e * 2^40, truncated.
+__device__ __forceinline__ unsigned long long mass_of_e(float e) {
+  return static_cast<unsigned long long>(static_cast<double>(e) * kMassScale);
 }
+__device__ __forceinline__ unsigned long long mass_of(float x, float m) { return mass_of_e(expf(x - m)); }
 
 __device__ __forceinline__ void zero_hist(Shared &sh) {
   __syncthreads();
@@ -529,15 +531,17 @@ __device__ __forceinline__ unsigned long long order_key(float x, int i) {
 }
 
 // Workspace: x [rows][kSlices][kFastMaxK] float, index the same in int32,
-// then count [rows][kSlices] int32 and maximum v [rows][kSlices] float.
+// then count [rows][kSlices] int32, maximum v [rows][kSlices] float and the
+// open rows' alive mass [rows][kSlices] uint64.
 struct SliceWs {
   float *x;
   int32_t *idx;
   int32_t *count;
   float *vmax;
+  unsigned long long *zpart;
 };
 __host__ __device__ inline size_t slice_ws_bytes(int rows) {
-  return static_cast<size_t>(rows) * kSlices * (2 * kFastMaxK * 4 + 8);
+  return static_cast<size_t>(rows) * kSlices * (2 * kFastMaxK * 4 + 16);
 }
 __host__ __device__ inline SliceWs slice_ws(void *base, int rows) {
   char *b = static_cast<char *>(base);
@@ -547,7 +551,27 @@ __host__ __device__ inline SliceWs slice_ws(void *base, int rows) {
   w.idx = reinterpret_cast<int32_t *>(b + n * kFastMaxK * 4);
   w.count = reinterpret_cast<int32_t *>(b + 2 * n * kFastMaxK * 4);
   w.vmax = reinterpret_cast<float *>(b + 2 * n * kFastMaxK * 4 + n * 4);
+  w.zpart = reinterpret_cast<unsigned long long *>(b + 2 * n * kFastMaxK * 4 + n * 8);
   return w;
+}
+
+// Stages a call may run (the caller's `stages` bits): the top-k stage for rows
+// with 0 < top_k <= kFastMaxK, the open stage for rows with no top-k cut and
+// a top-p or min-p cut (open_row).
+constexpr int kStageTopK = 1;
+constexpr int kStageOpen = 2;
+// Launch modes of sample_slices_kernel.
+constexpr int kModeTopK = 0;     // top-k rows: list of the slice's k largest
+constexpr int kModeOpenMax = 1;  // open rows: the slice's largest penalised logit only
+constexpr int kModeOpen = 2;     // open rows: list of the slice's kOpenK largest + alive mass
+// An open row's slices list their kOpenK largest: the merged lists then
+// certify about the row's first 400 (the largest of the slices' 64th keys).
+constexpr int kOpenK = 64;
+// Open rows the stage takes: sampled, no top-k cut, and a top-p or min-p cut
+// (a draw over the whole mass lands past the certified prefix too often, and
+// one such row sends the batch's slowest workgroup down the whole row).
+__device__ __forceinline__ bool open_row(float temp, long long k_req, float top_p, float min_p) {
+  return !(temp < kGreedyTemp) && k_req <= 0 && (top_p < 1.f || min_p > 0.f);
 }
 
 // Maximum over the wave (DPP within rows of 16, then the four rows).
@@ -579,6 +603,7 @@ struct SliceShared {
   unsigned long long cand[kSliceCand + 16];  // candidates' order keys (+ a zero batch)
   float fmax[kSliceThreads / 64];
   uint32_t wcount[kSliceThreads / 64];
+  unsigned long long zw[kSliceThreads / 64];
   uint32_t bound;
 };
 
@@ -646,11 +671,12 @@ struct SliceRegs {
   }
 };
 
-template <int DT>
+template <int DT, int MODE>
 __global__ __launch_bounds__(kSliceThreads) void sample_slices_kernel(
     const void *logits, int64_t row_stride, int V, const float *temperature, const int32_t *top_k,
-    const float *rep, const float *presence, const float *frequency, const int64_t *history,
-    int64_t hist_stride, const int32_t *hist_len, int64_t hist_len_stride, SliceWs ws) {
+    const float *top_p, const float *min_p, const float *rep, const float *presence,
+    const float *frequency, const int64_t *history, int64_t hist_stride, const int32_t *hist_len,
+    int64_t hist_len_stride, SliceWs ws) {
   typedef typename Elem<DT>::T E;
   __shared__ SliceShared sh;
   const int row = blockIdx.x / kSlices, sl = blockIdx.x % kSlices;
@@ -662,18 +688,30 @@ __global__ __launch_bounds__(kSliceThreads) void sample_slices_kernel(
   P.presence = presence ? presence[row] : 0.f;
   P.frequency = frequency ? frequency[row] : 0.f;
   P.use_hash = P.frequency != 0.f;
-  P.top_p = 1.f;
-  P.min_p = 0.f;
-  const long long k_req = k_request(P.top_k, V);
-  if (!sliced_row(P.temp, k_req)) return;  // the row workgroup does not read this slice
+  P.top_p = MODE != kModeTopK && top_p ? top_p[row] : 1.f;
+  P.min_p = MODE != kModeTopK && min_p ? min_p[row] : 0.f;
+  const long long k_row = k_request(P.top_k, V);
+  if (MODE == kModeTopK ? !sliced_row(P.temp, k_row) : !open_row(P.temp, k_row, P.top_p, P.min_p))
+    return;  // the row workgroup does not read this slice
+  const long long k_req = MODE == kModeTopK ? k_row : static_cast<long long>(kOpenK);
   const int64_t ws_i = static_cast<int64_t>(row) * kSlices + sl;
   const int L = slice_len(V), c0 = sl * L, c1 = min(V, c0 + L);
   if (c0 >= c1) {
     if (tid == 0) {
-      ws.count[ws_i] = 0;
-      ws.vmax[ws_i] = -INFINITY;
+      if (MODE != kModeOpenMax) ws.count[ws_i] = 0;
+      if (MODE != kModeOpen) ws.vmax[ws_i] = -INFINITY;
+      if (MODE == kModeOpen) ws.zpart[ws_i] = 0ull;
     }
     return;
+  }
+  // Open rows: the row's largest penalised logit, from the max-only launch
+  // before this one (vector loads, not the scalar cache).
+  float m_row = -INFINITY;
+  if (MODE == kModeOpen) {
+#pragma unroll
+    for (int s2 = 0; s2 < kSlices; ++s2)
+      m_row = fmaxf(m_row, __hip_atomic_load(ws.vmax + static_cast<int64_t>(row) * kSlices + s2,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
   }
   SliceRegs<DT> rg;  // the slice's logits, loaded while the history is read
   rg.load(reinterpret_cast<const E *>(logits) + row * row_stride, c0, c1 - c0);
@@ -710,12 +748,20 @@ __global__ __launch_bounds__(kSliceThreads) void sample_slices_kernel(
   float mv = -INFINITY;
   rg.penalise_all(c0, P, sh, has_hist, [&](int b, float v) {
     mv = fmaxf(mv, v);
-    if ((b % kSampleStride) == 0) sh.samp[b / kSampleStride] = fkey(v);
+    if (MODE != kModeOpenMax && (b % kSampleStride) == 0) sh.samp[b / kSampleStride] = fkey(v);
   });
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) mv = fmaxf(mv, __shfl_xor(mv, d));
   if (lane == 0) sh.fmax[wave] = mv;
   __syncthreads();
+  if constexpr (MODE == kModeOpenMax) {
+    if (tid == 0) {
+      float m = sh.fmax[0];
+      for (int w = 1; w < kSliceThreads / 64; ++w) m = fmaxf(m, sh.fmax[w]);
+      ws.vmax[ws_i] = m;
+    }
+    return;
+  }
 
   // ---- bound and candidates.  Wave 0 takes the r-th largest sample, then
   // the smallest v key whose x reaches that sample's x; every thread counts
@@ -823,19 +869,53 @@ __global__ __launch_bounds__(kSliceThreads) void sample_slices_kernel(
       }
     }
   }
-  if (tid == 0) {
-    ws.count[ws_i] = ok ? nk : -1;
-    float m = sh.fmax[0];
-    for (int w = 1; w < kSliceThreads / 64; ++w) m = fmaxf(m, sh.fmax[w]);
-    ws.vmax[ws_i] = m;
+  if constexpr (MODE == kModeOpen) {
+    // The slice's share of the row's alive mass, element for element the sum
+    // the one-workgroup path forms (x = v / temperature, the same min_p test
+    // and fixed-point mass against the row's largest x); integer sums, so the
+    // row's total is exact whatever the order.
+    const float m = m_row / P.temp;
+    unsigned long long z = 0;
+#pragma unroll
+    for (int q = 0; q <= SliceRegs<DT>::kVecs * SliceRegs<DT>::W; ++q) {
+      if (!rg.valid(q)) continue;
+      const float x = unkey(rg.key[q]) / P.temp;
+      const float e = expf(x - m);
+      if (P.min_p <= 0.f || e >= P.min_p) z += mass_of_e(e);
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+      const uint32_t lo = __shfl_xor(static_cast<uint32_t>(z), d);
+      const uint32_t hi = __shfl_xor(static_cast<uint32_t>(z >> 32), d);
+      z += (static_cast<unsigned long long>(hi) << 32) | lo;
+    }
+    if (lane == 0) sh.zw[wave] = z;
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long zs = 0;
+      for (int w = 0; w < kSliceThreads / 64; ++w) zs += sh.zw[w];
+      ws.zpart[ws_i] = zs;
+      ws.count[ws_i] = ok ? nk : -1;
+    }
+  } else {
+    if (tid == 0) {
+      ws.count[ws_i] = ok ? nk : -1;
+      float m = sh.fmax[0];
+      for (int w = 1; w < kSliceThreads / 64; ++w) m = fmaxf(m, sh.fmax[w]);
+      ws.vmax[ws_i] = m;
+    }
   }
 }
 
+// Merged positions the finish holds (one a thread).
+constexpr int kOpenPrefix = kThreads;
+static_assert(kSlices * kOpenK <= kOpenPrefix, "an open row's merged lists fit the finish");
+
 struct FinishShared {
   unsigned long long lists[kSlices * kFastMaxK];  // the slices' lists as order keys
-  float cx[kFastMaxK];                            // the merged top-k, in order
-  int32_t ci[kFastMaxK];
-  unsigned long long cums[kFastMaxK + 1];         // kept mass before each position
+  float cx[kOpenPrefix];                          // the merged prefix, in order
+  int32_t ci[kOpenPrefix];
+  unsigned long long cums[kOpenPrefix + 1];       // kept mass before each position
   unsigned long long wsum[kWaves];
   unsigned long long bcast[4];
 };
@@ -860,8 +940,20 @@ __device__ __forceinline__ bool sliced_lists(const SliceWs &ws, int row, int (&n
 
 // The row's sliced finish (see above): the merged top-k in sh.cx / sh.ci, in
 // order, then min_p, top_p and the draw as filter_and_draw makes them.
+//
+// Open rows (no top-k cut; `open`): every slice listed its kOpenK largest,
+// so the merged lists are the row's order up to the first element any slice
+// left out.  The certified prefix is every element whose key is above the
+// last listed key of each slice that listed fewer than all its elements
+// (whole key groups only, since ties are ordered by index).  min_p keeps a prefix of it; the top-p target is
+// top_p of the whole row's alive mass (the slices' exact partial sums), and
+// the draw is over the top-p prefix or, without a top-p cut, over that whole
+// mass.  A cut or a draw past the certified prefix returns -1: the caller
+// then takes the row through the one-workgroup path.  Every kept decision is
+// the one the whole-row computation makes.
 __device__ __forceinline__ int64_t sliced_finish(FinishShared &sh, const SliceWs &ws, int row, const Params &P,
-                                                 long long k_req, float u, const int (&n)[kSlices], float m) {
+                                                 long long k_req, float u, const int (&n)[kSlices], float m,
+                                                 bool open, int V) {
   const int tid = threadIdx.x;
   // Merge: element j of slice s goes to position j + (number of elements of
   // the other slices earlier in the order), found by binary search in each
@@ -876,7 +968,7 @@ __device__ __forceinline__ int64_t sliced_finish(FinishShared &sh, const SliceWs
     total += n[s];
   }
   __syncthreads();
-  const int kept_k = static_cast<int>(min<long long>(k_req, total));
+  const int kept_k = open ? total : static_cast<int>(min<long long>(k_req, total));
   for (int e = tid; e < total; e += kThreads) {  // element e of the lists, concatenated
     int s = 0, j = e, before = 0;  // (list, position) of e; n[] indexed by constants only
 #pragma unroll
@@ -906,10 +998,29 @@ __device__ __forceinline__ int64_t sliced_finish(FinishShared &sh, const SliceWs
     }
   }
   __syncthreads();
-  // Per position j < kept_k (one thread each; kept_k <= kFastMaxK < kThreads).
+  // Open rows: keys above `cut` (when has_cut) are certified.
+  bool has_cut = false;
+  uint32_t cut = 0;
+  unsigned long long Z_all = 0;
+  if (open) {
+    const int L = slice_len(V);
+#pragma unroll
+    for (int t = 0; t < kSlices; ++t) {
+      const int len_t = max(0, min(V, (t + 1) * L) - t * L);
+      if (n[t] < len_t) {  // (an empty list of a non-empty slice certifies nothing)
+        const uint32_t kt = n[t] > 0 ? static_cast<uint32_t>(lists[t * kFastMaxK + n[t] - 1] >> 32) : 0xffffffffu;
+        cut = has_cut ? max(cut, kt) : kt;
+        has_cut = true;
+      }
+      Z_all += __hip_atomic_load(ws.zpart + static_cast<int64_t>(row) * kSlices + t, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // Per position j < kept_k (one thread each; kept_k <= kOpenPrefix = kThreads).
   const int j = tid;
-  const bool live = j < kept_k;
-  const float x = live ? sh.cx[j] : 0.f;
+  const float x0 = j < kept_k ? sh.cx[j] : 0.f;
+  const bool live = j < kept_k && !(has_cut && fkey(x0) <= cut);
+  const float x = live ? x0 : 0.f;
   const uint32_t key = fkey(x);
   const bool alive = live && (P.min_p <= 0.f || expf(x - m) >= P.min_p);
   // The alive elements are a prefix; the top-k cut keeps the first min(k, alive).
@@ -931,7 +1042,7 @@ __device__ __forceinline__ int64_t sliced_finish(FinishShared &sh, const SliceWs
   // first element of each group tests its group), then j ties of it.
   int n2 = n1;
   if (P.top_p < 1.f) {
-    const double target = static_cast<double>(P.top_p) * static_cast<double>(Z);
+    const double target = static_cast<double>(P.top_p) * static_cast<double>(open ? Z_all : Z);
     if (tid == 0) sh.bcast[2] = 0;
     __syncthreads();
     if (in1 && gs == j) {
@@ -949,11 +1060,14 @@ __device__ __forceinline__ int64_t sliced_finish(FinishShared &sh, const SliceWs
       }
     }
     __syncthreads();
-    if (sh.bcast[2]) n2 = static_cast<int>(sh.bcast[0]);
+    const bool found = sh.bcast[2] != 0;
+    if (found) n2 = static_cast<int>(sh.bcast[0]);
     __syncthreads();
+    if (open && !found) return -1;  // the cut lies past the certified prefix
   }
-  // Draw: the element whose interval of the kept mass holds u * total.
-  const unsigned long long Wtot = cums[n2];
+  // Draw: the element whose interval of the kept mass holds u * total (an
+  // open row without a top-p cut: the whole row's alive mass).
+  const unsigned long long Wtot = open && !(P.top_p < 1.f) ? Z_all : cums[n2];
   unsigned long long T = static_cast<unsigned long long>(static_cast<double>(u) * static_cast<double>(Wtot));
   if (T >= Wtot) T = Wtot ? Wtot - 1 : 0;
   const double target = static_cast<double>(T) + 1.0;
@@ -971,6 +1085,7 @@ __device__ __forceinline__ int64_t sliced_finish(FinishShared &sh, const SliceWs
   }
   __syncthreads();
   if (sh.bcast[2]) return static_cast<int64_t>(sh.bcast[0]);
+  if (open && !(P.top_p < 1.f)) return -1;  // the draw lies past the certified prefix
   // No interval holds it (not reached: the first kept element weighs 2^40):
   // the smallest kept index.
   int best = 0x7fffffff;
@@ -983,7 +1098,8 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
     const void *logits, int64_t row_stride, int V, const float *temperature,
     const int32_t *top_k, const float *top_p, const float *min_p, const float *rep,
     const float *presence, const float *frequency, const int64_t *history, int64_t hist_stride,
-    const int32_t *hist_len, int64_t hist_len_stride, const float *uniforms, int64_t *out, SliceWs ws) {
+    const int32_t *hist_len, int64_t hist_len_stride, const float *uniforms, int64_t *out, SliceWs ws,
+    int stages) {
   typedef typename Elem<DT>::T E;
   extern __shared__ __align__(16) char smem_raw[];
   Shared &sh = *reinterpret_cast<Shared *>(smem_raw);
@@ -1000,15 +1116,23 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
   P.use_hash = P.frequency != 0.f;
 
   // ---- sliced rows whose slices certified their lists: merge and finish ------
-  if (ws.count && sliced_row(P.temp, k_request(P.top_k, V))) {
+  // (an open row's finish may leave the row undecided: then the row takes the
+  // one-workgroup path below)
+  const bool topk_s = (stages & kStageTopK) && sliced_row(P.temp, k_request(P.top_k, V));
+  const bool open_s = (stages & kStageOpen) && open_row(P.temp, k_request(P.top_k, V), P.top_p, P.min_p);
+  if (ws.count && (topk_s || open_s)) {
     int n[kSlices];
     float mv;
     if (sliced_lists(ws, row, n, &mv)) {
       static_assert(sizeof(FinishShared) <= sizeof(Shared), "the finish reuses the row kernel's LDS");
       const int64_t tok = sliced_finish(*reinterpret_cast<FinishShared *>(smem_raw), ws, row, P,
-                                        k_request(P.top_k, V), uniforms ? uniforms[row] : 0.f, n, mv / P.temp);
-      if (tid == 0) out[row] = tok;
-      return;
+                                        k_request(P.top_k, V), uniforms ? uniforms[row] : 0.f, n, mv / P.temp,
+                                        open_s, V);
+      if (tok >= 0) {
+        if (tid == 0) out[row] = tok;
+        return;
+      }
+      __syncthreads();  // the one-workgroup path reuses the LDS
     }
   }
 
@@ -1108,8 +1232,8 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
     unsigned long long z = 0;
     g.each_pen([&](int i, float v) {
       if (sum_alive) {
-        const float x = v / P.temp;
-        if (P.min_p <= 0.f || expf(x - m) >= P.min_p) z += mass_of(x, m);
+        const float e = expf(v / P.temp - m);
+        if (P.min_p <= 0.f || e >= P.min_p) z += mass_of_e(e);
       }
       if (fkey(v) < L) return;
       const unsigned long long o = atomicAdd(&sh.bcast[3], 1ull);
@@ -1148,6 +1272,7 @@ struct Args {
   const float *uniforms;
   int64_t *out;
   void *workspace;  // slice_ws_bytes(rows), or null: one workgroup per row throughout
+  int stages;       // kStageTopK | kStageOpen: the sliced stages to run (with a workspace)
 };
 
 template <int DT, bool VEC>
@@ -1161,18 +1286,29 @@ int launch(const Args &a, int rows, hipStream_t stream) {
     if (e != hipSuccess) return fail(SPK_EHIP, "sample: %s", hipGetErrorString(e));
     attr_set = true;
   }
-  SliceWs ws{nullptr, nullptr, nullptr, nullptr};
-  if constexpr (VEC) {  // the sliced stage reads whole 16-byte vectors: aligned rows only
-    if (a.workspace) {
+  SliceWs ws{nullptr, nullptr, nullptr, nullptr, nullptr};
+  int stages = 0;
+  if constexpr (VEC) {  // the sliced stages read whole 16-byte vectors: aligned rows only
+    if (a.workspace && a.stages) {
       ws = slice_ws(a.workspace, rows);
-      sample_slices_kernel<DT><<<rows * kSlices, kSliceThreads, 0, stream>>>(
-          a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.rep, a.presence, a.frequency, a.history,
-          a.hist_stride, a.hist_len, a.hist_len_stride, ws);
+      stages = a.stages;
+      if (stages & kStageOpen) {  // the row maxima, then the lists and masses
+        sample_slices_kernel<DT, kModeOpenMax><<<rows * kSlices, kSliceThreads, 0, stream>>>(
+            a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.top_p, a.min_p, a.rep, a.presence, a.frequency,
+            a.history, a.hist_stride, a.hist_len, a.hist_len_stride, ws);
+        sample_slices_kernel<DT, kModeOpen><<<rows * kSlices, kSliceThreads, 0, stream>>>(
+            a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.top_p, a.min_p, a.rep, a.presence, a.frequency,
+            a.history, a.hist_stride, a.hist_len, a.hist_len_stride, ws);
+      }
+      if (stages & kStageTopK)
+        sample_slices_kernel<DT, kModeTopK><<<rows * kSlices, kSliceThreads, 0, stream>>>(
+            a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.top_p, a.min_p, a.rep, a.presence, a.frequency,
+            a.history, a.hist_stride, a.hist_len, a.hist_len_stride, ws);
     }
   }
   sample_kernel<DT, VEC><<<rows, kThreads, shm, stream>>>(
       a.logits, a.row_stride, a.V, a.temperature, a.top_k, a.top_p, a.min_p, a.rep, a.presence,
-      a.frequency, a.history, a.hist_stride, a.hist_len, a.hist_len_stride, a.uniforms, a.out, ws);
+      a.frequency, a.history, a.hist_stride, a.hist_len, a.hist_len_stride, a.uniforms, a.out, ws, stages);
   return check_launch("sample");
 }
 

@@ -57,6 +57,7 @@ class DecodeRunner:
         self.live = torch.zeros(1, dtype=torch.int32, device=dev)  # rows that advance
         self.n_live = 0
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self.graph_stages: dict[int, int] = {}  # sampler stages each graph was captured with
         self._free_blocks = list(range(cache.num_allocatable_blocks))
 
     def _meta(self, b: int) -> AttentionMetadata:
@@ -90,7 +91,8 @@ class DecodeRunner:
         # decode_advance (no torch RNG in the captured step)
         sample_tokens(logits, s.temperature[:b], s.top_k[:b], s.top_p[:b], s.min_p[:b],
                       s.repetition_penalty[:b], s.presence_penalty[:b], s.frequency_penalty[:b],
-                      self.history, self.step_count, s.uniforms[:b], s.tokens[:b], workspace=s.workspace)
+                      self.history, self.step_count, s.uniforms[:b], s.tokens[:b], workspace=s.workspace,
+                      stages=s.stages)
         decode_advance(s.tokens, self.input_ids, self.positions, self.seq_lens, self.slot_mapping,
                        self.block_tables, self.bs, b, self.live, self.history, self.step_count,
                        s.rng_seeds, s.uniforms)
@@ -149,7 +151,8 @@ class DecodeRunner:
         s.draw_uniforms(n)
         sample_tokens(logits, s.temperature[:n], s.top_k[:n], s.top_p[:n], s.min_p[:n],
                       s.repetition_penalty[:n], s.presence_penalty[:n], s.frequency_penalty[:n],
-                      self.history, self.step_count, s.uniforms[:n], s.tokens[:n], workspace=s.workspace)
+                      self.history, self.step_count, s.uniforms[:n], s.tokens[:n], workspace=s.workspace,
+                      stages=s.stages)
         decode_advance(s.tokens, self.input_ids, self.positions, self.seq_lens, self.slot_mapping,
                        self.block_tables, self.bs, self.B, self.live, self.history, self.step_count,
                        s.rng_seeds, s.uniforms)
@@ -160,7 +163,9 @@ class DecodeRunner:
         """Captures one decode step per bucket (default: all of them), largest
         first into one shared memory pool.  Warm-up runs on the pad block only
         (the live rows are parked and restored), so capture changes no
-        sequence.  Returns the buckets captured."""
+        sequence.  A graph keeps the sampler's sliced stages of the requests
+        at capture (other requests replay it with the same tokens, perhaps
+        slower; :meth:`generate` recaptures).  Returns the buckets captured."""
         todo = sorted(self.buckets if buckets is None else buckets, reverse=True)
         for b in todo:
             if b not in self.buckets:
@@ -190,6 +195,7 @@ class DecodeRunner:
                 self._step(b)
             pool = g.pool()
             self.graphs[b] = g
+            self.graph_stages[b] = self.sampler.stages
         self.block_tables.copy_(bt)
         for t, v in zip(parked, saved):
             t.copy_(v)
@@ -220,7 +226,8 @@ class DecodeRunner:
                 f"max_new_tokens={max_new_tokens} exceeds the runner's history of "
                 f"{self.history.shape[1]} tokens (construct it with a larger max_new_tokens)")
         self.start(prompts, params, shuffle_blocks)
-        if self.graph is None:
-            self.capture((self.bucket_for(len(prompts)),))
+        b = self.bucket_for(len(prompts))
+        if self.graph is None or self.graph_stages.get(b) != self.sampler.stages:
+            self.capture((b,))
         self.replay(max_new_tokens - 1)
         return self.history[: len(prompts), :max_new_tokens].clone()

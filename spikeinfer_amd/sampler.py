@@ -60,6 +60,28 @@ class SamplingParams:
         return self.temperature < _GREEDY_TEMP
 
 
+# Sliced stages of sample_tokens (spk_sample_ws's SPK_SAMPLE_STAGE_* bits).
+STAGE_TOPK = 1
+STAGE_OPEN = 2
+_SLICED_MAX_K = 256  # largest top_k of the top-k stage
+
+
+def stages_for(params: list["SamplingParams"]) -> int:
+    """The sliced stages a batch of these requests can use: the top-k stage
+    for sampled rows with 0 < top_k <= 256, the open stage for sampled rows
+    with any other top_k (no cut, or one at least the vocabulary) and a top-p
+    or min-p cut."""
+    st = 0
+    for p in params:
+        if p.is_greedy:
+            continue
+        if 0 < p.top_k <= _SLICED_MAX_K:
+            st |= STAGE_TOPK
+        elif p.top_p < 1.0 or p.min_p > 0.0:
+            st |= STAGE_OPEN
+    return st
+
+
 def sample_tokens(
     logits: torch.Tensor,
     temperature: torch.Tensor,
@@ -74,6 +96,7 @@ def sample_tokens(
     uniforms: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
+    stages: int = STAGE_TOPK | STAGE_OPEN,
 ) -> torch.Tensor:
     """One token per row of ``logits [rows, vocab]`` (fp32/bf16/fp16, row
     stride free, vocab stride 1).
@@ -84,8 +107,12 @@ def sample_tokens(
     ``history_len`` int32 ``[rows]`` (or ``[1]``: one count for all rows) how
     many.  ``uniforms`` float32 ``[rows]`` in [0, 1) drive the draw.  Returns
     ``out`` int64 ``[rows]``.  ``workspace`` (uint8, at least
-    :func:`sample_workspace_bytes` ``(rows)``) lets rows with a top-k cut
-    gather their candidates over several workgroups per row (same tokens).
+    :func:`sample_workspace_bytes` ``(rows)``) lets rows spread their
+    candidate search over several workgroups per row, with the same tokens:
+    ``stages`` bit :data:`STAGE_TOPK` for rows with 0 < top_k <= 256, bit
+    :data:`STAGE_OPEN` for rows with no top-k cut and a top-p or min-p cut
+    (each stage costs its launches whether or not the batch holds such rows;
+    :func:`stages_for` picks them for a batch of requests).
     """
     dev = _lib.require_gpu(logits, temperature, top_k, top_p, min_p, repetition_penalty,
                            presence_penalty, frequency_penalty, history, history_len, uniforms, out)
@@ -123,7 +150,7 @@ def sample_tokens(
             temperature.data_ptr(), _lib.ptr(top_k), _lib.ptr(top_p), _lib.ptr(min_p),
             _lib.ptr(repetition_penalty), _lib.ptr(presence_penalty), _lib.ptr(frequency_penalty),
             _lib.ptr(history), hist_stride, _lib.ptr(history_len), len_stride, _lib.ptr(uniforms),
-            out.data_ptr(), _lib.ptr(workspace), ws_bytes, _lib.stream_of(dev),
+            out.data_ptr(), _lib.ptr(workspace), ws_bytes, int(stages), _lib.stream_of(dev),
         ),
         "sample",
     )
@@ -166,6 +193,7 @@ class BatchSampler:
         self.tokens = torch.zeros(max_rows, dtype=torch.int64, device=self.device)
         # candidates of the sliced top-k stage (sample_tokens' workspace)
         self.workspace = torch.empty(sample_workspace_bytes(max_rows), dtype=torch.uint8, device=self.device)
+        self.stages = 0  # sliced stages the current requests use (stages_for)
         self.params: list[SamplingParams] = []
         self._generators: dict[int, torch.Generator] = {}
 
@@ -174,6 +202,7 @@ class BatchSampler:
             raise ValueError(f"{len(params)} rows > max_rows {self.max_rows}")
         n = len(params)
         self.params = list(params)
+        self.stages = stages_for(self.params)
         host = lambda vals, dt: torch.tensor(vals, dtype=dt).to(self.device)
         self.temperature[:n] = host([p.temperature for p in params], torch.float32)
         self.top_k[:n] = host([p.top_k for p in params], torch.int32)
@@ -233,7 +262,7 @@ class BatchSampler:
             logits, self.temperature[:n], self.top_k[:n], self.top_p[:n], self.min_p[:n],
             self.repetition_penalty[:n], self.presence_penalty[:n], self.frequency_penalty[:n],
             self.history[:n], self.history_len[:n], self.uniforms[:n], self.tokens[:n],
-            workspace=self.workspace,
+            workspace=self.workspace, stages=self.stages,
         )
         if record:
             self.record(n)

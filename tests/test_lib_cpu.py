@@ -138,14 +138,35 @@ def test_python_api_refuses_cpu_tensors():
 
 def test_sampler_workspace_size_and_validation():
     """The sliced sampler's workspace: per row, 8 slices of 256 candidates
-    (x and index) plus a count and a maximum each; a short or misaligned one
-    is refused before anything is launched."""
+    (x and index) plus a count, a maximum and a mass partial each; a short or
+    misaligned one, or unknown stage bits, are refused before anything is
+    launched."""
     lib = _lib.load()
-    assert lib.spk_sample_workspace_bytes(64) == 64 * 8 * (2 * 256 * 4 + 8)
+    assert lib.spk_sample_workspace_bytes(64) == 64 * 8 * (2 * 256 * 4 + 16)
     assert lib.spk_sample_workspace_bytes(0) == 0
-    args = lambda ws, nbytes: (16, 2, 151936, 4, 151936, 16, None, None, None, None, None, None, None, 0,
-                               None, 0, None, 32, ws, nbytes, None)
+    args = lambda ws, nbytes, stages=3: (16, 2, 151936, 4, 151936, 16, None, None, None, None, None, None,
+                                         None, 0, None, 0, None, 32, ws, nbytes, stages, None)
     assert lib.spk_sample_ws(*args(64, 100)) == _lib.SPK_EINVAL
     assert b"workspace" in lib.spk_last_error()
     assert lib.spk_sample_ws(*args(8, lib.spk_sample_workspace_bytes(4))) == _lib.SPK_EINVAL
     assert b"aligned" in lib.spk_last_error()
+    assert lib.spk_sample_ws(*args(64, lib.spk_sample_workspace_bytes(4), 4)) == _lib.SPK_EINVAL
+    assert b"stage" in lib.spk_last_error()
+
+
+def test_sampler_stages_for_requests():
+    """Which sliced sampler stages a batch of requests can use: greedy rows
+    none, 0 < top_k <= 256 the top-k stage, every other top_k the open one
+    when the row has a top-p or min-p cut."""
+    from spikeinfer_amd.sampler import STAGE_OPEN, STAGE_TOPK, SamplingParams, stages_for
+
+    assert stages_for([]) == 0
+    assert stages_for([SamplingParams(temperature=0.0)]) == 0
+    assert stages_for([SamplingParams(temperature=0.8, top_k=50)]) == STAGE_TOPK
+    assert stages_for([SamplingParams(temperature=0.8, top_k=256)]) == STAGE_TOPK
+    assert stages_for([SamplingParams(temperature=0.8, top_k=257, top_p=0.9)]) == STAGE_OPEN
+    assert stages_for([SamplingParams(temperature=0.8, min_p=0.05)]) == STAGE_OPEN
+    assert stages_for([SamplingParams(temperature=0.8)]) == 0  # a draw over the whole mass
+    assert stages_for([SamplingParams(temperature=0.8, top_k=257)]) == 0
+    assert stages_for([SamplingParams(top_p=0.9), SamplingParams(top_k=5)]) == STAGE_TOPK | STAGE_OPEN
+    assert (STAGE_TOPK, STAGE_OPEN) == (1, 2)  # SPK_SAMPLE_STAGE_TOPK / _OPEN

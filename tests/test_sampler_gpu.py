@@ -121,6 +121,82 @@ def test_sampler_sliced_candidates_give_the_same_tokens(gpu, case, dtype):
     assert sliced == plain
 
 
+# Rows with no top-k cut (the open stage).  "peaked" logits are N(0, 6^2) (a
+# trained model's kind: the top few hundred tokens hold most of the mass, so
+# the slices decide most rows); flat N(0, 2^2) ones leave the cut past the
+# slices' lists, and the rows fall back to the one-workgroup path.
+OPEN_CASES = [
+    (151936, 6.0, dict(temperature=1.0)),                         # no cut at all: not taken by the stage
+    (151936, 6.0, dict(temperature=1.0, min_p=0.01)),             # min_p only: the draw over the alive mass
+    (151936, 6.0, dict(temperature=0.8, top_p=0.9, rep=1.1)),
+    (151936, 6.0, dict(temperature=1.0, min_p=0.05, top_p=0.95, presence=0.4, frequency=0.3)),
+    (151936, 6.0, dict(temperature=1.3, top_k=151936, top_p=0.7)),  # top_k >= vocab: no cut
+    (151936, 2.0, dict(temperature=1.0, min_p=0.001)),            # flat: falls back
+    (151936, 2.0, dict(temperature=1.0, top_p=0.9)),
+    (151936, 0.0, dict(temperature=1.0, top_p=0.5)),              # every logit equal
+    (151936, 0.05, dict(temperature=0.7, top_p=0.5)),             # bf16: heavy ties
+    (1000, 3.0, dict(temperature=1.0, top_p=0.8)),                # four slices, the last one short
+    (60, 3.0, dict(temperature=1.0, top_p=0.999, rep=2.0)),       # one slice, listed whole
+    (100, 3.0, dict(temperature=1.0, min_p=0.2, rep=2.0)),        # one partial slice
+    (262144, 8.0, dict(temperature=1.2, top_p=0.99)),             # the largest vocabulary
+    (151936, 30.0, dict(temperature=0.3, top_p=0.99)),            # nearly one-hot
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", range(len(OPEN_CASES)))
+def test_sampler_open_rows_give_the_same_tokens(gpu, case, dtype):
+    """With the workspace, rows with no top-k cut are decided from the slices'
+    lists and exact mass partials when their top-p cut and draw fall inside
+    the certified prefix, and by the one-workgroup path otherwise: every token
+    equals the one-workgroup path's."""
+    V, scale, p = OPEN_CASES[case]
+    print(f"open-row sampler case {case} V={V} dtype={dtype}", flush=True)
+    rng = np.random.default_rng(200 + case)
+    rows = 24
+    logits = (rng.standard_normal((rows, V)) * scale).astype(np.float32)
+    histories = [rng.integers(0, V, size=rng.integers(0, 60)).tolist() for _ in range(rows)]
+    for i, h in enumerate(histories):
+        for t in h[:3]:
+            logits[i, t] = 4 * scale + rng.standard_normal()
+    us = rng.random(rows).astype(np.float32).tolist()
+    us[0], us[1] = 0.0, float(np.nextafter(np.float32(1), np.float32(0)))  # the ends of the draw
+    plain, _ = _run(gpu, logits, [p] * rows, histories, us, dtype)
+    sliced, _ = _run(gpu, logits, [p] * rows, histories, us, dtype, sliced=True)
+    assert sliced == plain
+
+
+def test_sampler_mixed_batch_and_stage_bits(gpu):
+    """One batch of open, top-k, greedy and large-k rows: every stage set gives
+    the one-workgroup path's tokens, including a workspace last filled by a
+    call with other stages (the row kernel reads only the lists this call's
+    stages wrote)."""
+    from spikeinfer_amd.sampler import STAGE_OPEN, STAGE_TOPK, stages_for
+
+    rng = np.random.default_rng(77)
+    rows, V = 32, 151936
+    kinds = [dict(temperature=1.0), dict(temperature=0.8, top_k=40, top_p=0.9),
+             dict(temperature=0.0), dict(temperature=1.0, top_k=1000), dict(temperature=0.9, top_p=0.8),
+             dict(temperature=1.1, top_k=V, top_p=0.95)]
+    params = [kinds[i % len(kinds)] for i in range(rows)]
+    t = torch.tensor([q["temperature"] for q in params], dtype=torch.float32, device=gpu)
+    k = torch.tensor([q.get("top_k", -1) for q in params], dtype=torch.int32, device=gpu)
+    tp = torch.tensor([q.get("top_p", 1.0) for q in params], dtype=torch.float32, device=gpu)
+    ws = torch.empty(sample_workspace_bytes(rows), dtype=torch.uint8, device=gpu)
+    for trial in range(2):
+        lg = torch.from_numpy((rng.standard_normal((rows, V)) * 6).astype(np.float32)).to(gpu, torch.bfloat16)
+        u = torch.from_numpy(rng.random(rows).astype(np.float32)).to(gpu)
+        plain = sample_tokens(lg, t, k, tp, uniforms=u)
+        for st in (STAGE_TOPK | STAGE_OPEN, STAGE_TOPK, STAGE_OPEN, 0):
+            got = sample_tokens(lg, t, k, tp, uniforms=u, workspace=ws, stages=st)
+            assert torch.equal(plain, got), (trial, st)
+    sp = [SamplingParams(temperature=q["temperature"], top_k=q.get("top_k", -1), top_p=q.get("top_p", 1.0))
+          for q in kinds]
+    assert stages_for(sp) == STAGE_TOPK | STAGE_OPEN
+    assert stages_for(sp[1:2]) == STAGE_TOPK and stages_for(sp[2:3]) == 0
+    assert stages_for(sp[3:4]) == 0 and stages_for(sp[4:5]) == STAGE_OPEN
+
+
 def test_sampler_workspace_with_unaligned_rows_takes_the_row_path(gpu):
     """Rows whose stride is not a whole number of 16-byte vectors cannot be
     sliced: with a workspace they take the one-workgroup path, same tokens."""
