@@ -510,6 +510,51 @@ def bench_decode_step(steps, warmup, dev, batch=64, out_tokens=64):
     }
 
 
+def bench_sampler(steps, warmup, dev):
+    """The decode step's sampler alone: 64 rows x 151,936 bf16 logits, a
+    256-token history per row (150 counted), one call per graph replay, on the
+    one-workgroup path and with each sliced-stage mask.  Cases: config 5's
+    parameters on N(0, 1) logits, and rows with no top-k cut on peaked
+    N(0, 6^2) logits (top-p 0.9 with repetition 1.1; min-p 0.01; temperature
+    only, which the open stage does not take).  Every mask must give the
+    one-workgroup path's tokens."""
+    from spikeinfer_amd.sampler import STAGE_OPEN, STAGE_TOPK, sample_tokens, sample_workspace_bytes
+
+    R, V = 64, 151936
+    ws = torch.empty(sample_workspace_bytes(R), dtype=torch.uint8, device=dev)
+    out = torch.empty(R, device=dev, dtype=torch.int64)
+    full = lambda v: torch.full((R,), v, device=dev, dtype=torch.float32)
+    stream = torch.cuda.current_stream(dev)
+    cases = {"config5_topk50_topp0.9_rep1.1": (1.0, 0.8, 50, 0.9, 0.0, 1.1),
+             "peaked_topp0.9_rep1.1": (6.0, 0.8, -1, 0.9, 0.0, 1.1),
+             "peaked_minp0.01": (6.0, 1.0, -1, 1.0, 0.01, 1.0),
+             "peaked_temperature_only": (6.0, 1.0, -1, 1.0, 0.0, 1.0)}
+    res = {}
+    for name, (scale, temp, k, tp, mp, rp) in cases.items():
+        g = torch.Generator(device=dev).manual_seed(6000)
+        logits = (torch.randn((R, V), generator=g, device=dev) * scale).bfloat16()
+        hist = torch.randint(0, V, (R, 256), generator=g, device=dev)
+        hlen = torch.full((R,), 150, device=dev, dtype=torch.int32)
+        u = torch.rand(R, generator=g, device=dev)
+        args = (logits, full(temp), torch.full((R,), k, device=dev, dtype=torch.int32), full(tp), full(mp),
+                full(rp), None, None, hist, hlen, u, out)
+        row, ref = {}, None
+        for label, st in (("one_workgroup", 0), ("topk_stage", STAGE_TOPK), ("open_stage", STAGE_OPEN)):
+            call = lambda: sample_tokens(*args, workspace=ws if st else None, stages=st)
+            call()
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                call()
+            row[label + "_us"] = round(time_calls(gr.replay, steps, warmup, stream) * 1000, 1)
+            if ref is None:
+                ref = out.clone()
+            elif not torch.equal(out, ref):
+                raise RuntimeError(f"sampler {name}: stages {st} changed the tokens")
+        res[name] = row
+    return {"rows": R, "vocab": V, "dtype": "bf16", "graph_replay_us": res}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -525,7 +570,7 @@ def main():
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["config2", "config3", "config5"],
+    ap.add_argument("--only", choices=["config2", "config3", "config5", "sampler"],
                     help="run just this extra workload and print its figures (profiling)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one device copy of this many MiB (counter calibration)")
@@ -541,6 +586,8 @@ def main():
             res = bench_lif(args.steps, args.warmup, dev)
         elif args.only == "config5":
             res = bench_decode_step(args.steps, args.warmup, dev, out_tokens=64)
+        elif args.only == "sampler":
+            res = bench_sampler(min(args.steps, 50), min(args.warmup, 10), dev)
         else:
             c3 = make_attn_inputs(64, 128, 192, 0.2, 3000, dev, layers=24)
             ms3, _ = bench_attention(c3, args.steps, args.warmup, dev, torch.bfloat16, graph=1)
