@@ -579,3 +579,29 @@ def test_runner_sampling_in_graph_stays_in_top_k(gpu):
     tok = runner.history[:n, 1]
     top5 = logits.topk(5, dim=-1).indices
     assert all(int(tok[i]) in top5[i].tolist() for i in range(n))
+
+
+def test_runner_recaptures_when_sampler_stages_change(gpu):
+    """A graph keeps the sampler stages of the requests it was captured with:
+    generate() recaptures when new requests need other stages (top-k rows, then
+    top-p rows with no top-k cut), and the sampled tokens equal eager steps of
+    the same seeded requests."""
+    from spikeinfer_amd.sampler import STAGE_OPEN, STAGE_TOPK
+
+    m = _small_model(gpu, seed=21)
+    bs, n, plen, new = 16, 4, 10, 6
+    g = torch.Generator().manual_seed(23)
+    prompts = [torch.randint(0, 1024, (plen,), generator=g).tolist() for _ in range(n)]
+    runner = DecodeRunner(m, PagedSpikeCache(2, m.T, m.Hkv, m.D, 64, bs, device=gpu), batch_size=n,
+                          max_model_len=plen + new + 1, max_new_tokens=16)
+    for params, stages in (([SamplingParams(temperature=0.9, top_k=8, seed=31 + i) for i in range(n)], STAGE_TOPK),
+                           ([SamplingParams(temperature=0.9, top_p=0.8, seed=41 + i) for i in range(n)], STAGE_OPEN)):
+        toks = runner.generate(prompts, params, new, shuffle_blocks=3)
+        assert runner.graph_stages[n] == stages
+        eager = DecodeRunner(m, PagedSpikeCache(2, m.T, m.Hkv, m.D, 64, bs, device=gpu), batch_size=n,
+                             max_model_len=plen + new + 1, max_new_tokens=16)
+        eager.start(prompts, params, shuffle_blocks=3)
+        for _ in range(new - 1):
+            eager._step()
+        torch.cuda.synchronize()
+        assert torch.equal(toks, eager.history[:n, :new]), stages
