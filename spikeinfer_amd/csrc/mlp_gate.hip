@@ -49,6 +49,9 @@ constexpr int kRanges = 64;    // column ranges per token group
 constexpr int kMaxPairsPerRange = 8;
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int kSlotFloats = 2 * kMaxT * 4 * 64;  // one partial: 2 tiles x T row tiles x 4 x 64 lanes
+constexpr int kStageOff = 2 * kWaves * kSlotFloats * 4;  // the y staging tiles, after the slots
+constexpr int kStageBytes = kMaxT * 16 * 16 * 2;          // one wave's tile
+static_assert(kStageOff + kWaves * kStageBytes <= kLdsBytes, "slots and staging fit the LDS");
 
 // Packed W_gu (spk_mlp_gate_pack): for pair p (channels 16p..16p+15), k-step
 // ks (K 32ks..32ks+31) and tile g (0 gate, 1 up), 1 KB at ((p*KS + ks)*2 + g)
@@ -212,18 +215,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         su[t][j] += d[((1 * kMaxT + t) * 4 + j) * 64 + lane];
       }
   }
+  // The pair's y tile (T x 16 tokens x 16 channels, bf16) is staged in the
+  // wave's 2 KB above the partial slots, then each (t, token) row's 32 bytes
+  // go out as two 16-byte stores (16 two-byte stores a lane took ~2 us).
+  uint16_t *stg = reinterpret_cast<uint16_t *>(smem + kStageOff + wave * kStageBytes);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int tok = m * kTok + 4 * kq + j;
-    if (tok >= n) continue;
     float u = 0.f;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const float g = round_to<SPK_BF16>(sg[t][j]);
       const float up = round_to<SPK_BF16>(su[t][j]);
       const bool spike = lif_step(u, g, beta, th);
-      y[(static_cast<int64_t>(t) * n + tok) * I + ch] = f32_to_elem<SPK_BF16>((spike ? 1.f : 0.f) * up);
+      stg[(16 * t + 4 * kq + j) * 16 + r16] = f32_to_elem<SPK_BF16>((spike ? 1.f : 0.f) * up);
     }
+  }
+  const int tok = m * kTok + (lane & 15), t = lane >> 4;  // row (t, tok) of the tile
+  if (t < T && tok < n) {
+    const v4u *src = reinterpret_cast<const v4u *>(stg + lane * 16);
+    const v4u lo = src[0], hi = src[1];
+    v4u *dst = reinterpret_cast<v4u *>(y + (static_cast<int64_t>(t) * n + tok) * I + 16 * (p0 + pp));
+    dst[0] = lo;
+    dst[1] = hi;
   }
 }
 
@@ -283,8 +296,9 @@ extern "C" int spk_mlp_gate_lif(const void *x, const void *w_packed, const void 
   if (!mlp_shape_ok(T, n_tok, hidden, inter))
     return fail(SPK_EUNSUPPORTED, "mlp_gate_lif: T=%d n_tok=%d hidden=%d inter=%d not supported", T,
                 n_tok, hidden, inter);
-  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w_packed) & 15))
-    return fail(SPK_EINVAL, "mlp_gate_lif: x and packed weights must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w_packed) & 15) ||
+      (reinterpret_cast<uintptr_t>(y) & 15))
+    return fail(SPK_EINVAL, "mlp_gate_lif: x, packed weights and y must be 16-byte aligned");
   const int MG = (n_tok + mlp::kTok - 1) / mlp::kTok;
   const dim3 grid(MG * mlp::kRanges);
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -170,3 +170,13 @@ def test_sampler_stages_for_requests():
     assert stages_for([SamplingParams(temperature=0.8, top_k=257)]) == 0
     assert stages_for([SamplingParams(top_p=0.9), SamplingParams(top_k=5)]) == STAGE_TOPK | STAGE_OPEN
     assert (STAGE_TOPK, STAGE_OPEN) == (1, 2)  # SPK_SAMPLE_STAGE_TOPK / _OPEN
+
+
+def test_mlp_gate_lif_rejects_misaligned_pointers():
+    """The fused MLP gate writes y in 16-byte rows: a y (or x, or packed
+    weight) pointer off 16 bytes is refused before anything is launched."""
+    lib = _lib.load()
+    args = lambda x, w, y: (x, w, 16, 16, _lib.SPK_F32, y, 4, 64, 896, 4864, _lib.SPK_BF16, None)
+    assert lib.spk_mlp_gate_lif(*args(16, 16, 18)) == _lib.SPK_EINVAL
+    assert b"aligned" in lib.spk_last_error()
+    assert lib.spk_mlp_gate_lif(*args(24, 16, 16)) == _lib.SPK_EINVAL
