@@ -435,6 +435,9 @@ size_t spk_mlp_gate_packed_bytes(int hidden, int inter);
  * supports M <= 256, N a multiple of 16, K a multiple of 128 up to 1280, or up
  * to 5120 without a bias (the down projection), bf16 (SPK_EUNSUPPORTED
  * otherwise); sums are fp32 in a fixed order, bias added, then rounded once.
+ * x and w_packed 16-byte aligned; a y off 16 bytes is SPK_EUNSUPPORTED for
+ * the short-K path (its tiles go out as 16-byte rows).  The same holds for
+ * spk_mlp_gate_lif's y.
  */
 int spk_linear_pack(const void *w, int N, int K, int dtype, void *w_packed, void *stream);
 int spk_linear_decode(const void *x, const void *w_packed, const void *bias, void *y, int M, int N,

@@ -41,6 +41,9 @@ constexpr int kMaxUnitsPerWave = 2;  // tiles per range <= 2
 constexpr int kMaxPartSteps = 5;     // k-steps per part: K <= 8 * 5 * 32 = 1280
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int kSlotFloats = 4 * 4 * 64;  // one partial: 4 row tiles x 4 x 64 lanes
+constexpr int kStageOff = kWaves * kMaxUnitsPerWave * kSlotFloats * 4;  // y staging, after the slots
+constexpr int kStageBytes = 64 * 16 * 2;                               // one wave's 64 x 16 tile
+static_assert(kStageOff + kWaves * kStageBytes <= kLdsBytes, "slots and staging fit the LDS");
 
 // Packed W (spk_linear_pack): for tile p (rows 16p..16p+15 of W) and k-step
 // ks, 1 KB at (p * KS + ks) KB: lane l's 16 bytes are W[16p + l%16][32ks +
@@ -153,13 +156,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   }
   const int col = 16 * (p0 + wave) + r16;
   const float bv = bias ? elem_to_f32<SPK_BF16>(bias[col]) : 0.f;
+  // The tile (64 rows x 16 columns, bf16) is staged in the wave's 2 KB above
+  // the partial slots; each row's 32 bytes then go out as two 16-byte stores.
+  uint16_t *stg = reinterpret_cast<uint16_t *>(smem + kStageOff + wave * kStageBytes);
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = m0 + 16 * t + 4 * kq + i;
-      if (row < M) y[static_cast<int64_t>(row) * N + col] = f32_to_elem<SPK_BF16>(sum[t][i] + bv);
-    }
+    for (int i = 0; i < 4; ++i) stg[(16 * t + 4 * kq + i) * 16 + r16] = f32_to_elem<SPK_BF16>(sum[t][i] + bv);
+  const int row = m0 + lane;  // row `lane` of the tile
+  if (row < M) {
+    const v4u *src = reinterpret_cast<const v4u *>(stg + lane * 16);
+    const v4u lo = src[0], hi = src[1];
+    v4u *dst = reinterpret_cast<v4u *>(y + static_cast<int64_t>(row) * N + 16 * (p0 + wave));
+    dst[0] = lo;
+    dst[1] = hi;
+  }
 }
 
 // Wide N (the lm_head: 151,936 columns) at M <= 64: the x rows stay in LDS for
@@ -411,6 +422,8 @@ extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void
   const int P = N / 16;
   int R = ((256 / MG) + 7) / 8 * 8;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (reinterpret_cast<uintptr_t>(y) & 15)  // (the tile rows go out as 16-byte stores)
+    return fail(SPK_EUNSUPPORTED, "linear_decode: y must be 16-byte aligned for this shape");
   if (MG == 1 && P > lin::kMaxUnitsPerWave * R && N % 32 == 0) {
     // Wide N: 256 workgroups, each a range of tile pairs.
 #define SPK_WIDE_CASE(KS)                                                                              \

@@ -296,9 +296,10 @@ extern "C" int spk_mlp_gate_lif(const void *x, const void *w_packed, const void 
   if (!mlp_shape_ok(T, n_tok, hidden, inter))
     return fail(SPK_EUNSUPPORTED, "mlp_gate_lif: T=%d n_tok=%d hidden=%d inter=%d not supported", T,
                 n_tok, hidden, inter);
-  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w_packed) & 15) ||
-      (reinterpret_cast<uintptr_t>(y) & 15))
-    return fail(SPK_EINVAL, "mlp_gate_lif: x, packed weights and y must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w_packed) & 15))
+    return fail(SPK_EINVAL, "mlp_gate_lif: x and packed weights must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(y) & 15)  // (the tile rows go out as 16-byte stores)
+    return fail(SPK_EUNSUPPORTED, "mlp_gate_lif: y must be 16-byte aligned");
   const int MG = (n_tok + mlp::kTok - 1) / mlp::kTok;
   const dim3 grid(MG * mlp::kRanges);
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -172,11 +172,15 @@ def test_sampler_stages_for_requests():
     assert (STAGE_TOPK, STAGE_OPEN) == (1, 2)  # SPK_SAMPLE_STAGE_TOPK / _OPEN
 
 
-def test_mlp_gate_lif_rejects_misaligned_pointers():
-    """The fused MLP gate writes y in 16-byte rows: a y (or x, or packed
-    weight) pointer off 16 bytes is refused before anything is launched."""
+def test_decode_gemms_decline_misaligned_outputs():
+    """The fused MLP gate and linear_decode write y in 16-byte rows: a y off
+    16 bytes is declined as unsupported (the caller then takes the library
+    GEMM), a misaligned x or packed weight is an error; nothing is launched."""
     lib = _lib.load()
     args = lambda x, w, y: (x, w, 16, 16, _lib.SPK_F32, y, 4, 64, 896, 4864, _lib.SPK_BF16, None)
-    assert lib.spk_mlp_gate_lif(*args(16, 16, 18)) == _lib.SPK_EINVAL
+    assert lib.spk_mlp_gate_lif(*args(16, 16, 18)) == _lib.SPK_EUNSUPPORTED
     assert b"aligned" in lib.spk_last_error()
     assert lib.spk_mlp_gate_lif(*args(24, 16, 16)) == _lib.SPK_EINVAL
+    # linear_decode, q/k/v shape (M 256, N 1152, K 896)
+    assert lib.spk_linear_decode(16, 16, None, 18, 256, 1152, 896, _lib.SPK_BF16, None) == _lib.SPK_EUNSUPPORTED
+    assert b"aligned" in lib.spk_last_error()
