@@ -123,18 +123,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
   }
 
-  // Partials through LDS (x no longer read), slot = unit index.
+  // Partials through LDS (x no longer read), slot = unit index; a lane's
+  // accumulator of row tile t is one 16-byte chunk (t * 64 + lane).
   __syncthreads();
-  float *slots = reinterpret_cast<float *>(smem);
+  v4f *slots = reinterpret_cast<v4f *>(smem);
 #pragma unroll
   for (int j = 0; j < kMaxUnitsPerWave; ++j) {
     const int u = wave + kWaves * j;
     if (u < U) {
-      float *d = slots + u * kSlotFloats;
+      v4f *d = slots + u * (kSlotFloats / 4);
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) d[(t * 4 + i) * 64 + lane] = acc[j][t][i];
+      for (int t = 0; t < 4; ++t) d[t * 64 + lane] = acc[j][t];
     }
   }
   __syncthreads();
@@ -148,11 +147,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
     for (int i = 0; i < 4; ++i) sum[t][i] = 0.f;
   for (int part = 0; part < kParts; ++part) {
-    const float *d = slots + (wave * kParts + part) * kSlotFloats;
+    const v4f *d = slots + (wave * kParts + part) * (kSlotFloats / 4);
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 4; ++t) {
+      const v4f a = d[t * 64 + lane];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sum[t][i] += d[(t * 4 + i) * 64 + lane];
+      for (int i = 0; i < 4; ++i) sum[t][i] += a[i];
+    }
   }
   const int col = 16 * (p0 + wave) + r16;
   const float bv = bias ? elem_to_f32<SPK_BF16>(bias[col]) : 0.f;

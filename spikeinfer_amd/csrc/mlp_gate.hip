@@ -172,16 +172,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // Partials through LDS (the x rows are no longer read): slot 2w + 1 holds
   // the sums of the wave's last pair, slot 2w those of its first when split.
   __syncthreads();
-  float *slots = reinterpret_cast<float *>(smem);
+  // A lane's accumulator of (tile g, row tile t) is one 16-byte chunk.
+  v4f *slots = reinterpret_cast<v4f *>(smem);
   auto put = [&](int slot, const v4f (&g)[kMaxT], const v4f (&u)[kMaxT]) {
-    float *d = slots + slot * kSlotFloats;
+    v4f *d = slots + slot * (kSlotFloats / 4);
 #pragma unroll
-    for (int t = 0; t < kMaxT; ++t)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        d[((0 * kMaxT + t) * 4 + j) * 64 + lane] = g[t][j];
-        d[((1 * kMaxT + t) * 4 + j) * 64 + lane] = u[t][j];
-      }
+    for (int t = 0; t < T; ++t) {
+      d[(0 * kMaxT + t) * 64 + lane] = g[t];
+      d[(1 * kMaxT + t) * 64 + lane] = u[t];
+    }
   };
   if (nu > 0) {
     put(2 * wave + 1, accg, accu);
@@ -206,14 +205,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     if (pf == pp && pf != pl) slot = 2 * w;
     else if (pl == pp) slot = 2 * w + 1;
     if (slot < 0) continue;
-    const float *d = slots + slot * kSlotFloats;
+    const v4f *d = slots + slot * (kSlotFloats / 4);
 #pragma unroll
-    for (int t = 0; t < kMaxT; ++t)
+    for (int t = 0; t < T; ++t) {
+      const v4f a = d[(0 * kMaxT + t) * 64 + lane], c = d[(1 * kMaxT + t) * 64 + lane];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        sg[t][j] += d[((0 * kMaxT + t) * 4 + j) * 64 + lane];
-        su[t][j] += d[((1 * kMaxT + t) * 4 + j) * 64 + lane];
+        sg[t][j] += a[j];
+        su[t][j] += c[j];
       }
+    }
   }
   // The pair's y tile (T x 16 tokens x 16 channels, bf16) is staged in the
   // wave's 2 KB above the partial slots, then each (t, token) row's 32 bytes
