@@ -49,7 +49,7 @@ enum spk_dtype {
 /* Message of the last failing call on this thread ("" if none). */
 const char *spk_last_error(void);
 
-/* ABI version, bumped on any signature change (2: spk_decode_advance draws). */
+/* ABI version, bumped on any signature change (2: spk_decode_advance draws; 3: spk_decode_attn_combine takes the partials size). */
 int spk_abi_version(void);
 
 /*
@@ -147,7 +147,8 @@ size_t spk_decode_attn_workspace_bytes(int T, int N, int Hq, int Hkv,
  *
  * spk_decode_attn_combine: out[t, n, h, c] = sum_p a / sum_p l over the
  * partitions p < ceil(seq_lens[n] / part_len) (at most num_parts), summed in
- * partition order; a sequence with seq_len <= 0 gets zeros.
+ * partition order; a sequence with seq_len <= 0 gets zeros.  partials_bytes
+ * must cover num_parts * T*N*Hq*(head_dim+1) floats (SPK_EINVAL otherwise).
  */
 int spk_decode_attn_partials(const int32_t *q, const int64_t q_strides[4],
                              const int32_t *k_cache, const int64_t k_strides[4],
@@ -158,8 +159,8 @@ int spk_decode_attn_partials(const int32_t *q, const int64_t q_strides[4],
                              int head_dim, int block_size, int max_blocks, float scale,
                              int part_len, float *partials, size_t partials_bytes,
                              void *stream);
-int spk_decode_attn_combine(const float *partials, int num_parts, int part_len,
-                            const int32_t *seq_lens, void *out, int out_dtype,
+int spk_decode_attn_combine(const float *partials, size_t partials_bytes, int num_parts,
+                            int part_len, const int32_t *seq_lens, void *out, int out_dtype,
                             const int64_t out_strides[4], int T, int N, int Hq,
                             int head_dim, void *stream);
 

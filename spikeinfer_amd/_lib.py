@@ -29,7 +29,7 @@ _DTYPE_CODES = {
     torch.int32: SPK_I32,
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 DECODE_ATTN_SCRATCH_BYTES = 16 << 20  # SPK_DECODE_ATTN_SCRATCH_BYTES
 
 _i64p = ctypes.POINTER(ctypes.c_int64)
@@ -72,7 +72,7 @@ _SIGNATURES = {
         _vp, _i64p, _vp, _i64p, _vp, _i64p, _i64, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32,
         _i32, _i32, _i32, _f32, _i32, _vp, _sz, _vp]),
     "spk_decode_attn_combine": (_i32, [
-        _vp, _i32, _i32, _vp, _vp, _i32, _i64p, _i32, _i32, _i32, _i32, _vp]),
+        _vp, _sz, _i32, _i32, _vp, _vp, _i32, _i64p, _i32, _i32, _i32, _i32, _vp]),
     "spk_gather_unpack": (_i32, [
         _vp, _vp, _i64p, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "spk_qkv_decode_attn": (_i32, [

@@ -10,4 +10,4 @@ std::string &last_error_slot() {
 
 extern "C" const char *spk_last_error(void) { return spk::last_error_slot().c_str(); }
 
-extern "C" int spk_abi_version(void) { return 2; }
+extern "C" int spk_abi_version(void) { return 3; }

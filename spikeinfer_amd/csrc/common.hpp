@@ -43,6 +43,14 @@ inline int ilog2(int x) {
 
 // ---- element access by dtype code -----------------------------------------
 
+// Orders a wave's LDS writes before reads of what other lanes of the same
+// wave wrote (release fence, wave barrier, acquire fence).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }

@@ -458,8 +458,8 @@ extern "C" int spk_decode_attn_partials(const int32_t *q, const int64_t q_stride
                           stream, nullptr, 0, part_len, partials, partials_bytes);
 }
 
-extern "C" int spk_decode_attn_combine(const float *partials, int num_parts, int part_len,
-                                       const int32_t *seq_lens, void *out, int out_dtype,
+extern "C" int spk_decode_attn_combine(const float *partials, size_t partials_bytes, int num_parts,
+                                       int part_len, const int32_t *seq_lens, void *out, int out_dtype,
                                        const int64_t out_strides[4], int T, int N, int Hq,
                                        int head_dim, void *stream) {
   if (T <= 0 || N < 0 || Hq <= 0 || head_dim <= 0 || num_parts <= 0 || part_len <= 0)
@@ -468,6 +468,10 @@ extern "C" int spk_decode_attn_combine(const float *partials, int num_parts, int
   if (!valid_float_dtype(out_dtype)) return fail(SPK_EINVAL, "out dtype %d not a float type", out_dtype);
   if (N == 0) return SPK_OK;
   if (!partials || !seq_lens || !out) return fail(SPK_EINVAL, "decode_attn_combine: null pointer");
+  const size_t need = (size_t)num_parts * T * N * Hq * (head_dim + 1) * sizeof(float);
+  if (partials_bytes < need)
+    return fail(SPK_EINVAL, "decode_attn_combine: partials buffer has %zu bytes, %d partitions need %zu",
+                partials_bytes, num_parts, need);
   AttnParams p{};
   p.lens = seq_lens;
   // Partitions past num_parts do not exist in the buffer: lengths beyond

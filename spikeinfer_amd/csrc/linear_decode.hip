@@ -164,6 +164,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) stg[(16 * t + 4 * kq + i) * 16 + r16] = f32_to_elem<SPK_BF16>(sum[t][i] + bv);
+  wave_lds_sync();  // lanes read rows other lanes wrote
   const int row = m0 + lane;  // row `lane` of the tile
   if (row < M) {
     const v4u *src = reinterpret_cast<const v4u *>(stg + lane * 16);
@@ -423,8 +424,6 @@ extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void
   const int P = N / 16;
   int R = ((256 / MG) + 7) / 8 * 8;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (reinterpret_cast<uintptr_t>(y) & 15)  // (the tile rows go out as 16-byte stores)
-    return fail(SPK_EUNSUPPORTED, "linear_decode: y must be 16-byte aligned for this shape");
   if (MG == 1 && P > lin::kMaxUnitsPerWave * R && N % 32 == 0) {
     // Wide N: 256 workgroups, each a range of tile pairs.
 #define SPK_WIDE_CASE(KS)                                                                              \
@@ -453,6 +452,8 @@ extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void
 #undef SPK_WIDE_CASE
   }
   while (R * lin::kMaxUnitsPerWave < P) R += 8;
+  if (reinterpret_cast<uintptr_t>(y) & 15)  // (this kernel's tile rows go out as 16-byte stores)
+    return fail(SPK_EUNSUPPORTED, "linear_decode: y must be 16-byte aligned for this shape");
   static bool attr = false;
   if (!attr) {
     if (hipFuncSetAttribute(reinterpret_cast<const void *>(lin::linear_kernel),

@@ -231,6 +231,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       stg[(16 * t + 4 * kq + j) * 16 + r16] = f32_to_elem<SPK_BF16>((spike ? 1.f : 0.f) * up);
     }
   }
+  wave_lds_sync();  // lanes read rows other lanes wrote
   const int tok = m * kTok + (lane & 15), t = lane >> 4;  // row (t, tok) of the tile
   if (t < T && tok < n) {
     const v4u *src = reinterpret_cast<const v4u *>(stg + lane * 16);

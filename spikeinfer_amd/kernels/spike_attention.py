@@ -287,7 +287,7 @@ def combine_partitions(
         raise ValueError(f"out has shape {tuple(out.shape)}, expected {(T, n_seqs, n_heads, d1 - 1)}")
     _lib.check(
         _lib.load().spk_decode_attn_combine(
-            partials.data_ptr(), P, part_len, seq_lens.data_ptr(), out.data_ptr(),
+            partials.data_ptr(), partials.numel() * 4, P, part_len, seq_lens.data_ptr(), out.data_ptr(),
             _lib.dtype_code(out.dtype), _lib.strides(out), T, n_seqs, n_heads, d1 - 1,
             _lib.stream_of(dev),
         ),

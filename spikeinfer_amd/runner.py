@@ -165,7 +165,7 @@ class DecodeRunner:
         (the live rows are parked and restored), so capture changes no
         sequence.  A graph keeps the sampler's sliced stages of the requests
         at capture (other requests replay it with the same tokens, perhaps
-        slower; :meth:`generate` recaptures).  Returns the buckets captured."""
+        slower; :meth:`replay` recaptures).  Returns the buckets captured."""
         todo = sorted(self.buckets if buckets is None else buckets, reverse=True)
         for b in todo:
             if b not in self.buckets:
@@ -207,6 +207,13 @@ class DecodeRunner:
         return self.graphs.get(self.bucket_for(max(self.n_live, 1)))
 
     def replay(self, steps: int = 1) -> None:
+        """Replays the live batch's graph `steps` times.  The graph is
+        recaptured first when the live requests need other sampler stages than
+        the ones it was captured with (the tokens would not change, but the
+        captured stages would run the wrong kernels for these requests)."""
+        b = self.bucket_for(max(self.n_live, 1))
+        if b in self.graphs and self.graph_stages.get(b) != self.sampler.stages:
+            self.capture((b,))
         g = self.graph
         if g is None:
             raise RuntimeError(f"no graph captured for a batch of {self.n_live}")
@@ -227,7 +234,7 @@ class DecodeRunner:
                 f"{self.history.shape[1]} tokens (construct it with a larger max_new_tokens)")
         self.start(prompts, params, shuffle_blocks)
         b = self.bucket_for(len(prompts))
-        if self.graph is None or self.graph_stages.get(b) != self.sampler.stages:
+        if self.graph is None:
             self.capture((b,))
         self.replay(max_new_tokens - 1)
         return self.history[: len(prompts), :max_new_tokens].clone()

@@ -26,6 +26,14 @@ from . import _lib
 _GREEDY_TEMP = 1e-5
 
 
+def seed_as_int64(seed: int) -> int:
+    """A request seed as the int64 the device generator state holds: reduced
+    modulo 2**64 (as ``torch.Generator.manual_seed`` accepts any such value)
+    and stored as its two's-complement signed value."""
+    s = int(seed) & (2 ** 64 - 1)
+    return s - 2 ** 64 if s >= 2 ** 63 else s
+
+
 @dataclass
 class SamplingParams:
     """The sampling fields of spikeinfer/sampling_params.py:15-70, same
@@ -214,7 +222,7 @@ class BatchSampler:
         # seeded rows draw the same sequence whatever else is in the batch; the
         # others take seeds from torch's host generator
         fresh = torch.randint(0, 2 ** 62, (n,), dtype=torch.int64).tolist()
-        self.rng_seeds[:n] = host([int(p.seed) if p.seed is not None else fresh[i]
+        self.rng_seeds[:n] = host([seed_as_int64(p.seed) if p.seed is not None else fresh[i]
                                    for i, p in enumerate(params)], torch.int64)
         self.history_len.zero_()
         self._generators = {}

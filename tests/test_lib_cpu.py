@@ -184,3 +184,26 @@ def test_decode_gemms_decline_misaligned_outputs():
     # linear_decode, q/k/v shape (M 256, N 1152, K 896)
     assert lib.spk_linear_decode(16, 16, None, 18, 256, 1152, 896, _lib.SPK_BF16, None) == _lib.SPK_EUNSUPPORTED
     assert b"aligned" in lib.spk_last_error()
+
+
+def test_combine_checks_the_partials_size():
+    """spk_decode_attn_combine refuses a partials buffer smaller than
+    num_parts * T*N*Hq*(head_dim+1) floats before launching anything."""
+    lib = _lib.load()
+    s4 = _i64(0, 0, 0, 1)
+    need = 3 * 4 * 2 * 14 * 65 * 4
+    rc = lib.spk_decode_attn_combine(16, need - 4, 3, 512, 16, 16, _lib.SPK_F32, s4, 4, 2, 14, 64, None)
+    assert rc == _lib.SPK_EINVAL and b"partials buffer" in lib.spk_last_error()
+
+
+def test_request_seeds_as_int64():
+    """Request seeds are kept modulo 2**64 as two's-complement int64 (any seed
+    torch.Generator.manual_seed takes, including 2**63 and above)."""
+    from spikeinfer_amd.sampler import seed_as_int64
+
+    assert seed_as_int64(0) == 0
+    assert seed_as_int64(2 ** 63 - 1) == 2 ** 63 - 1
+    assert seed_as_int64(2 ** 63) == -(2 ** 63)
+    assert seed_as_int64(2 ** 64 - 1) == -1
+    assert seed_as_int64(2 ** 64 + 5) == 5
+    assert seed_as_int64(-1) == -1

@@ -319,6 +319,26 @@ def test_linear_decode_within_one_ulp(gpu, M, N, K, bias):
     assert bool((d <= want.float().abs() * 2.0 ** -7 + 1e-6).all()), f"max diff {float(d.max())}"
 
 
+def test_linear_decode_wide_accepts_a_misaligned_output(gpu):
+    """The wide-N kernel (the lm_head) writes y with 2-byte stores: an output
+    view 2 bytes off 16-byte alignment is accepted and gives the same bytes as
+    an aligned one."""
+    from spikeinfer_amd.kernels.decoder_ops import linear_decode, pack_linear
+
+    M, N, K = 64, 151936, 896
+    g = torch.Generator(device=gpu).manual_seed(7)
+    x = torch.randn((M, K), generator=g, device=gpu).bfloat16()
+    wp = pack_linear((torch.randn((N, K), generator=g, device=gpu) * 0.05).bfloat16())
+    want = linear_decode(x, wp)
+    buf = torch.empty(M * N + 8, device=gpu, dtype=torch.bfloat16)
+    out = buf[1:1 + M * N].view(M, N)
+    assert out.data_ptr() % 16 != 0
+    got = linear_decode(x, wp, out=out)
+    assert got is out
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_linear_decode_unsupported_shapes_return_none(gpu):
     from spikeinfer_amd.kernels.decoder_ops import linear_decode, pack_linear
 
@@ -605,3 +625,30 @@ def test_runner_recaptures_when_sampler_stages_change(gpu):
             eager._step()
         torch.cuda.synchronize()
         assert torch.equal(toks, eager.history[:n, :new]), stages
+
+
+def test_runner_replay_recaptures_when_sampler_stages_change(gpu):
+    """start() + replay() (without generate()) also recaptures the graph when
+    the new requests need other sampler stages; tokens equal eager steps."""
+    from spikeinfer_amd.sampler import STAGE_OPEN, STAGE_TOPK
+
+    m = _small_model(gpu, seed=22)
+    bs, n, plen, new = 16, 4, 10, 6
+    g = torch.Generator().manual_seed(24)
+    prompts = [torch.randint(0, 1024, (plen,), generator=g).tolist() for _ in range(n)]
+    mk = lambda: DecodeRunner(m, PagedSpikeCache(2, m.T, m.Hkv, m.D, 64, bs, device=gpu), batch_size=n,
+                              max_model_len=plen + new + 1, max_new_tokens=16)
+    runner = mk()
+    runner.generate(prompts, [SamplingParams(temperature=0.9, top_k=8, seed=51 + i) for i in range(n)], new,
+                    shuffle_blocks=3)
+    assert runner.graph_stages[n] == STAGE_TOPK
+    params = [SamplingParams(temperature=0.9, top_p=0.8, seed=61 + i) for i in range(n)]
+    runner.start(prompts, params, shuffle_blocks=3)
+    runner.replay(new - 1)
+    assert runner.graph_stages[n] == STAGE_OPEN
+    eager = mk()
+    eager.start(prompts, params, shuffle_blocks=3)
+    for _ in range(new - 1):
+        eager._step()
+    torch.cuda.synchronize()
+    assert torch.equal(runner.history[:n, :new], eager.history[:n, :new])
