@@ -246,26 +246,13 @@ extern "C" size_t spk_decode_attn_workspace_bytes(int T, int N, int Hq, int Hkv,
                                                   int block_size, int max_blocks) {
   if (T <= 0 || N <= 0 || Hkv <= 0 || max_blocks <= 0 || block_size <= 0) return 0;
   const int64_t ctx_max = (int64_t)max_blocks * block_size;
-  const int part = choose_part_len((int64_t)N * T * Hkv, ctx_max, block_size);
+  const int part = choose_part_len(block_size);
   const int64_t nparts = (ctx_max + part - 1) / part;
   // Partial sums of split contexts, then the launch order of long contexts.
   const size_t partials = nparts <= 1 ? 0 : (size_t)nparts * T * N * Hq * (head_dim + 1) * sizeof(float);
   const int64_t items = nparts * N;
   const size_t order = plan_in_workspace(ctx_max, items) ? ((size_t)items * T * Hkv + 1) * sizeof(int32_t) : 0;
   return partials + order;
-}
-
-// Compute units of the current device (cached per device; 256 if the query fails).
-static int device_cus() {
-  static int cus[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
 }
 
 // Shared by spk_decode_attn and spk_qkv_decode_attn: validation, parameters,
@@ -302,6 +289,8 @@ static int decode_attn_impl(const int32_t *q, const int64_t q_strides[4], const 
   }
   if (N == 0) return SPK_OK;
   const size_t need = partials ? 0 : spk_decode_attn_workspace_bytes(T, N, Hq, Hkv, head_dim, block_size, max_blocks);
+  if ((int64_t)N * T * Hkv * ((ctx_max + 32767) / 32768 + 1) >= (int64_t(1) << 30))
+    return fail(SPK_EUNSUPPORTED, "decode_attn: %d sequences x %d units is too many work items", N, T * Hkv);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(SPK_EINVAL, "workspace of %zu bytes, need %zu", workspace_bytes, need);
 
@@ -322,7 +311,7 @@ static int decode_attn_impl(const int32_t *q, const int64_t q_strides[4], const 
   p.T = T; p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.head_dim = head_dim;
   p.bs_log2 = ilog2(block_size); p.nrep = Hq / Hkv; p.scale = scale;
   p.ctx_cap = (int)std::min<int64_t>(ctx_max, INT32_MAX);
-  p.part_len = partials ? forced_part_len : choose_part_len((int64_t)N * T * Hkv, ctx_max, block_size);
+  p.part_len = partials ? forced_part_len : choose_part_len(block_size);
   p.num_parts = (int)((ctx_max + p.part_len - 1) / p.part_len);
   p.ws = partials ? partials : static_cast<float *>(workspace);
   p.partials_only = partials != nullptr;
@@ -343,14 +332,10 @@ static int decode_attn_impl(const int32_t *q, const int64_t q_strides[4], const 
                       (!partials || (int64_t)p.num_parts * N <= kInlinePlanItems);
     int32_t *order = !partials && plan_in_workspace(ctx_max, (int64_t)p.num_parts * N)
                          ? reinterpret_cast<int32_t *>(p.ws + partial_floats) : nullptr;
-    // Short contexts whose whole grid is resident at once (8 two-wave
-    // workgroups per CU) run 2 waves per unit: one round of workgroups
-    // instead of two.  Longer or ragged-long launches keep 4 waves, whose
-    // longest-first order balances them better.
-    const int64_t items = (int64_t)N * T * Hkv * p.num_parts;
-    int waves = !fz && head_dim == 64 && ctx_max <= 8192 && items <= 8 * (int64_t)device_cus() ? 2 : 4;
-    const char *wv = getenv("SPIKEINFER_AMD_ATTN_WAVES");  // tests force either launch
-    if (wv && (strcmp(wv, "2") == 0 || strcmp(wv, "4") == 0)) waves = atoi(wv);
+    // Contexts of at most kPairMaxLen tokens (every item short): the 2-wave
+    // launch, two waves per unit.  Otherwise 4-wave workgroups, which run the
+    // short items two units at a time in the same per-unit order.
+    const int waves = !fz && head_dim == 64 && ctx_max <= kPairMaxLen ? 2 : 4;
     launch_decode_mfma(p, plan, order, s, fz ? fused_dtype : 0, waves);
   } else if (fz) {
     return fail(SPK_EUNSUPPORTED, "qkv_decode_attn: needs head_dim 64, Hq/Hkv <= 8, aligned caches");

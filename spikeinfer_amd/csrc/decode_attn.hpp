@@ -4,12 +4,22 @@
 
 #include "common.hpp"
 
+#include <cstdlib>
+#include <cstring>
+
 namespace spk {
 
 constexpr int kAttnThreads = 256;   // 4 waves
 // Block-table entries of one partition staged in LDS by the matrix-core
 // kernel; choose_part_len never makes a partition span more blocks.
 constexpr int kMaxStagedBlocks = 2048;
+// Matrix-core path: items (partitions) of at most this many tokens sum their
+// tokens in the order of the 2-wave launch -- two waves per unit, 128-token
+// steps alternating -- in every launch shape (the 4-wave kernel runs two such
+// units per workgroup); longer items use four waves per unit.  The order is a
+// function of the item's own size, so a sequence's output does not depend on
+// the batch.
+constexpr int kPairMaxLen = 8192;
 constexpr int kMaxRep = 16;
 constexpr int kMaxFusedT = 8;  // timesteps the fused q/k/v path keeps in registers
 constexpr int kDigitEntries = 129;  // d = 0..128 (head_dim 64 or 128)
@@ -80,15 +90,13 @@ __device__ __forceinline__ int seq_len(const AttnParams &p, int n) { return min(
 // Fills digits[0..128] for `scale` (host; reuses the last table when unchanged).
 void build_digit_table(float scale, uint32_t digits[kDigitEntries]);
 
-// Partition length: long contexts are split so the grid has enough
-// workgroups and no single workgroup walks a 32k-token context alone.
-inline int choose_part_len(int64_t units, int64_t ctx_max, int block_size) {
+// Partition length: 32768 tokens, or fewer when a partition would stage
+// more than kMaxStagedBlocks block-table entries.  It depends on the block
+// size only -- never on the batch -- so a sequence is cut (and its sums
+// ordered) the same way whatever else is decoded with it.
+inline int choose_part_len(int block_size) {
   int part = 32768;
-  // At most kMaxStagedBlocks block-table entries per partition.
   while (part > block_size * kMaxStagedBlocks && part > 256) part >>= 1;
-  // Small decode batches: shorten partitions (down to 512) until the grid
-  // holds about four workgroups per CU.
-  while (part > 512 && part > block_size && units * ((ctx_max + part - 1) / part) < 1024) part >>= 1;
   return part < block_size ? block_size : part;  // partitions start on a block
 }
 
@@ -101,11 +109,16 @@ bool mfma_path_supported(const AttnParams &p);
 // (items + 1 ints of workspace, plan_in_workspace).
 inline bool plan_launch(int64_t ctx_max) { return ctx_max >= 8192; }
 constexpr int kInlinePlanItems = 4096;
+// SPIKEINFER_AMD_ATTN_PLAN=workspace forces the planner kernel for any
+// planned launch (tests check that both orders give the same bytes).
 inline bool plan_in_workspace(int64_t ctx_max, int64_t items) {
-  return plan_launch(ctx_max) && items > kInlinePlanItems;
+  const char *e = getenv("SPIKEINFER_AMD_ATTN_PLAN");
+  const bool force = e && strcmp(e, "workspace") == 0;
+  return plan_launch(ctx_max) && (items > kInlinePlanItems || force);
 }
 // Launches the matrix-core kernel; `plan` orders it longest first, from
-// `order` when not null (after the planner kernel fills it), else in-kernel.
+// `order` when not null (after the planner kernel fills it: items * T * Hkv
+// + 1 ints), else in-kernel.
 // fused_dtype: 0 for q from p.q, else the dtype (SPK_BF16 / SPK_F16) of p.fz.x.
 // waves: 4, or 2 for the short-context launch (plain path, head_dim 64 only;
 // otherwise 4 is used).

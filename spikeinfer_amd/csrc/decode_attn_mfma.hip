@@ -52,6 +52,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 namespace mfma {
 
 constexpr int kWaves = 4;  // waves per workgroup, except the short-context launch (KW = 2)
+
 constexpr int kStepTokens = 128;      // tokens per wave step (2 per lane)
 constexpr int kMaxPartBlocks = kMaxStagedBlocks;  // block-table entries staged per partition
 
@@ -228,26 +229,44 @@ __device__ __forceinline__ void mma_ops(const StepOps<W64> &o, v4f (&acc)[2][4 *
     accl[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(o.A[rt], Bl, accl[rt], 0, 4, 0, 127, 0, 127);
 }
 
-// Longest-processing-time-first order of the (sequence, partition) items,
-// computed by every workgroup for itself: slot q of the order is the item of
-// the q-th largest size bucket (256 tokens wide), ties in item order (item i =
-// part * N + sequence).  Items are counted into an LDS histogram, the buckets
-// scanned largest first, and the slot's item found by a block-wide prefix
-// count of that bucket's members.  Returns -1 past the last existing item
-// (uniform over the block).  Needs N * num_parts <= kInlinePlanItems; `sh`
-// holds kMaxBuckets + 8 ints and is free again after the call.  *len_out gets
-// the chosen item's sequence length (as seq_len computes it).  When every
-// sequence has the same length and one partition, the order is the item order
-// and is returned after one vote.
-constexpr int kMaxBuckets = 130;  // part_len <= 32768 tokens, 256 per bucket
-constexpr int kPlanKeys = 8;      // per-thread item keys kept in registers between the passes
-template <int KW>
-__device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh, int *len_out) {
+// Longest-processing-time-first order of the launch's blocks, computed by
+// every workgroup for itself.  An item ((sequence, partition), i = part * N +
+// sequence) takes ups blocks, one per unit, or -- with PAIRS (the 4-wave plain
+// kernel) and at most kPairMaxLen tokens -- ceil(ups / 2) blocks of two units
+// each, whose waves then take twice the steps.  Items are ordered by the
+// steps each of their waves takes (a paired item's tokens count twice), in
+// buckets 256 tokens wide whose low bit marks paired items, ties in item
+// order; the blocks of an item are consecutive.  Items are counted into an
+// LDS histogram, the buckets scanned largest first in blocks, and block b's
+// item found by a block-wide prefix count of its bucket's members.  When
+// every sequence has the same length and one partition, the order is the
+// item order, known after one vote.
+//
+// Returns block b's item, or -1 when the block has none (uniform over the
+// block); *sub_out gets the unit (or, paired, the unit pair) within the
+// item, *pair_out whether it is paired, *len_out its sequence length (as
+// seq_len computes it).  Needs N * num_parts <= kInlinePlanItems; `sh` holds
+// kMaxBuckets + 10 ints and is free again after the call.
+constexpr int kMaxBuckets = 2 * 130;  // (steps per wave in 256-token units + 2) x paired
+constexpr int kPlanKeys = 8;          // per-thread item keys kept in registers between the passes
+// Bucket of an item of `size` tokens (size <= 0: bucket 0, nothing to do).
+template <bool PAIRS>
+__device__ __forceinline__ int plan_bucket(int size) {
+  if (size <= 0) return 0;
+  const bool paired = PAIRS && size <= kPairMaxLen;
+  const int eff = paired ? 2 * size : size;
+  return 2 * (((eff + 255) >> 8) + 1) + (paired ? 1 : 0);
+}
+template <int KW, bool PAIRS>
+__device__ __forceinline__ int plan_slot(const AttnParams &p, int b, int ups, int *sh, int *len_out,
+                                         int *sub_out, bool *pair_out) {
   constexpr int kThreads = KW * 64;
   int *count = sh, *wsum = sh + kMaxBuckets, *res = wsum + KW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int M = p.N * p.num_parts;
-  const int nb = ((p.part_len + 255) >> 8) + 2;  // bucket of a full partition + 1
+  const int A = (ups + 1) >> 1;  // blocks of a paired item
+  const int nb = 2 * (((max(p.part_len, PAIRS ? 2 * kPairMaxLen : 0) + 255) >> 8) + 2);
+  auto bpi = [&](int bucket) { return (bucket & 1) ? A : ups; };  // blocks per item
   // Bucket of item i, -1 when the sequence has no such partition; `len` gets
   // the sequence's length.
   auto key = [&](int i, int &len) {
@@ -255,8 +274,7 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh, in
     len = seq_len(p, n);
     const int nparts = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
     if (part >= nparts) return -1;
-    const int size = min(p.part_len, len - part * p.part_len);
-    return size <= 0 ? 0 : ((size + 255) >> 8) + 1;
+    return plan_bucket<PAIRS>(min(p.part_len, len - part * p.part_len));
   };
   const int per = (M + kThreads - 1) / kThreads;
   const int i0 = min(M, tid * per), i1 = min(M, i0 + per);
@@ -274,7 +292,11 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh, in
 #pragma unroll
     for (int k = 0; k < kPlanKeys; ++k) same = same && (i0 + k >= i1 || lc[k] == l0);
     if (__syncthreads_and(same)) {
+      const int bk = plan_bucket<PAIRS>(min(p.part_len, l0));
+      const int q = b / bpi(bk);
       *len_out = l0;
+      *sub_out = b - q * bpi(bk);
+      *pair_out = (bk & 1) != 0;
       return q < M ? q : -1;
     }
   }
@@ -288,7 +310,7 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh, in
       }
     return key(i, len);
   };
-  for (int b = tid; b < nb; b += kThreads) count[b] = 0;
+  for (int bk = tid; bk < nb; bk += kThreads) count[bk] = 0;
   __syncthreads();
   for (int i = i0; i < i1; ++i) {
     int len;
@@ -296,12 +318,14 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh, in
     if (k >= 0) atomicAdd(&count[k], 1);
   }
   __syncthreads();
-  if (wave == 0) {  // largest bucket first: lane holds list positions 3*lane..3*lane+2
-    int c[3], sum = 0;
+  if (wave == 0) {  // largest bucket first, in blocks: lane holds list positions 5*lane..5*lane+4
+    constexpr int kPer = (kMaxBuckets + 63) / 64;
+    int c[kPer], sum = 0;
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      const int pos = 3 * lane + k;
-      c[k] = pos < nb ? count[nb - 1 - pos] : 0;
+    for (int k = 0; k < kPer; ++k) {
+      const int pos = kPer * lane + k;
+      const int bk = nb - 1 - pos;
+      c[k] = pos < nb ? count[bk] * bpi(bk) : 0;
       sum += c[k];
     }
     int incl = sum;
@@ -312,17 +336,21 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int q, int *sh, in
     }
     int run = incl - sum;
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      if (run <= q && q < run + c[k]) {
-        res[0] = nb - 1 - (3 * lane + k);
-        res[1] = q - run;
+    for (int k = 0; k < kPer; ++k) {
+      if (run <= b && b < run + c[k]) {
+        const int bk = nb - 1 - (kPer * lane + k);
+        res[0] = bk;
+        res[1] = (b - run) / bpi(bk);  // rank within the bucket
+        res[4] = (b - run) % bpi(bk);  // block within the item
       }
       run += c[k];
     }
-    if (lane == 63 && q >= incl) res[0] = -1;
+    if (lane == 63 && b >= incl) res[0] = -1;
   }
   __syncthreads();
   const int sel = res[0], j = res[1];
+  *sub_out = res[4];
+  *pair_out = (sel & 1) != 0;
   if (sel < 0) return -1;
   int mine = 0;
   for (int i = i0; i < i1; ++i) {
@@ -453,35 +481,63 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   // Unplanned launch: x = (sequence, timestep, kv head) unit, y = partition.
   // Either way consecutive block ids (dealt round-robin to the 8 XCDs) are
   // sibling units of equal length.
+  // Pair mode (PAIRS, planned launches): a short item's units run two
+  // waves each, two units per workgroup (waves 2s, 2s + 1: unit 2 * pair + s).
+  constexpr bool PAIRS = KW == 4 && XDT == 0 && W64 == 1;
   const int units = p.N * p.T * p.Hkv;
+  const int ups = p.T * p.Hkv;  // units per item
   int unit = blockIdx.x, part = blockIdx.y;
   int planned_len = 0;  // planned launch: the chosen item's sequence length
+  bool pair = false;
+  int pj = 0;  // pair mode: the unit pair of the item
   __shared__ __align__(16) char smem[kSmemBytes<W64, KW>];
   if (p.plan_inline) {  // planned launch: longest work items first
-    const int ups = p.T * p.Hkv;
-    const int i = plan_slot<KW>(p, (int)blockIdx.x / ups, reinterpret_cast<int *>(smem), &planned_len);
+    int sub;
+    const int i = plan_slot<KW, PAIRS>(p, blockIdx.x, ups, reinterpret_cast<int *>(smem), &planned_len,
+                                       &sub, &pair);
     if (i < 0) return;
-    unit = (i % p.N) * ups + (int)blockIdx.x % ups;
+    unit = (i % p.N) * ups + (pair ? 0 : sub);
+    pj = sub;
     part = i / p.N;
   } else if (p.order) {
-    const int items = units * p.num_parts;
-    if ((int)blockIdx.x >= p.order[items]) return;
-    const int item = p.order[blockIdx.x];
-    unit = item % units;
-    part = item / units;
+    // The planner's entry for this block (see decode_attn_plan).
+    if ((int)blockIdx.x >= p.order[units * p.num_parts]) return;
+    const int e = p.order[blockIdx.x];
+    const int rest = e & ((1 << 30) - 1);
+    const int item = rest / ups, sub = rest - item * ups;
+    pair = PAIRS && ((e >> 30) & 1);
+    pj = sub;
+    part = item / p.N;
+    unit = (item % p.N) * ups + (pair ? 0 : sub);
   }
-  const int kvh = unit % p.Hkv;
-  const int t = (unit / p.Hkv) % p.T;
-  const int n = unit / (p.Hkv * p.T);
+  const int n = unit / ups;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  int my_r = unit % ups;  // this wave's unit within the item
+  bool has_unit = true;
+  if (pair) {
+    my_r = 2 * pj + (wave >> 1);
+    has_unit = my_r < ups;  // an odd ups leaves the last pair half empty
+  }
+  // (wave-uniform; readfirstlane keeps the cache addresses in scalar registers)
+  const int kvh = __builtin_amdgcn_readfirstlane((has_unit ? my_r : 0) % p.Hkv);
+  const int t = __builtin_amdgcn_readfirstlane((has_unit ? my_r : 0) / p.Hkv);
 
   const int len = p.plan_inline ? planned_len : seq_len(p, n);
   const int nparts_seq = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
   if (part >= nparts_seq) return;
   const int start = part * p.part_len;
   const int end = min(len, start + p.part_len);
+  // Short items (at most kPairMaxLen tokens, head_dim 64) sum in the 2-wave
+  // order in every launch: the 2-wave launch, pairs in the 4-wave plain
+  // kernel, and in the fused kernel waves 0 and 1 alone (waves 2 and 3 only
+  // help derive the spikes).
+  const bool half = XDT != 0 && end - start <= kPairMaxLen;
+  const int kw_unit = KW == 2 || pair || half ? 2 : KW;  // waves per unit
+  const int wave_in = pair ? (wave & 1) : wave;         // wave index within the unit
+  const int leader = pair ? (wave & 2) : 0;             // the unit's reducing wave
+  if (half && wave >= 2) has_unit = false;              // (its spike work is done above the loop)
 
   FusedIn<XDT == 0 ? SPK_BF16 : XDT> fin;
   if constexpr (XDT != 0) fused_load<NREP, XDT>(p, n, t, kvh, wave, lane, fin);
@@ -549,9 +605,9 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
 
   v4f acc[2][4 * W64] = {}, accl[2] = {};
 
-  constexpr int kStride = KW * kStepTokens;
-  const int first = start + wave * kStepTokens;
-  const int span = end - first;
+  const int kStride = kw_unit * kStepTokens;
+  const int first = start + wave_in * kStepTokens;
+  const int span = has_unit ? end - first : 0;
   const int nfull = span > 0 ? (span / kStride) + ((span % kStride) >= kStepTokens ? 1 : 0) : 0;
   const int ntotal = span > 0 ? (span + kStride - 1) / kStride : 0;
 
@@ -692,7 +748,8 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   constexpr int kRed = kVals + 2;
   __syncthreads();
   float *red = reinterpret_cast<float *>(smem);
-  if (wave > 0) {
+  // Each unit's leader wave adds its other waves' values in wave order.
+  if (wave != leader) {
     float *dst = red + ((wave - 1) * 64 + lane) * kRed;
 #pragma unroll
     for (int k = 0; k < kVals; ++k) dst[k] = val[k];
@@ -700,8 +757,8 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
     for (int k = 0; k < 2; ++k) dst[kVals + k] = lh[k];
   }
   __syncthreads();
-  if (wave != 0) return;
-  for (int w = 1; w < KW; ++w) {
+  if (wave != leader || !has_unit) return;
+  for (int w = leader + 1; w < leader + kw_unit; ++w) {
     const float *src = red + ((w - 1) * 64 + lane) * kRed;
 #pragma unroll
     for (int k = 0; k < kVals; ++k) val[k] += src[k];
@@ -793,25 +850,31 @@ bool mfma_path_supported(const AttnParams &p) {
 
 namespace mfma {
 
-// Longest-processing-time-first launch order for split contexts.  One
-// workgroup counting-sorts the (sequence, partition) items by token count in
-// 256-token buckets, largest first; the T*Hkv sibling units of an item stay
-// adjacent.  Items past a sequence's length are left out (their blocks exit).
-// Ties are placed in arbitrary order: each item computes the same sums
-// wherever it runs, so outputs do not depend on it.
+// Longest-processing-time-first launch order, written by one workgroup for
+// launches with more items than plan_slot handles.  The same order as
+// plan_slot: items by the steps each of their waves takes (bucket from
+// plan_bucket; `pairs` as PAIRS there), largest first, the blocks of an item
+// adjacent.  Entry order[b] = (item * UPS + sub) | (paired << 30), item = part
+// * N + sequence, sub = the unit, or the unit pair of a paired item.  Items
+// past a sequence's length are left out (their blocks exit); order[N * UPS *
+// num_parts] gets the number of entries.  Ties are placed in arbitrary order:
+// each item computes the same sums wherever it runs, so outputs do not depend
+// on it.
 __global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, int ctx_cap, int N, int UPS,
-                                                        int part_len, int num_parts,
+                                                        int part_len, int num_parts, int pairs,
                                                         int32_t *order) {
   __shared__ int count[kMaxBuckets];
   __shared__ int offset[kMaxBuckets];
   const int tid = threadIdx.x;
-  const int nb = ((part_len + 255) >> 8) + 2;
+  const int A = (UPS + 1) >> 1;
+  const int nb = 2 * (((max(part_len, pairs ? 2 * kPairMaxLen : 0) + 255) >> 8) + 2);
   for (int b = tid; b < nb; b += blockDim.x) count[b] = 0;
   __syncthreads();
   auto bucket = [&](int len, int part) {
     const int size = min(part_len, len - part * part_len);
-    return size <= 0 ? 0 : ((size + 255) >> 8) + 1;  // len <= 0 items: bucket 0
+    return pairs ? plan_bucket<true>(size) : plan_bucket<false>(size);
   };
+  auto bpi = [&](int bk) { return (bk & 1) ? A : UPS; };
   auto exists = [&](int len, int part) {
     const int nparts = len <= 0 ? 1 : (len + part_len - 1) / part_len;
     return part < nparts;
@@ -819,7 +882,10 @@ __global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, in
   for (int i = tid; i < N * num_parts; i += blockDim.x) {
     const int n = i % N, part = i / N;
     const int len = min(lens[n], ctx_cap);
-    if (exists(len, part)) atomicAdd(&count[bucket(len, part)], UPS);
+    if (exists(len, part)) {
+      const int bk = bucket(len, part);
+      atomicAdd(&count[bk], bpi(bk));
+    }
   }
   __syncthreads();
   if (tid == 0) {
@@ -835,8 +901,9 @@ __global__ __launch_bounds__(1024) void decode_attn_plan(const int32_t *lens, in
     const int n = i % N, part = i / N;
     const int len = min(lens[n], ctx_cap);
     if (!exists(len, part)) continue;
-    const int at = atomicAdd(&offset[bucket(len, part)], UPS);
-    for (int ut = 0; ut < UPS; ++ut) order[at + ut] = part * (N * UPS) + n * UPS + ut;
+    const int bk = bucket(len, part);
+    const int at = atomicAdd(&offset[bk], bpi(bk));
+    for (int sub = 0; sub < bpi(bk); ++sub) order[at + sub] = (i * UPS + sub) | ((bk & 1) << 30);
   }
 }
 
@@ -854,8 +921,9 @@ void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s, 
     p.plan_inline = 1;
     grid = dim3(units * p.num_parts);
   } else if (plan) {
+    const bool pairs = !two && fused_dtype == 0 && p.head_dim == 64;  // as PAIRS in the kernel
     mfma::decode_attn_plan<<<1, 1024, 0, s>>>(p.lens, p.ctx_cap, p.N, p.T * p.Hkv, p.part_len, p.num_parts,
-                                              order);
+                                              pairs ? 1 : 0, order);
     p.order = order;
     grid = dim3(units * p.num_parts);
   }

@@ -20,19 +20,12 @@ ABS_TOL = 1e-3
 REL_TOL = 1e-5
 
 
-@pytest.fixture(autouse=True, params=["auto", "waves2", "waves4", "general"])
+@pytest.fixture(autouse=True, params=["auto", "general"])
 def attn_path(request, monkeypatch):
     """Every case runs on the dispatched path (matrix cores where the shape
-    allows: head_dim 64 or 128, n_rep <= 8), on the matrix-core kernel forced
-    to 2- and to 4-wave workgroups (head_dim 64; the dispatch picks 2 for
-    short contexts that fit the GPU in one round), and on the general VALU
-    path."""
-    path = "general" if request.param == "general" else "auto"
-    monkeypatch.setenv("SPIKEINFER_AMD_ATTN_PATH", path)
-    if request.param.startswith("waves"):
-        monkeypatch.setenv("SPIKEINFER_AMD_ATTN_WAVES", request.param[-1])
-    else:
-        monkeypatch.delenv("SPIKEINFER_AMD_ATTN_WAVES", raising=False)
+    allows: head_dim 64 or 128, n_rep <= 8; sequences of at most 8192 tokens
+    run two waves per unit, longer ones four) and on the general VALU path."""
+    monkeypatch.setenv("SPIKEINFER_AMD_ATTN_PATH", "general" if request.param == "general" else "auto")
     return request.param
 
 

@@ -1,0 +1,110 @@
+"""Batch invariance: one sequence's decode output does not depend on what it
+is decoded with (the reference asserts this end to end,
+tests/test_engine.py:104-114: a prompt alone and inside a batch give the same
+greedy tokens).
+
+Attention: a sequence's summation order depends only on its own length (two
+waves per unit up to 8192 tokens, four beyond; partitions of 32768 tokens),
+never on the batch, the launch order (the kernel's own longest-first order
+or the planner kernel's) or the neighbours' lengths, so the outputs of one
+sequence alone and in batches of 1..64 with short or 32k neighbours are
+compared bit for bit.  Inputs are uniform random words on
+the device (any bits will do for an identity)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+T, HQ, HKV, D, BS = 4, 14, 2, 64, 16
+
+
+def _inputs(lens, seed, dev):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    need = [(L + BS - 1) // BS for L in lens]
+    nb = sum(need) + 1
+    words = lambda *shape: torch.randint(-2 ** 31, 2 ** 31 - 1, shape, generator=g, device=dev,
+                                         dtype=torch.int32)
+    k, v = words(T, HKV, nb * BS, 2), words(T, HKV, nb * BS, 2)
+    q = words(T, len(lens), HQ, 2)
+    perm = torch.randperm(nb - 1, generator=g, device=dev).to(torch.int32)
+    tables = torch.full((len(lens), max(need)), nb - 1, dtype=torch.int32, device=dev)
+    at = 0
+    for i, m in enumerate(need):
+        tables[i, :m] = perm[at:at + m]
+        at += m
+    return dict(q=q, k=k, v=v, tables=tables, lens=torch.tensor(lens, dtype=torch.int32, device=dev))
+
+
+def _attn(inp, rows=None, **env):
+    from spikeinfer_amd.kernels import paged_spike_attn_decode
+
+    q, tables, lens = inp["q"], inp["tables"], inp["lens"]
+    if rows is not None:
+        q, tables, lens = q[:, rows].contiguous(), tables[rows].contiguous(), lens[rows].contiguous()
+    out = paged_spike_attn_decode(q, inp["k"], inp["v"], tables, lens, head_dim=D, block_size=BS,
+                                  num_q_heads=HQ, num_kv_heads=HKV)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.fixture
+def env(monkeypatch):
+    from spikeinfer_amd.kernels.spike_attention import decode_attn_workspace_bytes
+
+    def set_(plan=None):
+        decode_attn_workspace_bytes.cache_clear()  # its size depends on the plan
+        monkeypatch.delenv("SPIKEINFER_AMD_ATTN_PATH", raising=False)
+        if plan is None:
+            monkeypatch.delenv("SPIKEINFER_AMD_ATTN_PLAN", raising=False)
+        else:
+            monkeypatch.setenv("SPIKEINFER_AMD_ATTN_PLAN", plan)
+    set_()
+    yield set_
+    decode_attn_workspace_bytes.cache_clear()
+
+
+def test_config3_shape_alone_and_in_batches(gpu, env):
+    """Config 3 (64 sequences, ctx U[128, 192]): each sequence alone, in the
+    batch, and in a batch beside a 20,000-token sequence (which moves the
+    launch to the longest-first order): identical bytes."""
+    g = torch.Generator().manual_seed(31)
+    lens = torch.randint(128, 193, (64,), generator=g).tolist()
+    inp = _inputs(lens + [20000], 32, gpu)
+    print("batch invariance: config 3 shape", flush=True)
+    base = _attn(inp, rows=list(range(64)))
+    for i in (0, 17, 63):
+        assert torch.equal(_attn(inp, rows=[i])[:, 0], base[:, i]), f"sequence {i} alone"
+        mixed = _attn(inp, rows=[i, 64])
+        assert torch.equal(mixed[:, 0], base[:, i]), f"sequence {i} beside 20k tokens"
+    assert torch.equal(_attn(inp)[:, :64], base), "the batch with the long sequence"
+
+
+def test_config4_shape_alone_and_in_batches(gpu, env):
+    """Config-4 lengths (U[4096, 32768]) on 24 sequences plus one of exactly
+    8192 tokens: each alone, in the batch, in a sub-batch, and with the
+    launch order from the planner kernel instead of the kernel's own:
+    identical bytes."""
+    g = torch.Generator().manual_seed(41)
+    lens = torch.randint(4096, 32769, (24,), generator=g).tolist() + [8192]
+    inp = _inputs(lens, 42, gpu)
+    print("batch invariance: config 4 shape", flush=True)
+    base = _attn(inp)
+    env(plan="workspace")
+    assert torch.equal(_attn(inp), base), "planner-kernel order"
+    env()
+    for i in (0, 5, 23, 24):
+        assert torch.equal(_attn(inp, rows=[i])[:, 0], base[:, i]), f"sequence {i} alone"
+    sub = [3, 24, 7]
+    assert torch.equal(_attn(inp, rows=sub), base[:, sub]), "a sub-batch"
+
+
+def test_long_context_partitions_alone_and_in_batch(gpu, env):
+    """A 40,000-token sequence spans two 32,768-token partitions whatever its
+    batch: its output alone equals its output beside short sequences."""
+    inp = _inputs([40000, 150, 3000], 52, gpu)
+    print("batch invariance: 40k sequence", flush=True)
+    base = _attn(inp)
+    assert torch.equal(_attn(inp, rows=[0])[:, 0], base[:, 0])
+    assert torch.equal(_attn(inp, rows=[1])[:, 0], base[:, 1])

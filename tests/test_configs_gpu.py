@@ -90,7 +90,6 @@ def test_config4_against_oracle(density, config4_inputs, gpu, monkeypatch):
     from spikeinfer_amd.kernels import decode_attn_workspace_bytes, paged_spike_attn_decode
 
     monkeypatch.delenv("SPIKEINFER_AMD_ATTN_PATH", raising=False)
-    monkeypatch.delenv("SPIKEINFER_AMD_ATTN_WAVES", raising=False)
     q, ((k, v),), tables, lens = config4_inputs[density]
     assert int(lens.max()) == 32768
     # the headline launch: no partition split, no workspace, in-kernel order
@@ -160,8 +159,7 @@ def test_config4_deterministic_and_paths_agree(config4_inputs, gpu, monkeypatch)
     assert float((a - c).abs().max()) < 1e-5, "matrix-core and general paths disagree"
 
 
-@pytest.mark.parametrize("waves", ["2", "4"])
-def test_fixed_8k_batch_equal_and_unequal_lengths(waves, gpu, monkeypatch):
+def test_fixed_8k_batch_equal_and_unequal_lengths(gpu, monkeypatch):
     """The north_star shape, batch 256 x 8,192 tokens (one partition each, the
     in-kernel launch order): with every length equal the order is decided by
     one vote; with one sequence a token shorter the full histogram order runs.
@@ -170,10 +168,9 @@ def test_fixed_8k_batch_equal_and_unequal_lengths(waves, gpu, monkeypatch):
     from spikeinfer_amd.kernels import decode_attn_workspace_bytes, paged_spike_attn_decode
 
     monkeypatch.delenv("SPIKEINFER_AMD_ATTN_PATH", raising=False)
-    monkeypatch.setenv("SPIKEINFER_AMD_ATTN_WAVES", waves)
     q, ((k, v),), tables, lens = _paged_inputs(gpu, 256, 8192, 8192, 0.2, 8000)
     assert decode_attn_workspace_bytes(T, 256, HQ, HKV, D, BS, tables.shape[1]) == 0
-    print(f"fixed 8k waves={waves}", flush=True)
+    print("fixed 8k", flush=True)
     tg = tables.to(gpu)
     eq = paged_spike_attn_decode(q, k, v, tg, lens.to(gpu), D, BS, HQ, HKV).cpu().numpy()
     lens2 = lens.clone()

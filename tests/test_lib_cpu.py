@@ -49,9 +49,10 @@ def test_host_side_validation_without_a_gpu():
     rc = lib.spk_decode_attn(None, s4, None, s4, None, s4, 0, None, 0, 0, None, None, 0, s4,
                              4, 1, 14, 2, 64, 16, 8, 5.0, None, 0, None)
     assert rc == _lib.SPK_EINVAL and b"scale" in lib.spk_last_error()
-    # split contexts need a workspace; a missing one is rejected, not faulted
+    # split contexts (past 32768 tokens) need a workspace; a missing one is
+    # rejected, not faulted
     rc = lib.spk_decode_attn(None, s4, None, s4, None, s4, 0, None, 0, 0, None, None, 0, s4,
-                             4, 8, 14, 2, 64, 16, 2048, 0.125, None, 0, None)
+                             4, 8, 14, 2, 64, 16, 4096, 0.125, None, 0, None)
     assert rc == _lib.SPK_EINVAL and b"workspace" in lib.spk_last_error()
     assert lib.spk_lif_multistep(None, 2, _i64(0, 0, 1), None, None, 0, None, None, 0, None,
                                  0, 4, 4, None) == _lib.SPK_EINVAL
@@ -113,10 +114,16 @@ def test_workspace_sizing():
     # (one int per work item + the item count)
     ws = lib.spk_decode_attn_workspace_bytes(1, 4100, 14, 2, 64, 16, 750)
     assert ws == (4100 * 1 * 2 + 1) * 4
-    # a small batch of long contexts splits them: partial sums, no order
-    ws = lib.spk_decode_attn_workspace_bytes(4, 8, 14, 2, 64, 16, 2048)
-    nparts = ws // (4 * 8 * 14 * 65 * 4)
-    assert nparts > 1 and ws == nparts * 4 * 8 * 14 * 65 * 4
+    # a small batch is not split any further than a large one: partitions are
+    # 32768 tokens whatever the batch (its sums do not depend on the batch)
+    assert lib.spk_decode_attn_workspace_bytes(4, 8, 14, 2, 64, 16, 2048) == 0
+    # past 32768 tokens: partial sums of 32768-token partitions (8 sequences,
+    # 64k tokens: 2 partitions, 16 items, ordered inside the kernel)
+    ws = lib.spk_decode_attn_workspace_bytes(4, 8, 14, 2, 64, 16, 4096)
+    assert ws == 2 * 4 * 8 * 14 * 65 * 4
+    # smaller blocks cap a partition at 2048 staged blocks (8-token blocks: 16384)
+    ws = lib.spk_decode_attn_workspace_bytes(1, 1, 14, 2, 64, 8, 4096)
+    assert ws == 2 * 1 * 1 * 14 * 65 * 4
 
 
 def test_python_api_refuses_cpu_tensors():

@@ -32,7 +32,6 @@ def _close(got, want, ctx):
 @pytest.fixture(params=["auto", "general"])
 def path(request, monkeypatch):
     monkeypatch.setenv("SPIKEINFER_AMD_ATTN_PATH", request.param)
-    monkeypatch.delenv("SPIKEINFER_AMD_ATTN_WAVES", raising=False)
     return request.param
 
 

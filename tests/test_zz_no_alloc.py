@@ -1,7 +1,8 @@
 """spk_decode_attn_noalloc (the allocation-free decode attention entry point)
 through the C-ABI against spk_decode_attn with a caller workspace: identical
 outputs on two calls in a row, the second with a smaller input, both needing
-scratch (the launch-order list, then split-partition partial sums); and a
+scratch (the launch-order list, then the partial sums of a context longer
+than one partition); and a
 shape whose scratch exceeds the fixed size is rejected."""
 from __future__ import annotations
 
@@ -37,11 +38,11 @@ def _dev(case, gpu):
                 num_kv_heads=case["num_kv_heads"])
 
 
-def _ragged(n, seed):
+def _ragged(n, seed, longest):
     rng = np.random.default_rng(seed)
     lens = rng.integers(0, 200, n)
     lens[rng.choice(n, 20, replace=False)] = 0
-    lens[rng.choice(n, 3, replace=False)] = [8200, 12000, 8193]
+    lens[rng.choice(n, 3, replace=False)] = [longest, 12000, 8193]
     return attn_case(lens.tolist(), block_size=16, T=1, density=0.2, q_density=0.2, seed=seed,
                      compact=True)
 
@@ -51,10 +52,11 @@ def test_noalloc_matches_workspace_entry_on_consecutive_calls(gpu, monkeypatch):
     from spikeinfer_amd.kernels import decode_attn_workspace_bytes, paged_spike_attn_decode
 
     monkeypatch.delenv("SPIKEINFER_AMD_ATTN_PATH", raising=False)
-    monkeypatch.delenv("SPIKEINFER_AMD_ATTN_WAVES", raising=False)
     lib = _lib.load()
-    for n in (4100, 300):  # launch-order list in scratch, then partial sums
-        case = _ragged(n, n)
+    # launch-order list in scratch, then the partial sums of a context past
+    # one 32768-token partition
+    for n, longest in ((4100, 8200), (300, 40000)):
+        case = _ragged(n, n, longest)
         d = _dev(case, gpu)
         need = decode_attn_workspace_bytes(1, n, 14, 2, 64, 16, case["tables"].shape[1])
         assert 0 < need <= _lib.DECODE_ATTN_SCRATCH_BYTES
