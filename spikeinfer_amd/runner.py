@@ -31,7 +31,12 @@ DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64)
 class DecodeRunner:
     def __init__(self, model: SpikingDecoder, cache: PagedSpikeCache, batch_size: int,
                  max_model_len: int, max_new_tokens: int = 2048,
-                 buckets: tuple[int, ...] = DEFAULT_BUCKETS) -> None:
+                 buckets: tuple[int, ...] = DEFAULT_BUCKETS, batched_prefill: bool = False) -> None:
+        # batched_prefill: one prefill forward over all prompts (fewer, larger
+        # GEMMs) instead of one per prompt.  The library GEMMs of a prefill may
+        # then round a row differently with the batch around it, so tokens can
+        # depend on the batch; per-prompt prefill keeps them batch-invariant.
+        self.batched_prefill = batched_prefill
         self.model = model
         self.cache = cache
         self.B = batch_size
@@ -101,7 +106,8 @@ class DecodeRunner:
     @torch.no_grad()
     def start(self, prompts: list[list[int]], params: list[SamplingParams],
               shuffle_blocks: int | None = None) -> None:
-        """Allocates blocks, runs the prompts through one eager prefill, samples
+        """Allocates blocks, runs the prompts through an eager prefill (one
+        forward per prompt, or one for all with ``batched_prefill``), samples
         each row's first token and leaves the static buffers pointing at the
         first decode step.  ``shuffle_blocks`` seeds a random physical block
         order (the reference's block manager hands out whatever is free)."""
@@ -124,16 +130,31 @@ class DecodeRunner:
             pos += range(len(p))
             slots += slot_mapping(tab, 0, len(p), self.bs)
         dev = self.device
-        meta = AttentionMetadata(
-            slot_mapping=torch.tensor(slots, dtype=torch.int64, device=dev), block_size=self.bs,
-            num_decode_tokens=0, prefill_query_starts=starts,
-            prefill_query_lens=[len(p) for p in prompts], prefill_context_lens=[0] * n,
-            prefill_block_tables=[torch.tensor(t, dtype=torch.int32, device=dev) for t in tables])
-        hidden = self.model.forward_paged(torch.tensor(ids, dtype=torch.int64, device=dev),
-                                          torch.tensor(pos, dtype=torch.int64, device=dev),
-                                          self.cache.layers, meta)
-        last = torch.tensor([s + len(p) - 1 for s, p in zip(starts, prompts)], device=dev)
-        logits = self.model.compute_logits(hidden, last)
+
+        def prefill(group):  # prompt indices -> their last tokens' hidden rows
+            off, ss, ii, pp, sl = 0, [], [], [], []
+            for k in group:
+                ss.append(off)
+                ii += prompts[k]
+                pp += range(len(prompts[k]))
+                sl += slots[starts[k]:starts[k] + len(prompts[k])]
+                off += len(prompts[k])
+            meta = AttentionMetadata(
+                slot_mapping=torch.tensor(sl, dtype=torch.int64, device=dev), block_size=self.bs,
+                num_decode_tokens=0, prefill_query_starts=ss,
+                prefill_query_lens=[len(prompts[k]) for k in group], prefill_context_lens=[0] * len(group),
+                prefill_block_tables=[torch.tensor(tables[k], dtype=torch.int32, device=dev) for k in group])
+            hidden = self.model.forward_paged(torch.tensor(ii, dtype=torch.int64, device=dev),
+                                              torch.tensor(pp, dtype=torch.int64, device=dev),
+                                              self.cache.layers, meta)
+            last = torch.tensor([s + len(prompts[k]) - 1 for s, k in zip(ss, group)], device=dev)
+            return hidden.index_select(0, last)
+
+        if self.batched_prefill:
+            rows = prefill(list(range(n)))
+        else:
+            rows = torch.cat([prefill([k]) for k in range(n)])
+        logits = self.model.compute_logits(rows)
 
         self.live.fill_(n)
         self.n_live = n

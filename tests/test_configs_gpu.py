@@ -426,3 +426,44 @@ def test_config5_full_size_layers_stagewise(gpu):
             assert bool(((out - terms.mean(0).float()).abs() <= bound).all()), "final norm + mean"
     print("config5 stagewise stats:", stats, flush=True)
     assert stats["gate_flips"] <= 1e-5 * stats["gate_spikes"], stats
+
+
+def test_config5_graph_tokens_equal_eager_steps(gpu):
+    """Config 5 at its own workload: the Qwen2.5-0.5B-shaped spiking decoder
+    (24 layers, vocab 151,936, bf16 N(0, 0.02)), batch 64, 128-token random
+    prompts, 64 output tokens with config 5's sampling (temperature 0.8, top-k
+    50, top-p 0.9, repetition 1.1; seeded requests).  The 63 decode steps
+    replayed from the captured hipGraph (forward, lm_head, sampling and the
+    device-side advance in one graph) give the tokens of the same steps run
+    eagerly (reference: tests/test_engine.py:87-98, model_runner.py:218-287)."""
+    import math
+
+    from spikeinfer_amd.model import SpikingDecoder, SpikingQwenConfig
+    from spikeinfer_amd.runner import DecodeRunner
+    from spikeinfer_amd.sampler import SamplingParams
+    from spikeinfer_amd.spike_cache import PagedSpikeCache
+
+    cfg = SpikingQwenConfig()
+    B, plen, new = 64, 128, 64
+    model = SpikingDecoder(cfg, device=gpu, seed=5000)
+    max_len = plen + new + 1
+    blocks = B * math.ceil(max_len / BS) + 1
+    mk = lambda: DecodeRunner(model, PagedSpikeCache(cfg.num_hidden_layers, cfg.T, cfg.num_key_value_heads,
+                                                     cfg.head_dim, blocks, BS, device=gpu),
+                              B, max_len, max_new_tokens=new + 1)
+    g = torch.Generator().manual_seed(5001)
+    prompts = torch.randint(0, cfg.vocab_size, (B, plen), generator=g).tolist()
+    params = [SamplingParams(temperature=0.8, top_k=50, top_p=0.9, repetition_penalty=1.1, seed=7000 + i)
+              for i in range(B)]
+    print("config5 graph vs eager: graph", flush=True)
+    graphed = mk()
+    toks = graphed.generate(prompts, params, new, shuffle_blocks=5002)
+    print("config5 graph vs eager: eager", flush=True)
+    eager = mk()
+    eager.start(prompts, params, shuffle_blocks=5002)
+    for _ in range(new - 1):
+        eager._step()
+    torch.cuda.synchronize()
+    want = eager.history[:B, :new]
+    assert torch.equal(toks, want), f"{int((toks != want).sum())} tokens differ"
+    assert int(torch.unique(toks).numel()) > B  # the sampler really samples
