@@ -49,7 +49,7 @@ enum spk_dtype {
 /* Message of the last failing call on this thread ("" if none). */
 const char *spk_last_error(void);
 
-/* ABI version, bumped on any signature change (2: spk_decode_advance draws; 3: spk_decode_attn_combine takes the partials size). */
+/* ABI version, bumped on any signature change (2: spk_decode_advance draws; 3: spk_decode_attn_combine takes the partials size, spk_norm_* GEMMs). */
 int spk_abi_version(void);
 
 /*
@@ -448,6 +448,27 @@ int spk_mlp_gate_pack(const void *w_gu, int inter, int hidden, int dtype, void *
 int spk_mlp_gate_lif(const void *x, const void *w_packed, const void *beta,
                      const void *threshold, int param_dtype, void *y, int T, int n_tok,
                      int hidden, int inter, int dtype, void *stream);
+
+/*
+ * The same GEMMs starting from the residual stream instead of a normed input:
+ * the rows are add_rmsnorm(h, delta, norm_weight) (bf16, computed in the
+ * launch's prologue with spk_add_rmsnorm's arithmetic, so the results are
+ * identical to spk_add_rmsnorm followed by spk_linear_decode /
+ * spk_mlp_gate_lif), replacing the post-attention / next-layer RMSNorm and
+ * residual add (spikeinfer/modeling_fast.py:206-211) that precede the MLP and
+ * the q/k/v projections (:121-135, :186-190).  h_out (may be NULL; must not
+ * alias h or delta) receives round(h + delta).  h, delta: [rows, hidden]
+ * contiguous (rows = M, or T * n_tok), hidden <= 1024; 16-byte aligned.
+ * spk_norm_linear_decode supports the tiled shapes of spk_linear_decode (K =
+ * hidden a multiple of 128 up to 1024).
+ */
+int spk_norm_linear_decode(const void *h, const void *delta, const void *norm_weight, void *h_out,
+                           float eps, const void *w_packed, const void *bias, void *y, int M, int N,
+                           int K, int dtype, void *stream);
+int spk_norm_mlp_gate_lif(const void *h, const void *delta, const void *norm_weight, void *h_out,
+                          float eps, const void *w_packed, const void *beta, const void *threshold,
+                          int param_dtype, void *y, int T, int n_tok, int hidden, int inter, int dtype,
+                          void *stream);
 
 /*
  * Device-side advance of a decode batch after sampling: for rows i < n_live,

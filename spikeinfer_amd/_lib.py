@@ -101,6 +101,9 @@ _SIGNATURES = {
     "spk_linear_pack": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
     "spk_linear_decode": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
     "spk_mlp_gate_pack": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
+    "spk_norm_linear_decode": (_i32, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
+    "spk_norm_mlp_gate_lif": (_i32, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32,
+                                     _i32, _i32, _vp]),
     "spk_mlp_gate_lif": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "spk_decode_advance": (_i32, [
         _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp,

@@ -24,6 +24,7 @@
 // -> XCD b % 8), so W comes from HBM once.
 #include "common.hpp"
 #include "lif_math.hpp"
+#include "norm_rows.hpp"
 
 namespace spk {
 namespace lin {
@@ -49,9 +50,13 @@ static_assert(kStageOff + kWaves * kStageBytes <= kLdsBytes, "slots and staging 
 // ks, 1 KB at (p * KS + ks) KB: lane l's 16 bytes are W[16p + l%16][32ks +
 // 8(l/16) .. +7].
 
+// NORM: the rows are add_rmsnorm(nin.h, nin.delta, nin.w) (x unused), computed
+// in the prologue; the workgroups of the last column range (never empty) write
+// h + delta to nin.h_out.
+template <bool NORM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void linear_kernel(
     const uint16_t *x, const v4u *wp, const uint16_t *bias, uint16_t *y, int M, int N, int K,
-    int MG, int R) {
+    int MG, int R, NormIn nin) {
   extern __shared__ __align__(16) char smem[];
   const int KS = K / 32, kChunks = K / 8;  // k-steps, 16-byte chunks per row
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -83,14 +88,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   }
 
   // x rows m0..m0+63 (clamped to M - 1) into LDS, chunk c of row rr at c ^ (rr % 16).
-  const int total = kRows * kChunks;  // a multiple of 64 (K % 128 == 0)
-  for (int base = wave * 64; base < total; base += kWaves * 64) {
-    const int g = base + lane;
-    const int rr = g / kChunks, pc = g - rr * kChunks;
-    const int c = pc ^ (rr & 15);
-    const int row = min(m0 + rr, M - 1);
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(x + static_cast<int64_t>(row) * K + 8 * c),
-                                     (SPK_LDS void *)(smem + base * 16), 16, 0, 0);
+  if constexpr (NORM) {
+    norm_rows<kWaves, kRows / kWaves>(
+        nin, kRows, K, r == R - 1, wave, lane, [&](int rr) { return static_cast<int64_t>(min(m0 + rr, M - 1)); },
+        [&](int rr) { return m0 + rr < M; },
+        [&](int rr, int v, const NormRowBf16::v8u16 &yv) {
+          *reinterpret_cast<NormRowBf16::v8u16 *>(smem + rr * (kChunks * 16) + 16 * (v ^ (rr & 15))) = yv;
+        });
+  } else {
+    const int total = kRows * kChunks;  // a multiple of 64 (K % 128 == 0)
+    for (int base = wave * 64; base < total; base += kWaves * 64) {
+      const int g = base + lane;
+      const int rr = g / kChunks, pc = g - rr * kChunks;
+      const int c = pc ^ (rr & 15);
+      const int row = min(m0 + rr, M - 1);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(x + static_cast<int64_t>(row) * K + 8 * c),
+                                       (SPK_LDS void *)(smem + base * 16), 16, 0, 0);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
   __syncthreads();
@@ -389,6 +403,37 @@ extern "C" int spk_linear_pack(const void *w, int N, int K, int dtype, void *w_p
   return check_launch("linear_pack");
 }
 
+// The tiled kernel (K <= 1280, M <= 256): rows from x, or (nin) normed in the
+// prologue.  The column ranges are a multiple of 8 (one per XCD), about 256
+// workgroups in all, at most two 16-column tiles each.
+static int launch_linear_tiled(const void *x, const void *w_packed, const void *bias, void *y, int M, int N,
+                               int K, const NormIn *nin, hipStream_t s) {
+  const int MG = (M + lin::kRows - 1) / lin::kRows;
+  const int P = N / 16;
+  int R = ((256 / MG) + 7) / 8 * 8;
+  while (R * lin::kMaxUnitsPerWave < P) R += 8;
+  if (reinterpret_cast<uintptr_t>(y) & 15)  // (this kernel's tile rows go out as 16-byte stores)
+    return fail(SPK_EUNSUPPORTED, "linear_decode: y must be 16-byte aligned for this shape");
+  static bool attr[2] = {false, false};
+  const void *fn = nin ? reinterpret_cast<const void *>(lin::linear_kernel<true>)
+                       : reinterpret_cast<const void *>(lin::linear_kernel<false>);
+  if (!attr[nin ? 1 : 0]) {
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lin::kLdsBytes) != hipSuccess)
+      return fail(SPK_EHIP, "linear_decode: cannot reserve %d bytes of LDS", lin::kLdsBytes);
+    attr[nin ? 1 : 0] = true;
+  }
+  const NormIn none{};
+  if (nin)
+    lin::linear_kernel<true><<<MG * R, lin::kThreads, lin::kLdsBytes, s>>>(
+        nullptr, static_cast<const lin::v4u *>(w_packed), static_cast<const uint16_t *>(bias),
+        static_cast<uint16_t *>(y), M, N, K, MG, R, *nin);
+  else
+    lin::linear_kernel<false><<<MG * R, lin::kThreads, lin::kLdsBytes, s>>>(
+        static_cast<const uint16_t *>(x), static_cast<const lin::v4u *>(w_packed),
+        static_cast<const uint16_t *>(bias), static_cast<uint16_t *>(y), M, N, K, MG, R, none);
+  return check_launch("linear_decode");
+}
+
 extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void *bias, void *y,
                                  int M, int N, int K, int dtype, void *stream) {
   if (dtype != SPK_BF16) return fail(SPK_EUNSUPPORTED, "linear_decode: bf16 only");
@@ -451,20 +496,26 @@ extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void
     }
 #undef SPK_WIDE_CASE
   }
-  while (R * lin::kMaxUnitsPerWave < P) R += 8;
-  if (reinterpret_cast<uintptr_t>(y) & 15)  // (this kernel's tile rows go out as 16-byte stores)
-    return fail(SPK_EUNSUPPORTED, "linear_decode: y must be 16-byte aligned for this shape");
-  static bool attr = false;
-  if (!attr) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(lin::linear_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, lin::kLdsBytes) != hipSuccess)
-      return fail(SPK_EHIP, "linear_decode: cannot reserve %d bytes of LDS", lin::kLdsBytes);
-    attr = true;
-  }
-  lin::linear_kernel<<<MG * R, lin::kThreads, lin::kLdsBytes, s>>>(
-      static_cast<const uint16_t *>(x), static_cast<const lin::v4u *>(w_packed),
-      static_cast<const uint16_t *>(bias), static_cast<uint16_t *>(y), M, N, K, MG, R);
-  return check_launch("linear_decode");
+  return launch_linear_tiled(x, w_packed, bias, y, M, N, K, nullptr, s);
+}
+
+extern "C" int spk_norm_linear_decode(const void *h, const void *delta, const void *norm_weight, void *h_out,
+                                      float eps, const void *w_packed, const void *bias, void *y, int M, int N,
+                                      int K, int dtype, void *stream) {
+  if (dtype != SPK_BF16) return fail(SPK_EUNSUPPORTED, "norm_linear_decode: bf16 only");
+  if (M < 1 || M > 4 * lin::kRows || N < 16 || N % 16 || K % 128 || K > 1024 ||
+      K > lin::kParts * lin::kMaxPartSteps * 32)
+    return fail(SPK_EUNSUPPORTED, "norm_linear_decode: M=%d N=%d K=%d not supported", M, N, K);
+  if (!h || !delta || !norm_weight || !w_packed || !y)
+    return fail(SPK_EINVAL, "norm_linear_decode: null pointer");
+  const auto al = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  if (!al(h) || !al(delta) || !al(norm_weight) || !al(w_packed) || (h_out && !al(h_out)))
+    return fail(SPK_EINVAL, "norm_linear_decode: h, delta, norm weight, h_out and packed weights must be 16-byte aligned");
+  if (h_out && (h_out == h || h_out == delta))
+    return fail(SPK_EINVAL, "norm_linear_decode: h_out must not alias h or delta");
+  NormIn nin{static_cast<const uint16_t *>(h), static_cast<const uint16_t *>(delta),
+             static_cast<const uint16_t *>(norm_weight), static_cast<uint16_t *>(h_out), eps};
+  return launch_linear_tiled(nullptr, w_packed, bias, y, M, N, K, &nin, static_cast<hipStream_t>(stream));
 }
 
 }  // namespace spk

@@ -32,6 +32,7 @@
 // consecutive on one XCD (block b -> XCD b % 8), so W comes from HBM once.
 #include "common.hpp"
 #include "lif_math.hpp"
+#include "norm_rows.hpp"
 
 namespace spk {
 namespace mlp {
@@ -60,10 +61,13 @@ static_assert(kStageOff + kWaves * kStageBytes <= kLdsBytes, "slots and staging 
 
 // T is a template parameter: a runtime test per row tile would put branches
 // between the MFMAs (and the accumulator copies they bring cost registers).
-template <int KQ, int T>
+// NORM: the x rows are add_rmsnorm(nin.h, nin.delta, nin.w), computed in the
+// prologue; the workgroups of the last column range (never empty) write h +
+// delta to nin.h_out.
+template <int KQ, int T, bool NORM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void mlp_gate_lif_kernel(
     const uint16_t *x, const v4u *wp, const float *beta_p, const float *th_p, uint16_t *y, int n,
-    int I, int MG) {
+    int I, int MG, NormIn nin) {
   constexpr int KS = 4 * KQ;       // k-steps of 32 (H = 32 KS)
   constexpr int H = 32 * KS;
   constexpr int kChunks = 4 * KS;  // 16-byte chunks per x row
@@ -94,15 +98,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // x rows of the token group into LDS: row rr = 16 t + i holds token 16m + i
   // (clamped to n - 1) at timestep t; chunk c of it at chunk c ^ (rr % 16).
   const int rows = T * kTok;
-  const int total = rows * kChunks;  // a multiple of 64
-  for (int base = wave * 64; base < total; base += kWaves * 64) {
-    const int g = base + lane;
-    const int rr = g / kChunks, pc = g - rr * kChunks;
-    const int c = pc ^ (rr & 15);
-    const int t = rr >> 4, tok = min(m * kTok + (rr & 15), n - 1);
-    __builtin_amdgcn_global_load_lds(
-        reinterpret_cast<const void *>(x + (static_cast<int64_t>(t) * n + tok) * H + 8 * c),
-        (SPK_LDS void *)(smem + base * 16), 16, 0, 0);
+  if constexpr (NORM) {
+    norm_rows<kWaves, T * kTok / kWaves>(
+        nin, rows, H, r == kRanges - 1, wave, lane,
+        [&](int rr) { return static_cast<int64_t>(rr >> 4) * n + min(m * kTok + (rr & 15), n - 1); },
+        [&](int rr) { return m * kTok + (rr & 15) < n; },
+        [&](int rr, int v, const NormRowBf16::v8u16 &yv) {
+          *reinterpret_cast<NormRowBf16::v8u16 *>(smem + rr * (kChunks * 16) + 16 * (v ^ (rr & 15))) = yv;
+        });
+  } else {
+    const int total = rows * kChunks;  // a multiple of 64
+    for (int base = wave * 64; base < total; base += kWaves * 64) {
+      const int g = base + lane;
+      const int rr = g / kChunks, pc = g - rr * kChunks;
+      const int c = pc ^ (rr & 15);
+      const int t = rr >> 4, tok = min(m * kTok + (rr & 15), n - 1);
+      __builtin_amdgcn_global_load_lds(
+          reinterpret_cast<const void *>(x + (static_cast<int64_t>(t) * n + tok) * H + 8 * c),
+          (SPK_LDS void *)(smem + base * 16), 16, 0, 0);
+    }
   }
   // Then the first two units of W; the wait below lets those stay in flight
   // (vmcnt counts in issue order, so at most their loads outstanding means
@@ -286,9 +300,11 @@ extern "C" int spk_mlp_gate_pack(const void *w_gu, int inter, int hidden, int dt
   return check_launch("mlp_gate_pack");
 }
 
-extern "C" int spk_mlp_gate_lif(const void *x, const void *w_packed, const void *beta,
-                                const void *threshold, int param_dtype, void *y, int T, int n_tok,
-                                int hidden, int inter, int dtype, void *stream) {
+// Validation shared by both entry points; then the launch, rows from x or
+// (nin) normed in the prologue.
+static int mlp_gate_launch(const void *x, const NormIn *nin, const void *w_packed, const void *beta,
+                           const void *threshold, int param_dtype, void *y, int T, int n_tok, int hidden,
+                           int inter, int dtype, void *stream) {
   if (dtype != SPK_BF16) return fail(SPK_EUNSUPPORTED, "mlp_gate_lif: bf16 only");
   if (!valid_float_dtype(param_dtype))
     return fail(SPK_EINVAL, "mlp_gate_lif: parameter dtype %d is not a float type", param_dtype);
@@ -298,7 +314,7 @@ extern "C" int spk_mlp_gate_lif(const void *x, const void *w_packed, const void 
   if (!mlp_shape_ok(T, n_tok, hidden, inter))
     return fail(SPK_EUNSUPPORTED, "mlp_gate_lif: T=%d n_tok=%d hidden=%d inter=%d not supported", T,
                 n_tok, hidden, inter);
-  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w_packed) & 15))
+  if ((!nin && (reinterpret_cast<uintptr_t>(x) & 15)) || (reinterpret_cast<uintptr_t>(w_packed) & 15))
     return fail(SPK_EINVAL, "mlp_gate_lif: x and packed weights must be 16-byte aligned");
   if (reinterpret_cast<uintptr_t>(y) & 15)  // (the tile rows go out as 16-byte stores)
     return fail(SPK_EUNSUPPORTED, "mlp_gate_lif: y must be 16-byte aligned");
@@ -308,19 +324,22 @@ extern "C" int spk_mlp_gate_lif(const void *x, const void *w_packed, const void 
   const auto *xp = static_cast<const uint16_t *>(x);
   const auto *wp = static_cast<const mlp::v4u *>(w_packed);
   auto *yp = static_cast<uint16_t *>(y);
-#define SPK_MLP_LAUNCH(KQ, TT)                                                                       \
+  const NormIn none{};
+#define SPK_MLP_LAUNCH1(KQ, TT, NORM)                                                                \
   {                                                                                                \
     static bool attr = false;                                                                      \
     if (!attr) {                                                                                   \
-      if (hipFuncSetAttribute(reinterpret_cast<const void *>(mlp::mlp_gate_lif_kernel<KQ, TT>),     \
+      if (hipFuncSetAttribute(reinterpret_cast<const void *>(mlp::mlp_gate_lif_kernel<KQ, TT, NORM>), \
                               hipFuncAttributeMaxDynamicSharedMemorySize, mlp::kLdsBytes) != hipSuccess) \
         return fail(SPK_EHIP, "mlp_gate_lif: cannot reserve %d bytes of LDS", mlp::kLdsBytes);  \
       attr = true;                                                                                 \
     }                                                                                              \
-    mlp::mlp_gate_lif_kernel<KQ, TT><<<grid, mlp::kThreads, mlp::kLdsBytes, s>>>(                   \
+    mlp::mlp_gate_lif_kernel<KQ, TT, NORM><<<grid, mlp::kThreads, mlp::kLdsBytes, s>>>(             \
         xp, wp, static_cast<const float *>(beta), static_cast<const float *>(threshold), yp, n_tok,  \
-        inter, MG);                                                                                \
+        inter, MG, nin ? *nin : none);                                                             \
   }
+#define SPK_MLP_LAUNCH(KQ, TT)                                                                       \
+  if (nin) SPK_MLP_LAUNCH1(KQ, TT, true) else SPK_MLP_LAUNCH1(KQ, TT, false)
 #define SPK_MLP_CASE(KQ)                                                                             \
   case KQ:                                                                                         \
     if (T == 1) SPK_MLP_LAUNCH(KQ, 1)                                                             \
@@ -337,7 +356,32 @@ extern "C" int spk_mlp_gate_lif(const void *x, const void *w_packed, const void 
   }
 #undef SPK_MLP_CASE
 #undef SPK_MLP_LAUNCH
+#undef SPK_MLP_LAUNCH1
   return check_launch("mlp_gate_lif");
+}
+
+extern "C" int spk_mlp_gate_lif(const void *x, const void *w_packed, const void *beta,
+                                const void *threshold, int param_dtype, void *y, int T, int n_tok,
+                                int hidden, int inter, int dtype, void *stream) {
+  return mlp_gate_launch(x, nullptr, w_packed, beta, threshold, param_dtype, y, T, n_tok, hidden, inter, dtype,
+                         stream);
+}
+
+extern "C" int spk_norm_mlp_gate_lif(const void *h, const void *delta, const void *norm_weight, void *h_out,
+                                     float eps, const void *w_packed, const void *beta, const void *threshold,
+                                     int param_dtype, void *y, int T, int n_tok, int hidden, int inter,
+                                     int dtype, void *stream) {
+  if (!h || !delta || !norm_weight) return fail(SPK_EINVAL, "norm_mlp_gate_lif: null pointer");
+  const auto al = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  if (!al(h) || !al(delta) || !al(norm_weight) || (h_out && !al(h_out)))
+    return fail(SPK_EINVAL, "norm_mlp_gate_lif: h, delta, norm weight and h_out must be 16-byte aligned");
+  if (h_out && (h_out == h || h_out == delta))
+    return fail(SPK_EINVAL, "norm_mlp_gate_lif: h_out must not alias h or delta");
+  if (hidden > 1024) return fail(SPK_EUNSUPPORTED, "norm_mlp_gate_lif: hidden=%d (at most 1024)", hidden);
+  NormIn nin{static_cast<const uint16_t *>(h), static_cast<const uint16_t *>(delta),
+             static_cast<const uint16_t *>(norm_weight), static_cast<uint16_t *>(h_out), eps};
+  return mlp_gate_launch(nullptr, &nin, w_packed, beta, threshold, param_dtype, y, T, n_tok, hidden, inter,
+                         dtype, stream);
 }
 
 }  // namespace spk

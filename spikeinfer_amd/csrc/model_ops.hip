@@ -16,6 +16,7 @@
 // the same projection output.  Compiled with -ffp-contract=off.
 #include "common.hpp"
 #include "lif_math.hpp"
+#include "norm_rows.hpp"
 
 namespace spk {
 
@@ -108,27 +109,6 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(typename Elem<DT>::T *
   for (int v = lane; v < nv; v += 64) norm(hr[v], wr[v], v, r);
 }
 
-// Sum over the wave, the same value in every lane: DPP adds within each row of
-// 16 lanes (pairs, quads, half rows, rows), then the four row sums by readlane.
-__device__ __forceinline__ float wave_sum(float v) {
-  auto dpp = [](float x, int ctrl) -> float {
-    switch (ctrl) {  // the control must be a constant: one instantiation each
-      case 0xB1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
-      case 0x4E: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
-      case 0x141: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));
-      default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));
-    }
-  };
-  v += dpp(v, 0xB1);   // quad_perm [1,0,3,2]
-  v += dpp(v, 0x4E);   // quad_perm [2,3,0,1]
-  v += dpp(v, 0x141);  // row_half_mirror
-  v += dpp(v, 0x140);  // row_mirror
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-  return (r0 + r1) + (r2 + r3);
-}
 
 // add_rmsnorm for rows of at most 64 * kNormRegVecs vectors (hidden 896 at
 // bf16 is 112): every load of the row -- weights, h, delta -- is issued at once

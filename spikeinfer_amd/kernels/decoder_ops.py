@@ -380,6 +380,80 @@ def mlp_gate_lif(x: torch.Tensor, w_packed: torch.Tensor, beta: torch.Tensor,
     return out
 
 
+def _norm_inputs(h, delta, norm_weight, h_out, name):
+    """Checks of the residual-stream inputs of the norm_* GEMMs."""
+    if h.dtype != torch.bfloat16 or delta.dtype != h.dtype or norm_weight.dtype != h.dtype:
+        raise ValueError(f"{name}: h, delta and norm_weight must be bf16")
+    if delta.shape != h.shape or not h.is_contiguous() or not delta.is_contiguous():
+        raise ValueError(f"{name}: h and delta must be contiguous tensors of one shape")
+    if norm_weight.numel() != h.shape[-1] or not norm_weight.is_contiguous():
+        raise ValueError(f"{name}: norm_weight must be contiguous with hidden={h.shape[-1]} entries")
+    if h_out is not None and (h_out.shape != h.shape or h_out.dtype != h.dtype or not h_out.is_contiguous()):
+        raise ValueError(f"{name}: h_out must be a contiguous bf16 tensor shaped like h")
+
+
+def norm_linear_decode(h: torch.Tensor, delta: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                       w_packed: torch.Tensor, bias: torch.Tensor | None = None,
+                       out: torch.Tensor | None = None,
+                       h_out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """``linear_decode(add_rmsnorm(h, delta, norm_weight), w_packed, bias)`` in
+    one launch, without changing ``h``: ``h_out`` (when given) receives ``h +
+    delta``.  ``h``/``delta`` ``[..., K]`` bf16.  Identical values to the two
+    launches; None when the shape is outside the kernel's range."""
+    dev = _lib.require_gpu(h, delta, norm_weight, w_packed, bias, out, h_out)
+    _norm_inputs(h, delta, norm_weight, h_out, "norm_linear_decode")
+    N, K = w_packed.shape
+    if h.shape[-1] != K:
+        raise ValueError(f"norm_linear_decode: h has {h.shape[-1]} columns, the weight {K}")
+    if bias is not None and (bias.numel() != N or bias.dtype != torch.bfloat16):
+        raise ValueError(f"bias must be bf16 with {N} entries")
+    M = h.numel() // K
+    if out is None:
+        out = torch.empty((*h.shape[:-1], N), dtype=h.dtype, device=dev)
+    elif out.numel() != M * N or not out.is_contiguous() or out.dtype != h.dtype:
+        raise ValueError(f"out must be a contiguous bf16 tensor of {M} x {N}")
+    rc = _lib.load().spk_norm_linear_decode(
+        h.data_ptr(), delta.data_ptr(), norm_weight.data_ptr(), _lib.ptr(h_out), float(eps),
+        w_packed.data_ptr(), bias.contiguous().data_ptr() if bias is not None else None, out.data_ptr(),
+        M, N, K, _lib.dtype_code(h.dtype), _lib.stream_of(dev))
+    if rc == _lib.SPK_EUNSUPPORTED:
+        return None
+    _lib.check(rc, "norm_linear_decode")
+    return out
+
+
+def norm_mlp_gate_lif(h: torch.Tensor, delta: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                      w_packed: torch.Tensor, beta: torch.Tensor, threshold: torch.Tensor,
+                      out: torch.Tensor | None = None,
+                      h_out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """``mlp_gate_lif(add_rmsnorm(h, delta, norm_weight), ...)`` in one launch,
+    without changing ``h``: ``h_out`` (when given) receives ``h + delta``.
+    ``h``/``delta`` ``[T, n_tok, hidden]`` bf16.  Identical values to the two
+    launches; None when the shape is outside the kernel's range."""
+    dev = _lib.require_gpu(h, delta, norm_weight, w_packed, beta, threshold, out, h_out)
+    _norm_inputs(h, delta, norm_weight, h_out, "norm_mlp_gate_lif")
+    if h.ndim != 3:
+        raise ValueError("norm_mlp_gate_lif: h must be [T, n_tok, hidden]")
+    T, n, hidden = h.shape
+    I = beta.numel()
+    if threshold.numel() != I or w_packed.numel() * w_packed.element_size() != 4 * I * hidden:
+        raise ValueError(f"packed weight / beta / threshold do not match hidden={hidden}, I={I}")
+    if out is None:
+        out = torch.empty((T, n, I), dtype=h.dtype, device=dev)
+    elif tuple(out.shape) != (T, n, I) or not out.is_contiguous() or out.dtype != h.dtype:
+        raise ValueError(f"out must be contiguous bf16 [{T}, {n}, {I}]")
+    beta = beta.float().contiguous()
+    threshold = threshold.float().contiguous()
+    rc = _lib.load().spk_norm_mlp_gate_lif(
+        h.data_ptr(), delta.data_ptr(), norm_weight.data_ptr(), _lib.ptr(h_out), float(eps),
+        w_packed.data_ptr(), beta.data_ptr(), threshold.data_ptr(), _lib.dtype_code(beta.dtype),
+        out.data_ptr(), T, n, hidden, I, _lib.dtype_code(h.dtype), _lib.stream_of(dev))
+    if rc == _lib.SPK_EUNSUPPORTED:
+        return None
+    _lib.check(rc, "norm_mlp_gate_lif")
+    return out
+
+
 def decode_advance(next_tokens, input_ids, positions, seq_lens, slot_mapping, block_tables,
                    block_size: int, n_rows: int, live=None, history=None, step=None,
                    rng_seeds=None, uniforms=None) -> None:

@@ -13,10 +13,14 @@ MI355X layout of a layer:
     decode tokens);
   * gate and up are one GEMM on ``[2 I, hidden]``; one HIP kernel applies the
     gate LIF and the product with up;
-  * each residual add is fused into the RMSNorm that follows it; the final
-    norm is fused with the rate-coded mean over T.
-GEMMs go to hipBLASLt through torch.  Weights load from the reference's
-parameter names (:meth:`SpikingDecoder.load_reference_state_dict`).
+  * each residual add is fused into the RMSNorm that follows it, and at
+    decode sizes both into the GEMM that consumes the norm's output; the
+    final norm is fused with the rate-coded mean over T.
+At decode sizes the GEMMs are this package's kernels (linear_decode,
+mlp_gate_lif, and the norm_* variants that also compute the residual add +
+RMSNorm feeding them); larger batches (prefill) use torch's library GEMMs.
+Weights load from the reference's parameter names
+(:meth:`SpikingDecoder.load_reference_state_dict`).
 """
 from __future__ import annotations
 
@@ -28,8 +32,8 @@ import torch.nn.functional as F
 
 from .attention import AttentionMetadata
 from .kernels.decoder_ops import (add_rmsnorm, embed_rmsnorm, lif_gate_mul, linear_decode,
-                                  mlp_gate_lif, pack_gate_up, pack_linear, qkv_decode_attention,
-                                  qkv_rope_lif_pack, rmsnorm_mean_t)
+                                  mlp_gate_lif, norm_linear_decode, norm_mlp_gate_lif, pack_gate_up,
+                                  pack_linear, qkv_decode_attention, qkv_rope_lif_pack, rmsnorm_mean_t)
 from .kernels.packing import packed_width
 from .kernels.spike_attention import gather_kv_unpacked_pair, paged_spike_attn_decode
 
@@ -116,6 +120,14 @@ class SpikingDecoder:
         # rows (T * tokens): beyond, the library GEMM is faster.
         self.small_linear = True
         self.small_down_max_rows = 128
+        # True folds each residual add + RMSNorm into the GEMM that consumes
+        # its output (norm_linear_decode for q/k/v, norm_mlp_gate_lif for the
+        # MLP): two launches fewer a layer, identical values, the residual
+        # stream alternating between two buffers.  Off: every workgroup of a
+        # row group recomputes its rows' norm (64 column ranges share a row
+        # group), which costs more than the launches it saves (config 5: 2.28
+        # against 1.63 ms a step).
+        self.fused_norm = False
         self._pack_mlp()
         # Rotary inverse frequencies as Qwen2RotaryEmbedding builds them (fp32, host).
         exps = torch.arange(0, self.D, 2, dtype=torch.int64).float() / self.D
@@ -226,11 +238,21 @@ class SpikingDecoder:
                      torch.empty((T, Hkv, n, D), dtype=self.dtype, device=h.device),
                      torch.empty((T, Hkv, n, D), dtype=self.dtype, device=h.device))
         delta = None
+        fold = (self.fused_norm and self.small_linear and n <= self.fused_mlp_max_tokens
+                and self.dtype == torch.bfloat16)
+        h_alt = torch.empty_like(h) if fold else None  # the other residual buffer
         for i, L in enumerate(self.layers):
-            if i:
-                x = add_rmsnorm(h, delta, L.input_norm, c.rms_norm_eps, out=x)
             k_cache, v_cache = kv_caches[i]
-            qkv = self._linear(x, L.w_qkv, L.b_qkv, L.w_qkv_packed, n)
+            qkv = None
+            if i and fold and L.w_qkv_packed is not None:
+                qkv = norm_linear_decode(h, delta, L.input_norm, c.rms_norm_eps, L.w_qkv_packed, L.b_qkv,
+                                         h_out=h_alt)
+                if qkv is not None:
+                    h, h_alt = h_alt, h
+            if qkv is None:
+                if i:
+                    x = add_rmsnorm(h, delta, L.input_norm, c.rms_norm_eps, out=x)
+                qkv = self._linear(x, L.w_qkv, L.b_qkv, L.w_qkv_packed, n)
             fused = (self.fused_attention and not meta.num_prefills and n_dec == n and
                      qkv_decode_attention(qkv, self.rope_cos, self.rope_sin, positions, L.lif_qkv_beta,
                                           L.lif_qkv_th, k_cache, v_cache, meta.slot_mapping,
@@ -247,9 +269,15 @@ class SpikingDecoder:
             if meta.num_prefills:
                 self._prefill_attention(dense, k_cache, v_cache, meta, attn)
             o = self._linear(attn.view(T, n, Hq * D), L.w_o, None, L.w_o_packed, n)
-            x = add_rmsnorm(h, o, L.post_norm, c.rms_norm_eps, out=x)
             y = None
-            if self.fused_mlp and L.w_gu_packed is not None and n <= self.fused_mlp_max_tokens:
+            if fold and self.fused_mlp and L.w_gu_packed is not None:
+                y = norm_mlp_gate_lif(h, o, L.post_norm, c.rms_norm_eps, L.w_gu_packed, L.lif_gate_beta,
+                                      L.lif_gate_th, h_out=h_alt)
+                if y is not None:
+                    h, h_alt = h_alt, h
+            if y is None:
+                x = add_rmsnorm(h, o, L.post_norm, c.rms_norm_eps, out=x)
+            if y is None and self.fused_mlp and L.w_gu_packed is not None and n <= self.fused_mlp_max_tokens:
                 y = mlp_gate_lif(x, L.w_gu_packed, L.lif_gate_beta, L.lif_gate_th)
             if y is None:
                 y = lif_gate_mul(F.linear(x, L.w_gu), L.lif_gate_beta, L.lif_gate_th)

@@ -214,3 +214,18 @@ def test_request_seeds_as_int64():
     assert seed_as_int64(2 ** 64 - 1) == -1
     assert seed_as_int64(2 ** 64 + 5) == 5
     assert seed_as_int64(-1) == -1
+
+
+def test_norm_gemms_validate_on_the_host():
+    """The norm_* GEMM entry points refuse null inputs, misalignment and an
+    h_out aliasing h before launching anything."""
+    lib = _lib.load()
+    bf16, f32 = _lib.SPK_BF16, _lib.SPK_F32
+    A = 4096  # a 16-byte aligned stand-in address (never dereferenced)
+    assert lib.spk_norm_linear_decode(None, A, A, A, 1e-6, A, None, A, 64, 1152, 896, bf16, None) == _lib.SPK_EINVAL
+    assert lib.spk_norm_linear_decode(A, A + 16, A, A, 1e-6, A, None, A, 64, 1152, 896, bf16, None) == _lib.SPK_EINVAL
+    assert b"alias" in lib.spk_last_error()
+    assert lib.spk_norm_linear_decode(A, A + 16, A, A + 8, 1e-6, A, None, A, 64, 1152, 896, bf16, None) == _lib.SPK_EINVAL
+    assert lib.spk_norm_linear_decode(A, A, A, None, 1e-6, A, None, A, 64, 1152, 1280, bf16, None) == _lib.SPK_EUNSUPPORTED
+    assert lib.spk_norm_mlp_gate_lif(A, A + 16, A, A, 1e-6, A, A, A, f32, A, 4, 8, 896, 4864, bf16, None) == _lib.SPK_EINVAL
+    assert lib.spk_norm_mlp_gate_lif(None, A, A, None, 1e-6, A, A, A, f32, A, 4, 8, 896, 4864, bf16, None) == _lib.SPK_EINVAL

@@ -652,3 +652,57 @@ def test_runner_replay_recaptures_when_sampler_stages_change(gpu):
         eager._step()
     torch.cuda.synchronize()
     assert torch.equal(runner.history[:n, :new], eager.history[:n, :new])
+
+
+@pytest.mark.parametrize("M,N,bias", [(256, 1152, True), (4, 1152, True), (130, 896, False), (64, 896, False)])
+def test_norm_linear_decode_equals_add_rmsnorm_then_linear(gpu, M, N, bias):
+    """The GEMM with the residual add + RMSNorm in its prologue against
+    add_rmsnorm followed by linear_decode: identical y and identical h + delta
+    (in h_out; h itself unchanged)."""
+    from spikeinfer_amd.kernels.decoder_ops import add_rmsnorm, linear_decode, norm_linear_decode, pack_linear
+
+    K = 896
+    print(f"norm_linear_decode M={M} N={N}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(M * 7 + N)
+    h = torch.randn((M, K), generator=g, device=gpu).bfloat16()
+    d = (torch.randn((M, K), generator=g, device=gpu) * 0.5).bfloat16()
+    w = (1.0 + 0.1 * torch.randn(K, generator=g, device=gpu)).bfloat16()
+    wp = pack_linear((torch.randn((N, K), generator=g, device=gpu) * 0.05).bfloat16())
+    b = (torch.randn(N, generator=g, device=gpu) * 0.1).bfloat16() if bias else None
+    h0 = h.clone()
+    h_out = torch.full_like(h, float("nan"))
+    y = norm_linear_decode(h, d, w, 1e-6, wp, b, h_out=h_out)
+    h_ref = h0.clone()
+    x = add_rmsnorm(h_ref, d, w, 1e-6)
+    want = linear_decode(x, wp, b)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h0), "h changed"
+    assert torch.equal(h_out, h_ref), "h_out != h + delta"
+    assert torch.equal(y, want)
+
+
+@pytest.mark.parametrize("T,n", [(4, 64), (4, 5), (1, 33), (3, 17)])
+def test_norm_mlp_gate_lif_equals_add_rmsnorm_then_mlp(gpu, T, n):
+    """The fused MLP gate with the residual add + RMSNorm in its prologue
+    against add_rmsnorm followed by mlp_gate_lif: identical outputs."""
+    from spikeinfer_amd.kernels.decoder_ops import add_rmsnorm, mlp_gate_lif, norm_mlp_gate_lif, pack_gate_up
+
+    H, I = 896, 4864
+    print(f"norm_mlp_gate_lif T={T} n={n}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(T * 100 + n)
+    h = torch.randn((T, n, H), generator=g, device=gpu).bfloat16()
+    d = (torch.randn((T, n, H), generator=g, device=gpu) * 0.5).bfloat16()
+    w = (1.0 + 0.1 * torch.randn(H, generator=g, device=gpu)).bfloat16()
+    wp = pack_gate_up((torch.randn((2 * I, H), generator=g, device=gpu) * 0.05).bfloat16())
+    beta = 0.6 + 0.4 * torch.rand(I, generator=g, device=gpu)
+    th = 0.2 + 0.5 * torch.rand(I, generator=g, device=gpu)
+    h0 = h.clone()
+    h_out = torch.empty_like(h)
+    y = norm_mlp_gate_lif(h, d, w, 1e-6, wp, beta, th, h_out=h_out)
+    h_ref = h0.clone()
+    want = mlp_gate_lif(add_rmsnorm(h_ref, d, w, 1e-6), wp, beta, th)
+    torch.cuda.synchronize()
+    assert y is not None and torch.equal(h, h0)
+    assert torch.equal(h_out, h_ref)
+    assert torch.equal(y, want)
+    assert int((y != 0).sum()) > 0
