@@ -582,19 +582,24 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   // so every slot is.
   const int last_pair = (end - 1) & ~1;
   // Element offset (in u64 words / W64) of the pair's first slot.
-  auto slot_of = [&](int j) -> uint64_t {
+  // Byte offset of the pair's words in its (t, kv head) slab (the host keeps
+  // every slab under 4 GiB, so offsets are 32-bit and the loads are buffer
+  // loads from a scalar base: no 64-bit address arithmetic per step).
+  constexpr int kSlotShift = W64 == 1 ? 3 : 4;  // log2(bytes per token)
+  auto slot_of = [&](int j) -> uint32_t {
     const int jj = min(j, last_pair);
     const uint32_t phys = static_cast<uint32_t>(blocks[(jj - start) >> p.bs_log2]);
-    return (static_cast<uint64_t>(phys) << p.bs_log2) | static_cast<uint64_t>(jj & bs_mask);
+    return ((phys << p.bs_log2) | static_cast<uint32_t>(jj & bs_mask)) << kSlotShift;
   };
-  auto issue = [&](uint64_t slot, uint64_t (&kw)[2][W64], uint64_t (&vw)[2][W64]) {
+  const auto krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t *>(kbase), 0, 0x7fffffff, 0x00020000);
+  const auto vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t *>(vbase), 0, 0x7fffffff, 0x00020000);
+  auto issue = [&](uint32_t off, uint64_t (&kw)[2][W64], uint64_t (&vw)[2][W64]) {
     typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
-    const v2u64 *kp = reinterpret_cast<const v2u64 *>(kbase + slot * W64);
-    const v2u64 *vp = reinterpret_cast<const v2u64 *>(vbase + slot * W64);
 #pragma unroll
     for (int i = 0; i < W64; ++i) {  // u64 2i, 2i+1 of the pair: token (2i+c)/W64, word (2i+c)%W64
-      const v2u64 k2 = __builtin_nontemporal_load(kp + i);
-      const v2u64 v2 = __builtin_nontemporal_load(vp + i);
+      // aux 2: the nontemporal hint of the earlier global loads
+      const v2u64 k2 = __builtin_bit_cast(v2u64, __builtin_amdgcn_raw_buffer_load_b128(krs, off + 16 * i, 0, 2));
+      const v2u64 v2 = __builtin_bit_cast(v2u64, __builtin_amdgcn_raw_buffer_load_b128(vrs, off + 16 * i, 0, 2));
       kw[(2 * i) / W64][(2 * i) % W64] = k2.x;
       kw[(2 * i + 1) / W64][(2 * i + 1) % W64] = k2.y;
       vw[(2 * i) / W64][(2 * i) % W64] = v2.x;
@@ -693,7 +698,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   // waits behind this step's LDS traffic).
   auto none = [] {};
   int i = 0;
-  uint64_t snext = ntotal > 0 ? slot_of(first + 2 * kStride + lo) : 0;
+  uint32_t snext = ntotal > 0 ? slot_of(first + 2 * kStride + lo) : 0;
   for (; i + 2 <= nfull; i += 2) {
     // Waves with more steps left issue first (s_setprio): the longer units of
     // a CU's mix keep their pace as it drains.  Measured: config 4 119.2 ->
@@ -845,6 +850,8 @@ bool mfma_path_supported(const AttnParams &p) {
          p.ks2 == w32 && p.vs2 == w32 &&
          (p.ks0 % 4) == 0 && (p.ks1 % 4) == 0 && (p.vs0 % 4) == 0 && (p.vs1 % 4) == 0 &&
          al16(p.k) && al16(p.v) &&
+         // a (t, kv head) slab within the 2 GiB of the kernel's buffer loads
+         p.num_slots <= (int64_t(0x7fffffff) >> (p.head_dim == 64 ? 3 : 4)) &&
          ((p.part_len + (1 << p.bs_log2) - 1) >> p.bs_log2) <= mfma::kMaxPartBlocks;
 }
 
