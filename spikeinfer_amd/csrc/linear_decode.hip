@@ -43,7 +43,7 @@ constexpr int kMaxPartSteps = 5;     // k-steps per part: K <= 8 * 5 * 32 = 1280
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int kSlotFloats = 4 * 4 * 64;  // one partial: 4 row tiles x 4 x 64 lanes
 constexpr int kStageOff = kWaves * kMaxUnitsPerWave * kSlotFloats * 4;  // y staging, after the slots
-constexpr int kStageBytes = 64 * 16 * 2;                               // one wave's 64 x 16 tile
+constexpr int kStageBytes = 16 * 16 * 2;                               // one wave's 16 x 16 tile
 static_assert(kStageOff + kWaves * kStageBytes <= kLdsBytes, "slots and staging fit the LDS");
 
 // Packed W (spk_linear_pack): for tile p (rows 16p..16p+15 of W) and k-step
@@ -67,6 +67,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   if (np <= 0) return;  // uniform over the workgroup
   const int m0 = m * kRows;
 
+  // The bias of the epilogue's columns, loaded first (its latency hides under
+  // the whole launch).
+  float bv[kMaxUnitsPerWave];
+#pragma unroll
+  for (int e = 0; e < kMaxUnitsPerWave; ++e)
+    bv[e] = bias ? elem_to_f32<SPK_BF16>(bias[16 * (p0 + min(e, np - 1)) + (lane & 15)]) : 0.f;
   // Units (tile, part): wave w takes units w and w + 8 (np <= 2 tiles).
   const int U = np * kParts;
   auto part_range = [&](int part, int &k0, int &k1) {
@@ -152,40 +158,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   }
   __syncthreads();
 
-  // Epilogue: wave e < np sums tile p0 + e's eight parts in order, adds the
-  // bias and writes y (fp32 sum + bias, rounded once, as the GEMM epilogue).
-  if (wave >= np) return;
-  float sum[4][4];
+  // Epilogue: wave w finishes row tile w % 4 of tile p0 + w / 4 (w / 4 < np),
+  // summing its eight parts in order, adding the bias (loaded at the start)
+  // and writing y (fp32 sum + bias, rounded once, as the GEMM epilogue).
+  const int et = wave & 3, ee = wave >> 2;
+  if (ee >= np) return;
+  float sum[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int i = 0; i < 4; ++i) sum[i] = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sum[t][i] = 0.f;
   for (int part = 0; part < kParts; ++part) {
-    const v4f *d = slots + (wave * kParts + part) * (kSlotFloats / 4);
+    const v4f a = slots[(ee * kParts + part) * (kSlotFloats / 4) + et * 64 + lane];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const v4f a = d[t * 64 + lane];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sum[t][i] += a[i];
-    }
+    for (int i = 0; i < 4; ++i) sum[i] += a[i];
   }
-  const int col = 16 * (p0 + wave) + r16;
-  const float bv = bias ? elem_to_f32<SPK_BF16>(bias[col]) : 0.f;
-  // The tile (64 rows x 16 columns, bf16) is staged in the wave's 2 KB above
-  // the partial slots; each row's 32 bytes then go out as two 16-byte stores.
+  // The 16 x 16 bf16 tile is staged in the wave's 512 bytes above the
+  // partial slots; its rows' 32 bytes then go out as two 16-byte stores.
   uint16_t *stg = reinterpret_cast<uint16_t *>(smem + kStageOff + wave * kStageBytes);
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) stg[(16 * t + 4 * kq + i) * 16 + r16] = f32_to_elem<SPK_BF16>(sum[t][i] + bv);
+  for (int i = 0; i < 4; ++i) stg[(4 * kq + i) * 16 + r16] = f32_to_elem<SPK_BF16>(sum[i] + bv[ee]);
   wave_lds_sync();  // lanes read rows other lanes wrote
-  const int row = m0 + lane;  // row `lane` of the tile
-  if (row < M) {
-    const v4u *src = reinterpret_cast<const v4u *>(stg + lane * 16);
-    const v4u lo = src[0], hi = src[1];
-    v4u *dst = reinterpret_cast<v4u *>(y + static_cast<int64_t>(row) * N + 16 * (p0 + wave));
-    dst[0] = lo;
-    dst[1] = hi;
+  const int row = m0 + 16 * et + (lane >> 1);  // lane pair -> one row
+  if (lane < 32 && row < M) {
+    const v4u v = reinterpret_cast<const v4u *>(stg)[lane];
+    reinterpret_cast<v4u *>(y + static_cast<int64_t>(row) * N + 16 * (p0 + ee))[lane & 1] = v;
   }
 }
 
