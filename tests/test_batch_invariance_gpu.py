@@ -126,8 +126,10 @@ def test_runner_tokens_alone_and_in_batch(gpu, sampling):
     seeded top-k sampling, whose per-request generators draw the same
     uniforms whatever the batch).  Every stage is batch-invariant: prefill
     runs prompt by prompt, the decode GEMMs split K the same way at any row
-    count, attention sums a sequence's tokens in an order fixed by its own
-    length, norms and the sampler work per row."""
+    count (while the routing below keeps them on this library's kernels:
+    T * rows <= small_down_max_rows for the down projection), attention sums
+    a sequence's tokens in an order fixed by its own length, norms and the
+    sampler work per row."""
     from spikeinfer_amd.runner import DecodeRunner
     from spikeinfer_amd.sampler import SamplingParams
     from spikeinfer_amd.spike_cache import PagedSpikeCache
@@ -150,3 +152,59 @@ def test_runner_tokens_alone_and_in_batch(gpu, sampling):
     together = runner.generate(prompts, [params(i) for i in range(len(prompts))], new, shuffle_blocks=99)
     for i in range(len(prompts)):
         assert torch.equal(together[i], alone[i]), f"prompt {i}: {together[i].tolist()} vs {alone[i].tolist()}"
+
+
+def test_runner_one_bucket_invariant_through_library_gemm(gpu):
+    """Past small_down_max_rows the down projection is the library GEMM, whose
+    kernel depends on the row count.  A runner whose only graph bucket is its
+    batch size runs every step at that row count (rows past the live ones
+    read the pad block), so a prompt alone and in the batch still give the
+    same tokens.  Routing forced here: every step's down projection goes to
+    the library GEMM."""
+    from spikeinfer_amd.runner import DecodeRunner
+    from spikeinfer_amd.sampler import SamplingParams
+    from spikeinfer_amd.spike_cache import PagedSpikeCache
+
+    m = _small_model(gpu, seed=81)
+    m.small_down_max_rows = 0
+    g = torch.Generator().manual_seed(82)
+    lens = (9, 30, 17, 4)
+    prompts = [torch.randint(0, 1024, (L,), generator=g).tolist() for L in lens]
+    new = 8
+    runner = DecodeRunner(m, PagedSpikeCache(2, m.T, m.Hkv, m.D, 64, 16, device=gpu), batch_size=len(prompts),
+                          max_model_len=max(lens) + new + 1, max_new_tokens=16, buckets=())
+    assert runner.buckets == (len(prompts),)
+    print("runner invariance: one bucket, library down projection", flush=True)
+    greedy = SamplingParams(temperature=0.0)
+    alone = [runner.generate([p], [greedy], new, shuffle_blocks=i)[0] for i, p in enumerate(prompts)]
+    together = runner.generate(prompts, [greedy] * len(prompts), new, shuffle_blocks=99)
+    for i in range(len(prompts)):
+        assert torch.equal(together[i], alone[i]), f"prompt {i}: {together[i].tolist()} vs {alone[i].tolist()}"
+
+
+def test_down_projection_routing_switch_is_within_one_ulp(gpu):
+    """Where the bucket's row count crosses small_down_max_rows (config-5
+    shapes: K = 4864, N = 896), one token's down projection moves from this
+    library's long-K kernel (4 rows alone) to the library GEMM (256 rows in
+    a batch of 64).  The two may round a sum differently; this bounds that:
+    every element of both is within 1 bf16 ulp of the fp64 product, so the
+    two differ by at most one rounding step."""
+    import torch.nn.functional as F
+    from spikeinfer_amd.kernels.decoder_ops import linear_decode, pack_linear
+
+    T, n, K, N = 4, 64, 4864, 896
+    g = torch.Generator(device=gpu).manual_seed(91)
+    y = torch.randn((T, n, K), generator=g, device=gpu).bfloat16()
+    w = (torch.randn((N, K), generator=g, device=gpu) * 0.02).bfloat16()
+    batch = F.linear(y, w)  # 256 rows: the library GEMM
+    wp = pack_linear(w)
+    want = (y.double() @ w.double().t())
+    for tok in (0, 17, 63):
+        print(f"down projection switch: token {tok}", flush=True)
+        alone = linear_decode(y[:, tok:tok + 1].contiguous(), wp, None)  # 4 rows: the long-K kernel
+        torch.cuda.synchronize()
+        ref = want[:, tok:tok + 1].to(torch.bfloat16).float()
+        bound = ref.abs() * 2.0 ** -7 + 1e-6
+        assert bool(((alone.float() - ref).abs() <= bound).all())
+        assert bool(((batch[:, tok:tok + 1].float() - ref).abs() <= bound).all())
+        assert bool(((alone.float() - batch[:, tok:tok + 1].float()).abs() <= 2 * bound).all())
