@@ -14,7 +14,7 @@ the decode queries), so dense q/k/v spikes are never materialised for decode tok
 """
 from __future__ import annotations
 
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import torch
 import torch.nn.functional as F
@@ -48,9 +48,29 @@ class AttentionMetadata:
     prefill_context_lens: list[int] = field(default_factory=list)
     prefill_block_tables: list[torch.Tensor] = field(default_factory=list)
 
+    # device -> copy of this metadata there (see on()); not part of equality
+    _copies: dict = field(default_factory=dict, repr=False, compare=False)
+
     @property
     def num_prefills(self) -> int:
         return len(self.prefill_query_lens)
+
+    def on(self, device: torch.device | str) -> "AttentionMetadata":
+        """The same metadata with its index tensors on ``device``
+        (spikeinfer/attention.py:62-95): ``self`` when ``slot_mapping`` is
+        already there, otherwise a copy made once per device and kept on this
+        object (metadata is rebuilt every step, so the copies live one step)."""
+        device = torch.device(device)
+        if self.slot_mapping.device == device:
+            return self
+        key = str(device)
+        if key not in self._copies:
+            move = lambda t: None if t is None else t.to(device, non_blocking=True)
+            self._copies[key] = replace(
+                self, slot_mapping=move(self.slot_mapping), block_tables=move(self.block_tables),
+                seq_lens=move(self.seq_lens),
+                prefill_block_tables=[move(t) for t in self.prefill_block_tables], _copies={})
+        return self._copies[key]
 
 
 def _causal_offset_mask(query_len: int, total_len: int, device, dtype) -> torch.Tensor:

@@ -60,3 +60,26 @@ def test_paged_attention_refuses_cpu_tensors():
     spk = torch.zeros(4, 1, 2, 1, 64)
     with pytest.raises(ValueError, match="GPU"):
         paged_attention(torch.zeros(4, 1, 14, 1, 64), spk, spk, c.k[0], c.v[0], meta, 14, 2, 64)
+
+
+def test_attention_metadata_on_device():
+    """AttentionMetadata.on (spikeinfer/attention.py:62-95): the object itself
+    when its tensors are already on the device; otherwise one copy per device,
+    made once, with every index tensor moved and the plain fields shared."""
+    import torch
+    from spikeinfer_amd.attention import AttentionMetadata
+
+    meta = AttentionMetadata(slot_mapping=torch.arange(5), block_size=16, num_decode_tokens=2,
+                             block_tables=torch.zeros((2, 3), dtype=torch.int32),
+                             seq_lens=torch.tensor([3, 7], dtype=torch.int32),
+                             prefill_query_starts=[2], prefill_query_lens=[3], prefill_context_lens=[0],
+                             prefill_block_tables=[torch.tensor([4], dtype=torch.int32)])
+    assert meta.on(torch.device("cpu")) is meta
+    assert meta.on("cpu") is meta
+    moved = meta.on("meta")
+    assert moved is not meta and meta.on(torch.device("meta")) is moved
+    assert moved.slot_mapping.device.type == "meta" and moved.block_tables.device.type == "meta"
+    assert moved.seq_lens.device.type == "meta" and moved.prefill_block_tables[0].device.type == "meta"
+    assert (moved.block_size, moved.num_decode_tokens, moved.prefill_query_lens) == (16, 2, [3])
+    assert moved.on("meta") is moved
+    assert meta.slot_mapping.device.type == "cpu"  # the original is untouched
