@@ -8,17 +8,19 @@ carried as one ``[T, n_tok, hidden]`` tensor so every GEMM has M = T * n_tok
 
 MI355X layout of a layer:
   * q/k/v projections are one GEMM on the concatenated weight ``[(Hq + 2 Hkv)
-    D, hidden]``; its output feeds one HIP kernel doing RoPE -> LIF -> pack and
-    writing k/v straight into their cache slots (no dense q/k/v spikes for
-    decode tokens);
-  * gate and up are one GEMM on ``[2 I, hidden]``; one HIP kernel applies the
-    gate LIF and the product with up;
-  * each residual add is fused into the RMSNorm that follows it, and at
-    decode sizes both into the GEMM that consumes the norm's output; the
-    final norm is fused with the rate-coded mean over T.
+    D, hidden]``; at decode its output feeds the attention kernel itself
+    (qkv_decode_attention: RoPE -> LIF -> pack of its heads, k/v written to
+    their cache slots, then the decode attention), at prefill one kernel doing
+    RoPE -> LIF -> pack and the cache write;
+  * gate and up are one GEMM on ``[2 I, hidden]`` fused with the gate LIF and
+    the product with up (mlp_gate_lif) at decode sizes;
+  * each residual add is fused into the RMSNorm that follows it; the final
+    norm is fused with the rate-coded mean over T.  (``fused_norm`` also moves
+    the add + norm into the prologue of the GEMM that consumes it; it is off
+    by default, being slower.)
 At decode sizes the GEMMs are this package's kernels (linear_decode,
-mlp_gate_lif, and the norm_* variants that also compute the residual add +
-RMSNorm feeding them); larger batches (prefill) use torch's library GEMMs.
+mlp_gate_lif), except the down projection above ``small_down_max_rows``
+rows; larger batches (prefill) use torch's library GEMMs.
 Weights load from the reference's parameter names
 (:meth:`SpikingDecoder.load_reference_state_dict`).
 """
