@@ -924,15 +924,20 @@ void launch_decode_mfma(AttnParams p, bool plan, int32_t *order, hipStream_t s, 
   dim3 grid(units, p.num_parts);
   p.order = nullptr;
   p.plan_inline = 0;
+  const bool pairs = !two && fused_dtype == 0 && p.head_dim == 64;  // as PAIRS in the kernel
+  // A planned launch whose table holds at most kPairMaxLen tokens has only
+  // paired items: ceil(T * Hkv / 2) workgroups each, no more.
+  const int planned_blocks = pairs && p.ctx_cap <= kPairMaxLen
+                                 ? p.N * p.num_parts * ((p.T * p.Hkv + 1) / 2)
+                                 : units * p.num_parts;
   if (plan && !order) {
     p.plan_inline = 1;
-    grid = dim3(units * p.num_parts);
+    grid = dim3(planned_blocks);
   } else if (plan) {
-    const bool pairs = !two && fused_dtype == 0 && p.head_dim == 64;  // as PAIRS in the kernel
     mfma::decode_attn_plan<<<1, 1024, 0, s>>>(p.lens, p.ctx_cap, p.N, p.T * p.Hkv, p.part_len, p.num_parts,
                                               pairs ? 1 : 0, order);
     p.order = order;
-    grid = dim3(units * p.num_parts);
+    grid = dim3(planned_blocks);
   }
 #define SPK_NREP_CASES(XDT, W64, KW)                                                              \
   switch (p.nrep) {                                                                               \
