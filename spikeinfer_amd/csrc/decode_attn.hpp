@@ -103,11 +103,14 @@ inline int choose_part_len(int block_size) {
 // Matrix-core path for head_dim 64, n_rep <= 8 (decode_attn_mfma.hip).
 // Returns false when the shape or alignment does not qualify.
 bool mfma_path_supported(const AttnParams &p);
-// Long contexts (plan_launch) are launched longest first.  Up to
-// kInlinePlanItems (sequence, partition) items the main kernel orders them
-// itself; beyond, a planner kernel first writes the order into `order`
-// (items + 1 ints of workspace, plan_in_workspace).
-inline bool plan_launch(int64_t ctx_max) { return ctx_max >= 8192; }
+// Contexts from 3072 tokens (table capacity, plan_launch) are launched
+// longest first.  Up to kInlinePlanItems (sequence, partition) items the main
+// kernel orders them itself; beyond, a planner kernel first writes the order
+// into `order` (items + 1 ints of workspace, plan_in_workspace).  Below the
+// threshold the plan's prologue costs more than the order gains (measured:
+// ragged contexts up to 2000 tokens 15.2 -> 16.7 us with a plan, up to 4000
+// 24.1 -> 22.1 us).
+inline bool plan_launch(int64_t ctx_max) { return ctx_max >= 3072; }
 constexpr int kInlinePlanItems = 4096;
 // SPIKEINFER_AMD_ATTN_PLAN=workspace forces the planner kernel for any
 // planned launch (tests check that both orders give the same bytes).
