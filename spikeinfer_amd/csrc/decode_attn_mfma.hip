@@ -249,10 +249,13 @@ __device__ __forceinline__ void mma_ops(const StepOps<W64> &o, v4f (&acc)[2][4 *
 // kMaxBuckets + 10 ints and is free again after the call.
 constexpr int kMaxBuckets = 2 * 130;  // (steps per wave in 256-token units + 2) x paired
 constexpr int kPlanKeys = 8;          // per-thread item keys kept in registers between the passes
-// Bucket of an item of `size` tokens (size <= 0: bucket 0, nothing to do).
+// Bucket of an item of `size` tokens.  An empty item (size <= 0: nothing to
+// sum, zeros out) is paired whenever pairs are on, so no item takes more than
+// ceil(ups / 2) blocks when every item is short (the host sizes such a grid
+// to N * num_parts * ceil(ups / 2)).
 template <bool PAIRS>
 __device__ __forceinline__ int plan_bucket(int size) {
-  if (size <= 0) return 0;
+  if (size <= 0) return PAIRS ? 1 : 0;
   const bool paired = PAIRS && size <= kPairMaxLen;
   const int eff = paired ? 2 * size : size;
   return 2 * (((eff + 255) >> 8) + 1) + (paired ? 1 : 0);

@@ -165,6 +165,43 @@ def test_long_context_launch_order_over_ragged_batches(n, gpu):
     _check(_run(case, gpu), oracle_attn(case), f"ragged n={n}")
 
 
+@pytest.mark.parametrize("T,q_heads,kv_heads", [(3, 7, 1), (4, 14, 2), (1, 8, 8)])
+def test_planned_short_contexts_pair_mode(T, q_heads, kv_heads, gpu):
+    """Tables of 3072..8192 tokens: the launch is planned (longest first) and
+    its items, all of at most 8192 tokens, run as pairs of 2-wave units in
+    4-wave workgroups (an odd T * Hkv leaves the last pair half empty);
+    ragged and empty sequences."""
+    rng = np.random.default_rng(T * 100 + q_heads)
+    lens = rng.integers(0, 4000, 37)
+    lens[[3, 9]] = 0
+    lens[5] = 4096
+    case = attn_case(lens.tolist(), block_size=16, T=T, q_heads=q_heads, kv_heads=kv_heads,
+                     density=0.2, q_density=0.2, seed=T + q_heads, compact=True)
+    _check(_run(case, gpu), oracle_attn(case), f"planned short T={T} H={q_heads}/{kv_heads}")
+
+
+@pytest.mark.parametrize("lens,T,q_heads,kv_heads", [
+    ([0, 3500, 0, 17, 4096, 1], 4, 14, 2),     # planned, all items short: pairs, grid of ceil(ups/2)
+    ([0, 3500, 0, 17, 4096, 1], 3, 7, 1),      # odd T * Hkv: the last pair half empty
+    ([0, 9000, 0, 17, 300], 2, 8, 2),          # planned, short and long items
+    ([0, 100, 0, 17], 4, 14, 2),               # unplanned short launch
+    ([0, 0, 0], 1, 4, 4),                      # nothing but empty sequences
+])
+def test_every_output_written(lens, T, q_heads, kv_heads, gpu):
+    """`out` pre-filled with NaN: every (t, sequence, head) row is written,
+    empty sequences included (zeros), in every launch shape."""
+    case = attn_case(lens, block_size=16, T=T, q_heads=q_heads, kv_heads=kv_heads,
+                     density=0.2, q_density=0.2, seed=len(lens) + T, compact=True)
+    d = _to_dev(case, gpu)
+    out = torch.full((T, len(lens), q_heads, 64), float("nan"), device=gpu)
+    from spikeinfer_amd.kernels import paged_spike_attn_decode
+
+    print(f"every output written: lens={lens} T={T} H={q_heads}/{kv_heads}", flush=True)
+    paged_spike_attn_decode(**d, out=out)
+    torch.cuda.synchronize()
+    _check(out, oracle_attn(case), f"lens={lens}")
+
+
 def test_bf16_output_within_bf16_rounding(gpu):
     case = attn_case([1, 5, 40, 97, 300], block_size=16, seed=13)
     got = _run(case, gpu, dtype=torch.bfloat16)
