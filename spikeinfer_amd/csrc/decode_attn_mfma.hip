@@ -517,6 +517,22 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+
+  const int len = p.plan_inline ? planned_len : seq_len(p, n);
+  const int nparts_seq = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
+  if (part >= nparts_seq) return;
+  const int start = part * p.part_len;
+  const int end = min(len, start + p.part_len);
+  if constexpr (PAIRS) {
+    // An unplanned 4-wave launch (the partials entry past kInlinePlanItems
+    // items) pairs a short item's units too, so it keeps the 2-wave order:
+    // the block of even unit 2s runs units 2s and 2s + 1, the odd one exits.
+    if (!p.plan_inline && !p.order && end - start <= kPairMaxLen) {
+      if ((unit % ups) & 1) return;
+      pair = true;
+      pj = (unit % ups) >> 1;
+    }
+  }
   int my_r = unit % ups;  // this wave's unit within the item
   bool has_unit = true;
   if (pair) {
@@ -526,12 +542,6 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   // (wave-uniform; readfirstlane keeps the cache addresses in scalar registers)
   const int kvh = __builtin_amdgcn_readfirstlane((has_unit ? my_r : 0) % p.Hkv);
   const int t = __builtin_amdgcn_readfirstlane((has_unit ? my_r : 0) / p.Hkv);
-
-  const int len = p.plan_inline ? planned_len : seq_len(p, n);
-  const int nparts_seq = len <= 0 ? 1 : (len + p.part_len - 1) / p.part_len;
-  if (part >= nparts_seq) return;
-  const int start = part * p.part_len;
-  const int end = min(len, start + p.part_len);
   // Short items (at most kPairMaxLen tokens, head_dim 64) sum in the 2-wave
   // order in every launch: the 2-wave launch, pairs in the 4-wave plain
   // kernel, and in the fused kernel waves 0 and 1 alone (waves 2 and 3 only

@@ -110,6 +110,35 @@ def test_long_context_partitions_alone_and_in_batch(gpu, env):
     assert torch.equal(_attn(inp, rows=[1])[:, 0], base[:, 1])
 
 
+def test_partials_entry_alone_and_in_a_large_batch(gpu, env):
+    """The split-context partials entry orders its items only up to 4096 of
+    them; past that its 4-wave launch is unplanned and still runs a short
+    item as a pair of 2-wave units.  Short sequences of 300..3000 tokens
+    (3+ steps, where the 4-wave and 2-wave orders would differ) and a long
+    one: their partial sums in a batch of 4,099 items equal theirs alone,
+    bit for bit."""
+    from spikeinfer_amd.kernels import paged_spike_attn_decode_partials
+
+    lens = [int(x) for x in torch.randint(300, 3000, (4099,), generator=torch.Generator().manual_seed(61))]
+    lens[17] = 9000
+    inp = _inputs(lens, 62, gpu)
+
+    def parts(rows=None):
+        q, tables, ln = inp["q"], inp["tables"], inp["lens"]
+        if rows is not None:
+            q, tables, ln = q[:, rows].contiguous(), tables[rows].contiguous(), ln[rows].contiguous()
+        out = paged_spike_attn_decode_partials(q, inp["k"], inp["v"], tables, ln, head_dim=D, block_size=BS,
+                                               num_q_heads=HQ, num_kv_heads=HKV, part_len=16384)
+        torch.cuda.synchronize()
+        return out
+
+    print("batch invariance: partials entry, 4,099 sequences", flush=True)
+    base = parts()
+    for i in (0, 17, 2048, 4098):
+        alone = parts([i])
+        assert torch.equal(alone[0, :, 0], base[0, :, i]), f"sequence {i} (len {lens[i]})"
+
+
 def _small_model(gpu, seed):
     from spikeinfer_amd.model import SpikingDecoder, SpikingQwenConfig
 
