@@ -165,8 +165,9 @@ def test_long_context_launch_order_over_ragged_batches(n, gpu):
     _check(_run(case, gpu), oracle_attn(case), f"ragged n={n}")
 
 
-@pytest.mark.parametrize("T,q_heads,kv_heads", [(3, 7, 1), (4, 14, 2), (1, 8, 8)])
-def test_planned_short_contexts_pair_mode(T, q_heads, kv_heads, gpu):
+@pytest.mark.parametrize("T,q_heads,kv_heads,bs", [(3, 7, 1, 16), (4, 14, 2, 16), (1, 8, 8, 16),
+                                                  (2, 14, 2, 32), (4, 6, 2, 64)])
+def test_planned_short_contexts_pair_mode(T, q_heads, kv_heads, bs, gpu):
     """Tables of 3072..8192 tokens: the launch is planned (longest first) and
     its items, all of at most 8192 tokens, run as pairs of 2-wave units in
     4-wave workgroups (an odd T * Hkv leaves the last pair half empty);
@@ -175,9 +176,9 @@ def test_planned_short_contexts_pair_mode(T, q_heads, kv_heads, gpu):
     lens = rng.integers(0, 4000, 37)
     lens[[3, 9]] = 0
     lens[5] = 4096
-    case = attn_case(lens.tolist(), block_size=16, T=T, q_heads=q_heads, kv_heads=kv_heads,
+    case = attn_case(lens.tolist(), block_size=bs, T=T, q_heads=q_heads, kv_heads=kv_heads,
                      density=0.2, q_density=0.2, seed=T + q_heads, compact=True)
-    _check(_run(case, gpu), oracle_attn(case), f"planned short T={T} H={q_heads}/{kv_heads}")
+    _check(_run(case, gpu), oracle_attn(case), f"planned short T={T} H={q_heads}/{kv_heads} bs={bs}")
 
 
 @pytest.mark.parametrize("lens,T,q_heads,kv_heads", [
