@@ -203,6 +203,19 @@ def cold_start(inp, dev):
             "gbs": round(attn_bytes(inp["lens_cpu"], 4) / us / 1e3, 1)}
 
 
+def calib_copy(mib, dev):
+    """One device copy of `mib` MiB (0: none): the reference a counter run
+    scales FETCH_SIZE / WRITE_SIZE by."""
+    if not mib:
+        return
+    src = torch.empty(mib << 18, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def cpu_info():
     """What the CPU legs ran on: nproc, the lscpu model name, torch threads."""
     model = None
@@ -590,7 +603,7 @@ def main():
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["config2", "config3", "config5", "sampler"],
+    ap.add_argument("--only", choices=["config2", "config3", "config5", "sampler", "fixed8k"],
                     help="run just this extra workload and print its figures (profiling)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one device copy of this many MiB (counter calibration)")
@@ -608,10 +621,19 @@ def main():
             res = bench_decode_step(args.steps, args.warmup, dev, out_tokens=64)
         elif args.only == "sampler":
             res = bench_sampler(min(args.steps, 50), min(args.warmup, 10), dev)
+        elif args.only == "fixed8k":  # north_star's shape, pre-warmed like the headline
+            alt = make_attn_inputs(256, 8192, 8192, 0.2, 4000, dev)
+            calls = prewarm(alt, dev, args.prewarm_ms)
+            ms_8k, _ = bench_attention(alt, args.steps, args.warmup, dev)
+            nb = attn_bytes(alt["lens_cpu"], 4)
+            res = {"us_per_call": round(ms_8k * 1000, 2), "gbs": round(nb / ms_8k / 1e6, 1),
+                   "frac_of_hbm_peak": round(nb / ms_8k / 1e6 / HBM_PEAK_GBS, 4),
+                   "algorithmic_bytes_per_call": nb, "prewarm_calls": calls}
         else:
             c3 = make_attn_inputs(64, 128, 192, 0.2, 3000, dev, layers=24)
             ms3, _ = bench_attention(c3, args.steps, args.warmup, dev, torch.bfloat16, graph=1)
             res = {"config3_attn_us_per_step_24_layers": round(ms3 * 1000, 1)}
+        calib_copy(args.calib_copy_mib, dev)
         print(json.dumps({"workload": args.only, **res}), flush=True)
         return
 
@@ -665,13 +687,7 @@ def main():
         extras["config5_decode_batch8"] = {k: small[k] for k in ("decode_tok_s", "ms_per_step")}
     # Measured after the headline: the first 20 calls after 0.5 s idle.
     extras["config4_cold_start"] = cold_start(inp, dev)
-    if args.calib_copy_mib:
-        src = torch.empty(args.calib_copy_mib << 18, dtype=torch.float32, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    calib_copy(args.calib_copy_mib, dev)
     cpu = None
     if not args.no_cpu:
         print("cpu baseline", file=sys.stderr, flush=True)
