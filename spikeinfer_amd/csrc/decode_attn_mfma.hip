@@ -286,7 +286,24 @@ __device__ __forceinline__ int plan_slot(const AttnParams &p, int b, int ups, in
   // trip fewer in the prologue of every workgroup).
   int kc[kPlanKeys], lc[kPlanKeys];
 #pragma unroll
-  for (int k = 0; k < kPlanKeys; ++k) kc[k] = i0 + k < i1 ? key(i0 + k, lc[k]) : -1;
+  for (int k = 0; k < kPlanKeys; ++k) {
+    kc[k] = -1;
+    lc[k] = 0;
+  }
+  if (p.num_parts == 1 && per > 1) {
+    // One partition per sequence (item i is sequence i), several items a
+    // thread: the loads are unconditional (past the thread's range they
+    // re-read its last item, in bounds), so they are in flight together --
+    // a branch per key made the compiler wait for each load before the next.
+#pragma unroll
+    for (int k = 0; k < kPlanKeys; ++k) lc[k] = seq_len(p, min(i0 + k, max(i1 - 1, 0)));
+#pragma unroll
+    for (int k = 0; k < kPlanKeys; ++k)
+      if (i0 + k < i1) kc[k] = plan_bucket<PAIRS>(min(p.part_len, lc[k]));
+  } else {
+#pragma unroll
+    for (int k = 0; k < kPlanKeys; ++k) kc[k] = i0 + k < i1 ? key(i0 + k, lc[k]) : -1;
+  }
   // Equal lengths (one partition each): the order is the item order, known
   // after one vote -- the histogram passes and their barriers are skipped.
   if (p.num_parts == 1) {
