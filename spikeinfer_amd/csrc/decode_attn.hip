@@ -308,6 +308,9 @@ static int decode_attn_impl(const int32_t *q, const int64_t q_strides[4], const 
   p.lens = seq_lens;
   p.out = out; p.out_dtype = out_dtype;
   p.os0 = out_strides[0]; p.os1 = out_strides[1]; p.os2 = out_strides[2]; p.os3 = out_strides[3];
+  p.out_vec = out && (out_dtype == SPK_F32 || out_dtype == SPK_BF16 || out_dtype == SPK_F16) &&
+              p.os3 == 1 && p.os0 % 4 == 0 && p.os1 % 4 == 0 && p.os2 % 4 == 0 &&
+              (reinterpret_cast<uintptr_t>(out) & 15) == 0;
   p.T = T; p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.head_dim = head_dim;
   p.bs_log2 = ilog2(block_size); p.nrep = Hq / Hkv; p.scale = scale;
   p.ctx_cap = (int)std::min<int64_t>(ctx_max, INT32_MAX);

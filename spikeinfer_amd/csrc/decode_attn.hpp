@@ -75,6 +75,10 @@ struct AttnParams {
   // sequence has a single partition (spk_decode_attn_partials); the combine
   // then normalises every row.
   int partials_only;
+  // The output rows take whole 4-channel vectors: fp32/bf16/f16 out, unit
+  // channel stride, the other strides multiples of 4 and `out` 16-byte
+  // aligned (the matrix-core epilogue then stores 16 or 8 bytes a lane).
+  int out_vec;
   // Matrix-core path: for d = popc(q & ~k) in 0..head_dim (<= 128), the four
   // e4m3 digits of exp(-d*scale) * 2^8 (byte s weighs 2^-(4s)), built on the
   // host once per scale (build_digit_table) and copied into LDS by every

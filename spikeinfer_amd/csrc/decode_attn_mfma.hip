@@ -802,6 +802,43 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   }
 
   const bool single = nparts_seq == 1 && !p.partials_only;
+  if (single && p.out_vec) {
+    // A lane's values of one head are 4 consecutive channels per 64-channel
+    // group: one 16-byte (fp32) or 8-byte (16-bit) store each.
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int h = 4 * rt + (lane >> 4);
+      if (h >= NREP) continue;
+      const int64_t row = t * p.os0 + n * p.os1 + (kvh * NREP + h) * p.os2;
+#pragma unroll
+      for (int g = 0; g < W64; ++g) {
+        float o[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = len <= 0 ? 0.f : val[4 * W64 * rt + 4 * g + c] / lh[rt];
+        const int64_t at = row + 64 * g + 4 * (lane & 15);
+        if (p.out_dtype == SPK_F32) {
+          *reinterpret_cast<v4f *>(static_cast<float *>(p.out) + at) = v4f{o[0], o[1], o[2], o[3]};
+        } else {
+          typedef unsigned v2u __attribute__((ext_vector_type(2)));
+          uint32_t w[2];
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            uint16_t lo, hi;
+            if (p.out_dtype == SPK_BF16) {
+              lo = f32_to_bf16_bits(o[2 * c]);
+              hi = f32_to_bf16_bits(o[2 * c + 1]);
+            } else {
+              lo = __builtin_bit_cast(uint16_t, static_cast<_Float16>(o[2 * c]));
+              hi = __builtin_bit_cast(uint16_t, static_cast<_Float16>(o[2 * c + 1]));
+            }
+            w[c] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+          }
+          *reinterpret_cast<v2u *>(static_cast<uint16_t *>(p.out) + at) = v2u{w[0], w[1]};
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const int h = 4 * rt + (lane >> 4);
