@@ -68,13 +68,10 @@ struct alignas(16) WaveStage {
   uint4 a[2][kStepTokens];            // digit rows, window-major            (4 KB)
 };
 
-// Cross-wave reduction: 8 * W64 values + 2 denominators per lane.
+// The workgroup's stages (each wave's also holds its cross-wave reduction
+// values, 8 * W64 + 2 floats a lane, after its last step).
 template <int W64, int KW>
-constexpr int kReduceFloats = (KW - 1) * 64 * (8 * W64 + 2);
-template <int W64, int KW>
-constexpr int kSmemBytes = (KW * (int)sizeof(WaveStage<W64>) > kReduceFloats<W64, KW> * 4)
-                               ? KW * (int)sizeof(WaveStage<W64>)
-                               : kReduceFloats<W64, KW> * 4;
+constexpr int kSmemBytes = KW * (int)sizeof(WaveStage<W64>);
 
 __device__ __forceinline__ v2i tr_b4(const SPK_LDS char *p) {
   return __builtin_amdgcn_ds_read_tr4_b64_v2i32((SPK_LDS v2i *)p);
@@ -779,13 +776,15 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
     }
   }
 
-  // Cross-wave reduction (fixed order) through LDS, reusing the stage area.
+  // Cross-wave reduction (fixed order) through LDS: a wave writes its values
+  // into its own stage, which no other wave reads (so no barrier before the
+  // writes), and each unit's leader adds its other waves' values in wave
+  // order after one barrier.
   constexpr int kRed = kVals + 2;
-  __syncthreads();
-  float *red = reinterpret_cast<float *>(smem);
-  // Each unit's leader wave adds its other waves' values in wave order.
+  static_assert(64 * kRed * 4 <= (int)sizeof(WaveStage<W64>), "a wave's values fit its stage");
+  auto red_of = [&](int w) { return reinterpret_cast<float *>(smem + w * sizeof(WaveStage<W64>)) + lane * kRed; };
   if (wave != leader) {
-    float *dst = red + ((wave - 1) * 64 + lane) * kRed;
+    float *dst = red_of(wave);
 #pragma unroll
     for (int k = 0; k < kVals; ++k) dst[k] = val[k];
 #pragma unroll
@@ -794,7 +793,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   __syncthreads();
   if (wave != leader || !has_unit) return;
   for (int w = leader + 1; w < leader + kw_unit; ++w) {
-    const float *src = red + ((w - 1) * 64 + lane) * kRed;
+    const float *src = red_of(w);
 #pragma unroll
     for (int k = 0; k < kVals; ++k) val[k] += src[k];
 #pragma unroll
