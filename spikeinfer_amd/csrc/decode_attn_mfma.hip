@@ -498,7 +498,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(XDT == 
   // Unplanned launch: x = (sequence, timestep, kv head) unit, y = partition.
   // Either way consecutive block ids (dealt round-robin to the 8 XCDs) are
   // sibling units of equal length.
-  // Pair mode (PAIRS, planned launches): a short item's units run two
+  // Pair mode (PAIRS: the 4-wave plain kernel): a short item's units run two
   // waves each, two units per workgroup (waves 2s, 2s + 1: unit 2 * pair + s).
   constexpr bool PAIRS = KW == 4 && XDT == 0 && W64 == 1;
   const int units = p.N * p.T * p.Hkv;
