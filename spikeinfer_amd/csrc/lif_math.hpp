@@ -17,6 +17,16 @@ __device__ __forceinline__ bool lif_step(float &u, float cur, float beta, float 
   return u - th > 0.f;
 }
 
+// The same recurrence carrying the reset flag: r is the previous step's
+// spike (u - th > 0 on the same u), which the reset of this step needs, so it
+// is not recomputed; r * th is th or zth = 0 * th (the same value, signed
+// zero included).  Start with r = (u0 - th > 0) and zth = 0.f * th.
+__device__ __forceinline__ bool lif_step_r(float &u, bool &r, float cur, float beta, float th, float zth) {
+  u = (beta * u + cur) - (r ? th : zth);
+  r = u - th > 0.f;
+  return r;
+}
+
 __device__ __forceinline__ float clamp01(float b) { return fminf(fmaxf(b, 0.f), 1.f); }
 
 // ---- element types of the 16-byte vector paths ------------------------------

@@ -124,13 +124,16 @@ __global__ __launch_bounds__(256) void lif_dense_vec_kernel(LifParams p, int64_t
        gi += (int64_t)gridDim.x * blockDim.x) {
     const int64_t m = gi / (N / V);
     const int c0 = static_cast<int>(gi - m * (N / V)) * V;
-    float beta[V], th[V], u[V];
+    float beta[V], th[V], zth[V], u[V];
+    bool r[V];
     load_params(p.beta, p.param_dtype, c0, beta);
     load_params(p.th, p.param_dtype, c0, th);
 #pragma unroll
     for (int i = 0; i < V; ++i) {
       beta[i] = clamp01(beta[i]);
       u[i] = mem0 ? mem0[m * N + c0 + i] : 0.f;
+      zth[i] = 0.f * th[i];
+      r[i] = u[i] - th[i] > 0.f;
     }
     const E *xrow = static_cast<const E *>(p.x) + m * xs1 + c0;
     E *srow = static_cast<E *>(spikes) + m * N + c0;
@@ -147,7 +150,7 @@ __global__ __launch_bounds__(256) void lif_dense_vec_kernel(LifParams p, int64_t
         Vec sv;
 #pragma unroll
         for (int i = 0; i < V; ++i)
-          sv[i] = spike_elem<DT>(lif_step(u[i], elem_to_f32<DT>(xv[k][i]), beta[i], th[i]));
+          sv[i] = spike_elem<DT>(lif_step_r(u[i], r[i], elem_to_f32<DT>(xv[k][i]), beta[i], th[i], zth[i]));
         __builtin_nontemporal_store(sv, reinterpret_cast<Vec *>(srow + (t0 + k) * total));
       }
     }
@@ -359,13 +362,16 @@ __global__ __launch_bounds__(256) void lif_pack_sites_kernel(MultiSites m) {
 #pragma unroll
     for (int k = 0; k < kTBatch; ++k)
       xv[k] = __builtin_nontemporal_load(reinterpret_cast<const Vec *>(xrow + min(k, m.T - 1) * xs0));
-    float beta[8], th[8], u[8];
+    float beta[8], th[8], zth[8], u[8];
+    bool r[8];
     load_params(st.beta, st.param_dtype, c0, beta);
     load_params(st.threshold, st.param_dtype, c0, th);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       beta[i] = clamp01(beta[i]);
       u[i] = 0.f;
+      zth[i] = 0.f * th[i];
+      r[i] = 0.f - th[i] > 0.f;
     }
     bool write = true;
     int64_t dst;
@@ -390,7 +396,8 @@ __global__ __launch_bounds__(256) void lif_pack_sites_kernel(MultiSites m) {
         const Vec x = xv[k];
         uint32_t byte = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) byte |= lif_step(u[i], elem_to_f32<DT>(x[i]), beta[i], th[i]) ? (1u << i) : 0u;
+        for (int i = 0; i < 8; ++i)
+          byte |= lif_step_r(u[i], r[i], elem_to_f32<DT>(x[i]), beta[i], th[i], zth[i]) ? (1u << i) : 0u;
         const uint32_t lo = or_octet(sub < 4 ? byte << (8 * sub) : 0u);
         const uint32_t hi = or_octet(sub < 4 ? 0u : byte << (8 * (sub - 4)));
         if (write && sub == 0) out[(t0 + k) * os0] = (static_cast<uint64_t>(hi) << 32) | lo;

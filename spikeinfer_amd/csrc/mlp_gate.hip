@@ -234,14 +234,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // wave's 2 KB above the partial slots, then each (t, token) row's 32 bytes
   // go out as two 16-byte stores (16 two-byte stores a lane took ~2 us).
   uint16_t *stg = reinterpret_cast<uint16_t *>(smem + kStageOff + wave * kStageBytes);
+  const float zth = 0.f * th;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     float u = 0.f;
+    bool r = 0.f - th > 0.f;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const float g = round_to<SPK_BF16>(sg[t][j]);
       const float up = round_to<SPK_BF16>(su[t][j]);
-      const bool spike = lif_step(u, g, beta, th);
+      const bool spike = lif_step_r(u, r, g, beta, th, zth);
       stg[(16 * t + 4 * kq + j) * 16 + r16] = f32_to_elem<SPK_BF16>((spike ? 1.f : 0.f) * up);
     }
   }

@@ -667,13 +667,16 @@ __global__ __launch_bounds__(256) void lif_gate_mul_kernel(const typename Elem<D
   if (gi >= groups) return;
   const int64_t row = gi / (I / V);
   const int c0 = static_cast<int>(gi - row * (I / V)) * V;
-  float beta[V], th[V], u[V];
+  float beta[V], th[V], zth[V], u[V];
+  bool r[V];
   load_params(beta_p, param_dtype, c0, beta);
   load_params(th_p, param_dtype, c0, th);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     beta[i] = clamp01(beta[i]);
     u[i] = 0.f;
+    zth[i] = 0.f * th[i];
+    r[i] = 0.f - th[i] > 0.f;
   }
   const E *grow = x + row * xs1 + c0;
   E *orow = out + row * I + c0;
@@ -692,7 +695,7 @@ __global__ __launch_bounds__(256) void lif_gate_mul_kernel(const typename Elem<D
       Vec y;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
-        const bool s = lif_step(u[i], elem_to_f32<DT>(gv[k][i]), beta[i], th[i]);
+        const bool s = lif_step_r(u[i], r[i], elem_to_f32<DT>(gv[k][i]), beta[i], th[i], zth[i]);
         y[i] = f32_to_elem<DT>((s ? 1.f : 0.f) * elem_to_f32<DT>(uv[k][i]));
       }
       __builtin_nontemporal_store(y, reinterpret_cast<Vec *>(orow + (t0 + k) * rows * I));
