@@ -203,9 +203,10 @@ constexpr int ring_depth(int ks) {
 }
 template <int KS>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void linear_wide_kernel(
-    const uint16_t *x, const v4u *wp, const uint16_t *bias, uint16_t *y, int M, int N) {
+    const uint16_t *x, const v4u *wp, const uint16_t *bias, uint16_t *y, int M, int N, bool vec) {
   extern __shared__ __align__(16) char smem[];
   constexpr int K = 32 * KS, kChunks = K / 8, kRowChunks = kChunks + 1;
+  static_assert(kRows * kRowChunks * 16 <= kLdsBytes, "the padded x rows fit the LDS");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int PP = N / 32;  // tile pairs
   const int q0 = static_cast<int>(static_cast<int64_t>(blockIdx.x) * PP / gridDim.x);
@@ -235,16 +236,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs, vofs, ks * 1024, 2));
   };
   constexpr int D = ring_depth(KS);
-  for (int q = q0 + wave; q < q1; q += kWaves) {
+  // Ring of D k-steps: slot ks % D is read by k-step ks's MFMAs and then
+  // refilled with k-step ks + D; past the pair's last k-step it takes the
+  // wave's next pair's first ones (KS is a multiple of D, so k-step j of the
+  // next pair lands in slot j % D), and the ring never drains between pairs.
+  int q = q0 + wave;
+  if (q >= q1) return;  // no barrier below
+  v4u r0[D], r1[D];
+  {
     const int vofs0 = (2 * q * KS * 64 + lane) * 16, vofs1 = vofs0 + KS * 1024;
-    // Ring of D k-steps: slot ks % D is read by k-step ks's MFMAs and then
-    // refilled with k-step ks + D.
-    v4u r0[D], r1[D];
 #pragma unroll
     for (int ks = 0; ks < D; ++ks) {
       r0[ks] = wload(vofs0, ks);
       r1[ks] = wload(vofs1, ks);
     }
+  }
+  for (; q < q1; q += kWaves) {
+    const int vofs0 = (2 * q * KS * 64 + lane) * 16, vofs1 = vofs0 + KS * 1024;
+    const bool more = q + kWaves < q1;
+    const int nofs0 = vofs0 + 2 * kWaves * KS * 1024, nofs1 = nofs0 + KS * 1024;
     v4f acc0[4], acc1[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc0[t] = acc1[t] = v4f{};
@@ -264,11 +274,41 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       if (ks + D < KS) {
         r0[slot] = wload(vofs0, ks + D);
         r1[slot] = wload(vofs1, ks + D);
+      } else if (more) {  // the next pair's first k-steps, into the same slots
+        r0[slot] = wload(nofs0, ks + D - KS);
+        r1[slot] = wload(nofs1, ks + D - KS);
       }
     }
     const int col = 32 * q + r16;
     const float bv0 = bias ? elem_to_f32<SPK_BF16>(bias[col]) : 0.f;
     const float bv1 = bias ? elem_to_f32<SPK_BF16>(bias[col + 16]) : 0.f;
+    constexpr int kXBytes = kRows * kRowChunks * 16;
+    // The pair's 64 x 32 tile through a per-wave LDS stage, out as 16-byte row
+    // pieces (64 B a row; 55.2 -> 53.3 us at the lm_head with the unbroken
+    // ring, against 2-byte stores); a y that is not 16-byte aligned, or an x
+    // that leaves no room for the stage, keeps the 2-byte stores.
+    if constexpr (kXBytes + kWaves * 4096 <= kLdsBytes) {
+      if (vec) {
+        uint16_t *stg = reinterpret_cast<uint16_t *>(smem + kXBytes + wave * 4096);
+        wave_lds_sync();  // the previous pair's reads are done
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int row = 16 * t + 4 * kq + i;
+            stg[row * 32 + r16] = f32_to_elem<SPK_BF16>(acc0[t][i] + bv0);
+            stg[row * 32 + 16 + r16] = f32_to_elem<SPK_BF16>(acc1[t][i] + bv1);
+          }
+        wave_lds_sync();  // lanes read rows other lanes wrote
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = lane + 64 * j, row = c >> 2;
+          const v4u v = reinterpret_cast<const v4u *>(stg)[c];
+          if (row < M) *reinterpret_cast<v4u *>(y + static_cast<int64_t>(row) * N + 32 * q + 8 * (c & 3)) = v;
+        }
+        continue;
+      }
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -471,7 +511,9 @@ extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void
   int R = ((256 / MG) + 7) / 8 * 8;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (MG == 1 && P > lin::kMaxUnitsPerWave * R && N % 32 == 0) {
-    // Wide N: 256 workgroups, each a range of tile pairs.
+    // Wide N: 256 workgroups, each a range of tile pairs.  Rows of y are
+    // N * 2 bytes (a multiple of 64), so an aligned y takes 16-byte stores.
+    const bool vec = (reinterpret_cast<uintptr_t>(y) & 15) == 0;
 #define SPK_WIDE_CASE(KS)                                                                              \
   case KS: {                                                                                         \
     static bool attr = false;                                                                        \
@@ -483,9 +525,11 @@ extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void
     }                                                                                                \
     lin::linear_wide_kernel<KS><<<256, lin::kThreads, lin::kLdsBytes, s>>>(                           \
         static_cast<const uint16_t *>(x), static_cast<const lin::v4u *>(w_packed),                   \
-        static_cast<const uint16_t *>(bias), static_cast<uint16_t *>(y), M, N);                      \
+        static_cast<const uint16_t *>(bias), static_cast<uint16_t *>(y), M, N, vec);                 \
     return check_launch("linear_decode");                                                           \
   }
+    // K = 1280 is not here: its padded x rows (164,864 B) exceed the LDS, and
+    // the tiled kernel takes it.
     switch (K / 32) {
       SPK_WIDE_CASE(16)
       SPK_WIDE_CASE(20)
@@ -493,7 +537,6 @@ extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void
       SPK_WIDE_CASE(28)
       SPK_WIDE_CASE(32)
       SPK_WIDE_CASE(36)
-      SPK_WIDE_CASE(40)
     }
 #undef SPK_WIDE_CASE
   }

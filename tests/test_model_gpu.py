@@ -297,7 +297,8 @@ def test_mlp_gate_lif_unsupported_shapes_return_none(gpu):
                                          (64, 151936, 896, False), (5, 20480, 640, True),
                                          (128, 896, 4864, False), (44, 896, 4864, False),
                                          (4, 896, 4864, False), (256, 896, 4864, False),
-                                         (20, 64, 2048, False)])
+                                         (20, 64, 2048, False), (64, 16384, 1280, False),
+                                         (64, 16384, 1152, True), (33, 20480, 512, False)])
 def test_linear_decode_within_one_ulp(gpu, M, N, K, bias):
     """Small-M linear against the fp64 product rounded to bf16: every output
     within 1 bf16 ulp (fp32 sums in a different order may round the other
