@@ -7,9 +7,9 @@
 // MI355X design (the same ground rules as the fused MLP gate in mlp_gate.hip):
 // at these sizes a projection is bound by moving x and W into the CUs and by
 // latency, not by the matrix cores.
-//   * A workgroup owns a 64-row group of x, the whole K, in LDS (at most
-//     160 KB), loaded once by global_load_lds into a layout swizzled by row
-//     (16-byte chunk c of row r at chunk c ^ (r % 16)).
+//   * A workgroup owns a 32- or 64-row group of x, the whole K, in LDS (at
+//     most 160 KB), loaded once by global_load_lds into a layout swizzled by
+//     row (16-byte chunk c of row r at chunk c ^ (r % 16)).
 //   * W is repacked once at load in MFMA-fragment order (spk_linear_pack):
 //     one k-step (32 K) of one 16-column tile is one contiguous 1 KB block, so a
 //     wave's B operand arrives with one coalesced 16-byte load per lane.
@@ -22,6 +22,8 @@
 // Grid: row groups x column ranges (ranges chosen so the launch has about 256
 // workgroups); the row groups of one range are consecutive on one XCD (block b
 // -> XCD b % 8), so W comes from HBM once.
+#include <algorithm>
+
 #include "common.hpp"
 #include "lif_math.hpp"
 #include "norm_rows.hpp"
@@ -36,15 +38,16 @@ typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kRows = 64;            // rows of x per workgroup (4 row tiles)
+constexpr int kRows = 64;            // rows of x per workgroup, at most (4 row tiles)
 constexpr int kParts = 8;            // K split of a tile into units
 constexpr int kMaxUnitsPerWave = 2;  // tiles per range <= 2
 constexpr int kMaxPartSteps = 5;     // k-steps per part: K <= 8 * 5 * 32 = 1280
 constexpr int kLdsBytes = 160 * 1024;
-constexpr int kSlotFloats = 4 * 4 * 64;  // one partial: 4 row tiles x 4 x 64 lanes
-constexpr int kStageOff = kWaves * kMaxUnitsPerWave * kSlotFloats * 4;  // y staging, after the slots
+// One partial: RT row tiles x 4 x 64 lanes; the y staging follows the slots.
+template <int RT> constexpr int slot_floats() { return RT * 4 * 64; }
+template <int RT> constexpr int stage_off() { return kWaves * kMaxUnitsPerWave * slot_floats<RT>() * 4; }
 constexpr int kStageBytes = 16 * 16 * 2;                               // one wave's 16 x 16 tile
-static_assert(kStageOff + kWaves * kStageBytes <= kLdsBytes, "slots and staging fit the LDS");
+static_assert(stage_off<4>() + kWaves * kStageBytes <= kLdsBytes, "slots and staging fit the LDS");
 
 // Packed W (spk_linear_pack): for tile p (rows 16p..16p+15 of W) and k-step
 // ks, 1 KB at (p * KS + ks) KB: lane l's 16 bytes are W[16p + l%16][32ks +
@@ -53,8 +56,9 @@ static_assert(kStageOff + kWaves * kStageBytes <= kLdsBytes, "slots and staging 
 // NORM: the rows are add_rmsnorm(nin.h, nin.delta, nin.w) (x unused), computed
 // in the prologue; the workgroups of the last column range (never empty) write
 // h + delta to nin.h_out.
-template <bool NORM>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void linear_kernel(
+// RT: row tiles of 16 per workgroup (2 or 4).
+template <bool NORM, int RT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(RT == 4 ? 2 : 4))) void linear_kernel(
     const uint16_t *x, const v4u *wp, const uint16_t *bias, uint16_t *y, int M, int N, int K,
     int MG, int R, NormIn nin) {
   extern __shared__ __align__(16) char smem[];
@@ -65,7 +69,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int P = N / 16;
   const int p0 = r * P / R, np = (r + 1) * P / R - p0;
   if (np <= 0) return;  // uniform over the workgroup
-  const int m0 = m * kRows;
+  static_assert(!NORM || RT == 4, "the norm prologue runs 64-row groups");
+  constexpr int kR = 16 * RT, kSF = slot_floats<RT>();
+  const int m0 = m * kR;
 
   // The bias of the epilogue's columns, loaded first (its latency hides under
   // the whole launch).
@@ -96,7 +102,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
   }
 
-  // x rows m0..m0+63 (clamped to M - 1) into LDS, chunk c of row rr at c ^ (rr % 16).
+  // x rows m0..m0+16RT-1 (clamped to M - 1) into LDS, chunk c of row rr at c ^ (rr % 16).
   if constexpr (NORM) {
     norm_rows<kWaves, kRows / kWaves>(
         nin, kRows, K, r == R - 1, wave, lane, [&](int rr) { return static_cast<int64_t>(min(m0 + rr, M - 1)); },
@@ -105,7 +111,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
           *reinterpret_cast<NormRowBf16::v8u16 *>(smem + rr * (kChunks * 16) + 16 * (v ^ (rr & 15))) = yv;
         });
   } else {
-    const int total = kRows * kChunks;  // a multiple of 64 (K % 128 == 0)
+    const int total = kR * kChunks;  // a multiple of 64 (K % 128 == 0)
     for (int base = wave * 64; base < total; base += kWaves * 64) {
       const int g = base + lane;
       const int rr = g / kChunks, pc = g - rr * kChunks;
@@ -119,11 +125,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   __syncthreads();
 
   const int r16 = lane & 15, kq = lane >> 4;
-  v4f acc[kMaxUnitsPerWave][4];
+  v4f acc[kMaxUnitsPerWave][RT];
 #pragma unroll
   for (int j = 0; j < kMaxUnitsPerWave; ++j)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[j][t] = v4f{};
+    for (int t = 0; t < RT; ++t) acc[j][t] = v4f{};
 #pragma unroll
   for (int j = 0; j < kMaxUnitsPerWave; ++j) {
     const int u = wave + kWaves * j;
@@ -136,7 +142,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
           const int c = 4 * (k0 + ks) + kq;
           const v8b bw = __builtin_bit_cast(v8b, bq[j][ks]);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
+          for (int t = 0; t < RT; ++t) {
             const int rr = 16 * t + r16;
             const v8b a = *reinterpret_cast<const v8b *>(smem + rr * (kChunks * 16) + 16 * (c ^ r16));
             acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bw, acc[j][t], 0, 0, 0);
@@ -154,30 +160,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   for (int j = 0; j < kMaxUnitsPerWave; ++j) {
     const int u = wave + kWaves * j;
     if (u < U) {
-      v4f *d = slots + u * (kSlotFloats / 4);
+      v4f *d = slots + u * (kSF / 4);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) d[t * 64 + lane] = acc[j][t];
+      for (int t = 0; t < RT; ++t) d[t * 64 + lane] = acc[j][t];
     }
   }
   __syncthreads();
 
-  // Epilogue: wave w finishes row tile w % 4 of tile p0 + w / 4 (w / 4 < np),
+  // Epilogue: wave w finishes row tile w % RT of tile p0 + w / RT (w / RT < np),
   // summing its eight parts in order, adding the bias (loaded at the start)
   // and writing y (fp32 sum + bias, rounded once, as the GEMM epilogue).
-  const int et = wave & 3, ee = wave >> 2;
+  const int et = wave % RT, ee = wave / RT;
   if (ee >= np) return;
   float sum[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sum[i] = 0.f;
 #pragma unroll
   for (int part = 0; part < kParts; ++part) {
-    const v4f a = slots[(ee * kParts + part) * (kSlotFloats / 4) + et * 64 + lane];
+    const v4f a = slots[(ee * kParts + part) * (kSF / 4) + et * 64 + lane];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sum[i] += a[i];
   }
   // The 16 x 16 bf16 tile is staged in the wave's 512 bytes above the
   // partial slots; its rows' 32 bytes then go out as two 16-byte stores.
-  uint16_t *stg = reinterpret_cast<uint16_t *>(smem + kStageOff + wave * kStageBytes);
+  uint16_t *stg = reinterpret_cast<uint16_t *>(smem + stage_off<RT>() + wave * kStageBytes);
 #pragma unroll
   for (int i = 0; i < 4; ++i) stg[(4 * kq + i) * 16 + r16] = f32_to_elem<SPK_BF16>(sum[i] + bv[ee]);
   wave_lds_sync();  // lanes read rows other lanes wrote
@@ -449,29 +455,53 @@ extern "C" int spk_linear_pack(const void *w, int N, int K, int dtype, void *w_p
 // workgroups in all, at most two 16-column tiles each.
 static int launch_linear_tiled(const void *x, const void *w_packed, const void *bias, void *y, int M, int N,
                                int K, const NormIn *nin, hipStream_t s) {
-  const int MG = (M + lin::kRows - 1) / lin::kRows;
+  // Column ranges: a multiple of 8 (one per XCD), about 256 workgroups in
+  // all, at most two 16-column tiles each.  32-row groups (two workgroups fit
+  // a CU, so one's x fill overlaps the other's MFMAs) whenever that grid stays
+  // within 256 workgroups, 64-row groups otherwise.  Measured (graph of 24
+  // distinct weights, K = 896): M = 32: q/k/v 5.46 -> 4.25 us, o 5.17 -> 4.11
+  // us; M = 256: o (N = 896) 5.37 -> 5.14 us, while q/k/v (N = 1152: 320
+  // workgroups) stays on 64 rows (6.87 against 6.96 us).  The sum of every
+  // element (eight K parts in order) is the same either way.
   const int P = N / 16;
-  int R = ((256 / MG) + 7) / 8 * 8;
-  while (R * lin::kMaxUnitsPerWave < P) R += 8;
+  auto ranges = [&](int MG) {
+    int R = ((256 / MG) + 7) / 8 * 8;
+    if (R < 8) R = 8;
+    while (R * lin::kMaxUnitsPerWave < P) R += 8;
+    return R;
+  };
+  const int MG2 = (M + 31) / 32;
+  const int RT = !nin && MG2 * ranges(MG2) <= 256 ? 2 : 4;
+  const int rows = 16 * RT;
+  const int MG = (M + rows - 1) / rows;
+  const int R = ranges(MG);
   if (reinterpret_cast<uintptr_t>(y) & 15)  // (this kernel's tile rows go out as 16-byte stores)
     return fail(SPK_EUNSUPPORTED, "linear_decode: y must be 16-byte aligned for this shape");
-  static bool attr[2] = {false, false};
-  const void *fn = nin ? reinterpret_cast<const void *>(lin::linear_kernel<true>)
-                       : reinterpret_cast<const void *>(lin::linear_kernel<false>);
-  if (!attr[nin ? 1 : 0]) {
+  static bool attr[3] = {false, false, false};
+  const void *fn = nin ? reinterpret_cast<const void *>(lin::linear_kernel<true, 4>)
+                 : RT == 4 ? reinterpret_cast<const void *>(lin::linear_kernel<false, 4>)
+                           : reinterpret_cast<const void *>(lin::linear_kernel<false, 2>);
+  const int ai = nin ? 1 : RT == 4 ? 0 : 2;
+  if (!attr[ai]) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lin::kLdsBytes) != hipSuccess)
       return fail(SPK_EHIP, "linear_decode: cannot reserve %d bytes of LDS", lin::kLdsBytes);
-    attr[nin ? 1 : 0] = true;
+    attr[ai] = true;
   }
   const NormIn none{};
-  if (nin)
-    lin::linear_kernel<true><<<MG * R, lin::kThreads, lin::kLdsBytes, s>>>(
+  if (nin) {
+    lin::linear_kernel<true, 4><<<MG * R, lin::kThreads, lin::kLdsBytes, s>>>(
         nullptr, static_cast<const lin::v4u *>(w_packed), static_cast<const uint16_t *>(bias),
         static_cast<uint16_t *>(y), M, N, K, MG, R, *nin);
-  else
-    lin::linear_kernel<false><<<MG * R, lin::kThreads, lin::kLdsBytes, s>>>(
+  } else if (RT == 4) {
+    lin::linear_kernel<false, 4><<<MG * R, lin::kThreads, lin::kLdsBytes, s>>>(
         static_cast<const uint16_t *>(x), static_cast<const lin::v4u *>(w_packed),
         static_cast<const uint16_t *>(bias), static_cast<uint16_t *>(y), M, N, K, MG, R, none);
+  } else {
+    const int lds = std::max(rows * K * 2, lin::stage_off<2>() + lin::kWaves * lin::kStageBytes);
+    lin::linear_kernel<false, 2><<<MG * R, lin::kThreads, lds, s>>>(
+        static_cast<const uint16_t *>(x), static_cast<const lin::v4u *>(w_packed),
+        static_cast<const uint16_t *>(bias), static_cast<uint16_t *>(y), M, N, K, MG, R, none);
+  }
   return check_launch("linear_decode");
 }
 
