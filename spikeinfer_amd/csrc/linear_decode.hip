@@ -40,14 +40,14 @@ constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kRows = 64;            // rows of x per workgroup, at most (4 row tiles)
 constexpr int kParts = 8;            // K split of a tile into units
-constexpr int kMaxUnitsPerWave = 2;  // tiles per range <= 2
+constexpr int kMaxUnitsPerWave = 2;  // tiles per range <= 2 (3 for the 32-row groups, below)
 constexpr int kMaxPartSteps = 5;     // k-steps per part: K <= 8 * 5 * 32 = 1280
 constexpr int kLdsBytes = 160 * 1024;
 // One partial: RT row tiles x 4 x 64 lanes; the y staging follows the slots.
 template <int RT> constexpr int slot_floats() { return RT * 4 * 64; }
-template <int RT> constexpr int stage_off() { return kWaves * kMaxUnitsPerWave * slot_floats<RT>() * 4; }
+template <int RT, int MU> constexpr int stage_off() { return kWaves * MU * slot_floats<RT>() * 4; }
 constexpr int kStageBytes = 16 * 16 * 2;                               // one wave's 16 x 16 tile
-static_assert(stage_off<4>() + kWaves * kStageBytes <= kLdsBytes, "slots and staging fit the LDS");
+static_assert(stage_off<4, 2>() + kWaves * kStageBytes <= kLdsBytes, "slots and staging fit the LDS");
 
 // Packed W (spk_linear_pack): for tile p (rows 16p..16p+15 of W) and k-step
 // ks, 1 KB at (p * KS + ks) KB: lane l's 16 bytes are W[16p + l%16][32ks +
@@ -56,8 +56,9 @@ static_assert(stage_off<4>() + kWaves * kStageBytes <= kLdsBytes, "slots and sta
 // NORM: the rows are add_rmsnorm(nin.h, nin.delta, nin.w) (x unused), computed
 // in the prologue; the workgroups of the last column range (never empty) write
 // h + delta to nin.h_out.
-// RT: row tiles of 16 per workgroup (2 or 4).
-template <bool NORM, int RT>
+// RT: row tiles of 16 per workgroup (2 or 4); MU: tiles per column range,
+// at most (2, or 3 with 32-row groups).
+template <bool NORM, int RT, int MU>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(RT == 4 ? 2 : 4))) void linear_kernel(
     const uint16_t *x, const v4u *wp, const uint16_t *bias, uint16_t *y, int M, int N, int K,
     int MG, int R, NormIn nin) {
@@ -75,11 +76,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(RT == 
 
   // The bias of the epilogue's columns, loaded first (its latency hides under
   // the whole launch).
-  float bv[kMaxUnitsPerWave];
+  float bv[MU];
 #pragma unroll
-  for (int e = 0; e < kMaxUnitsPerWave; ++e)
+  for (int e = 0; e < MU; ++e)
     bv[e] = bias ? elem_to_f32<SPK_BF16>(bias[16 * (p0 + min(e, np - 1)) + (lane & 15)]) : 0.f;
-  // Units (tile, part): wave w takes units w and w + 8 (np <= 2 tiles).
+  // Units (tile, part): wave w takes units w, w + 8 (and w + 16) (np <= MU tiles).
   // W arrives with nontemporal loads: the row groups of a range run on one
   // XCD at about the same time, and streaming W past the caches measured
   // faster in the decode step (with the MLP gate's: 1.570 -> 1.549 ms).
@@ -88,9 +89,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(RT == 
     k0 = part * KS / kParts;
     k1 = (part + 1) * KS / kParts;
   };
-  v4u bq[kMaxUnitsPerWave][kMaxPartSteps];
+  v4u bq[MU][kMaxPartSteps];
 #pragma unroll
-  for (int j = 0; j < kMaxUnitsPerWave; ++j) {
+  for (int j = 0; j < MU; ++j) {
     const int u = wave + kWaves * j;
     if (u < U) {
       int k0, k1;
@@ -125,13 +126,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(RT == 
   __syncthreads();
 
   const int r16 = lane & 15, kq = lane >> 4;
-  v4f acc[kMaxUnitsPerWave][RT];
+  v4f acc[MU][RT];
 #pragma unroll
-  for (int j = 0; j < kMaxUnitsPerWave; ++j)
+  for (int j = 0; j < MU; ++j)
 #pragma unroll
     for (int t = 0; t < RT; ++t) acc[j][t] = v4f{};
 #pragma unroll
-  for (int j = 0; j < kMaxUnitsPerWave; ++j) {
+  for (int j = 0; j < MU; ++j) {
     const int u = wave + kWaves * j;
     if (u < U) {
       int k0, k1;
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(RT == 
   __syncthreads();
   v4f *slots = reinterpret_cast<v4f *>(smem);
 #pragma unroll
-  for (int j = 0; j < kMaxUnitsPerWave; ++j) {
+  for (int j = 0; j < MU; ++j) {
     const int u = wave + kWaves * j;
     if (u < U) {
       v4f *d = slots + u * (kSF / 4);
@@ -183,7 +184,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(RT == 
   }
   // The 16 x 16 bf16 tile is staged in the wave's 512 bytes above the
   // partial slots; its rows' 32 bytes then go out as two 16-byte stores.
-  uint16_t *stg = reinterpret_cast<uint16_t *>(smem + stage_off<RT>() + wave * kStageBytes);
+  uint16_t *stg = reinterpret_cast<uint16_t *>(smem + stage_off<RT, MU>() + wave * kStageBytes);
 #pragma unroll
   for (int i = 0; i < 4; ++i) stg[(4 * kq + i) * 16 + r16] = f32_to_elem<SPK_BF16>(sum[i] + bv[ee]);
   wave_lds_sync();  // lanes read rows other lanes wrote
@@ -451,58 +452,57 @@ extern "C" int spk_linear_pack(const void *w, int N, int K, int dtype, void *w_p
 }
 
 // The tiled kernel (K <= 1280, M <= 256): rows from x, or (nin) normed in the
-// prologue.  The column ranges are a multiple of 8 (one per XCD), about 256
-// workgroups in all, at most two 16-column tiles each.
+// prologue.
 static int launch_linear_tiled(const void *x, const void *w_packed, const void *bias, void *y, int M, int N,
                                int K, const NormIn *nin, hipStream_t s) {
   // Column ranges: a multiple of 8 (one per XCD), about 256 workgroups in
-  // all, at most two 16-column tiles each.  32-row groups (two workgroups fit
-  // a CU, so one's x fill overlaps the other's MFMAs) whenever that grid stays
-  // within 256 workgroups, 64-row groups otherwise.  Measured (graph of 24
-  // distinct weights, K = 896): M = 32: q/k/v 5.46 -> 4.25 us, o 5.17 -> 4.11
-  // us; M = 256: o (N = 896) 5.37 -> 5.14 us, while q/k/v (N = 1152: 320
-  // workgroups) stays on 64 rows (6.87 against 6.96 us).  The sum of every
-  // element (eight K parts in order) is the same either way.
+  // all, at most two 16-column tiles each (three with 32-row groups).  32-row
+  // groups (two workgroups fit a CU, so one's x fill overlaps the other's
+  // MFMAs) whenever that grid stays within 256 workgroups, 64-row groups
+  // otherwise.  Measured (graph of 24 distinct weights, K = 896): M = 32:
+  // q/k/v 5.46 -> 4.25 us, o 5.17 -> 4.11 us; M = 256: o (N = 896) 5.37 ->
+  // 5.14 us, q/k/v (N = 1152, three tiles a range) 6.90 -> 6.45 us.  The sum
+  // of every element (eight K parts in order) is the same either way.
   const int P = N / 16;
-  auto ranges = [&](int MG) {
+  auto ranges = [&](int MG, int mu) {
     int R = ((256 / MG) + 7) / 8 * 8;
     if (R < 8) R = 8;
-    while (R * lin::kMaxUnitsPerWave < P) R += 8;
+    while (R * mu < P) R += 8;
     return R;
   };
   const int MG2 = (M + 31) / 32;
-  const int RT = !nin && MG2 * ranges(MG2) <= 256 ? 2 : 4;
+  const int RT = !nin && MG2 * ranges(MG2, 3) <= 256 ? 2 : 4;
   const int rows = 16 * RT;
   const int MG = (M + rows - 1) / rows;
-  const int R = ranges(MG);
+  const int R = ranges(MG, RT == 2 ? 3 : 2);
+  const int MU = R * 2 >= P ? 2 : 3;  // 3 only where a range needs it (more registers)
   if (reinterpret_cast<uintptr_t>(y) & 15)  // (this kernel's tile rows go out as 16-byte stores)
     return fail(SPK_EUNSUPPORTED, "linear_decode: y must be 16-byte aligned for this shape");
-  static bool attr[3] = {false, false, false};
-  const void *fn = nin ? reinterpret_cast<const void *>(lin::linear_kernel<true, 4>)
-                 : RT == 4 ? reinterpret_cast<const void *>(lin::linear_kernel<false, 4>)
-                           : reinterpret_cast<const void *>(lin::linear_kernel<false, 2>);
-  const int ai = nin ? 1 : RT == 4 ? 0 : 2;
-  if (!attr[ai]) {
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lin::kLdsBytes) != hipSuccess)
-      return fail(SPK_EHIP, "linear_decode: cannot reserve %d bytes of LDS", lin::kLdsBytes);
-    attr[ai] = true;
-  }
   const NormIn none{};
-  if (nin) {
-    lin::linear_kernel<true, 4><<<MG * R, lin::kThreads, lin::kLdsBytes, s>>>(
-        nullptr, static_cast<const lin::v4u *>(w_packed), static_cast<const uint16_t *>(bias),
-        static_cast<uint16_t *>(y), M, N, K, MG, R, *nin);
-  } else if (RT == 4) {
-    lin::linear_kernel<false, 4><<<MG * R, lin::kThreads, lin::kLdsBytes, s>>>(
-        static_cast<const uint16_t *>(x), static_cast<const lin::v4u *>(w_packed),
-        static_cast<const uint16_t *>(bias), static_cast<uint16_t *>(y), M, N, K, MG, R, none);
-  } else {
-    const int lds = std::max(rows * K * 2, lin::stage_off<2>() + lin::kWaves * lin::kStageBytes);
-    lin::linear_kernel<false, 2><<<MG * R, lin::kThreads, lds, s>>>(
-        static_cast<const uint16_t *>(x), static_cast<const lin::v4u *>(w_packed),
-        static_cast<const uint16_t *>(bias), static_cast<uint16_t *>(y), M, N, K, MG, R, none);
-  }
-  return check_launch("linear_decode");
+  const lin::v4u *wp = static_cast<const lin::v4u *>(w_packed);
+  const uint16_t *xb = static_cast<const uint16_t *>(x), *bb = static_cast<const uint16_t *>(bias);
+  uint16_t *yb = static_cast<uint16_t *>(y);
+  // Each launch takes the LDS it needs; the attribute (set once per kernel,
+  // index k) lets any of them take all 160 KB.
+  static bool attr[4] = {false, false, false, false};
+  auto go = [&](auto kernel, int k, int lds, const NormIn &ni) -> int {
+    if (!attr[k]) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              lin::kLdsBytes) != hipSuccess)
+        return fail(SPK_EHIP, "linear_decode: cannot reserve %d bytes of LDS", lin::kLdsBytes);
+      attr[k] = true;
+    }
+    kernel<<<MG * R, lin::kThreads, lds, s>>>(xb, wp, bb, yb, M, N, K, MG, R, ni);
+    return check_launch("linear_decode");
+  };
+  if (nin) return go(lin::linear_kernel<true, 4, 2>, 0, lin::kLdsBytes, *nin);
+  if (RT == 4) return go(lin::linear_kernel<false, 4, 2>, 1, lin::kLdsBytes, none);
+  const int x_bytes = rows * K * 2;
+  if (MU == 2)
+    return go(lin::linear_kernel<false, 2, 2>, 2,
+              std::max(x_bytes, lin::stage_off<2, 2>() + lin::kWaves * lin::kStageBytes), none);
+  return go(lin::linear_kernel<false, 2, 3>, 3, std::max(x_bytes, lin::stage_off<2, 3>() + lin::kWaves * lin::kStageBytes),
+            none);
 }
 
 extern "C" int spk_linear_decode(const void *x, const void *w_packed, const void *bias, void *y,

@@ -218,9 +218,10 @@ def test_model_fused_attention_is_identical(gpu):
                              block_tables=tables.to(gpu), seq_lens=lens.to(torch.int32).to(gpu))
     ids = torch.randint(0, 1024, (n,), generator=g).to(gpu)
     caches = [PagedSpikeCache(2, m.T, m.Hkv, m.D, 65, bs, device=gpu) for _ in range(2)]
+    gc = torch.Generator(device=gpu).manual_seed(21)  # the test's own stream: order-independent
     for c in caches:
         for k, v in c.layers:
-            k.random_(-2**31, 2**31 - 1)
+            k.random_(-2**31, 2**31 - 1, generator=gc)
         for (k0, v0), (k1, v1) in zip(caches[0].layers, caches[1].layers):
             k1.copy_(k0)
             v1.copy_(v0)
@@ -298,7 +299,8 @@ def test_mlp_gate_lif_unsupported_shapes_return_none(gpu):
                                          (128, 896, 4864, False), (44, 896, 4864, False),
                                          (4, 896, 4864, False), (256, 896, 4864, False),
                                          (20, 64, 2048, False), (64, 16384, 1280, False),
-                                         (64, 16384, 1152, True), (33, 20480, 512, False)])
+                                         (64, 16384, 1152, True), (33, 20480, 512, False),
+                                         (32, 512, 1280, True), (100, 1152, 896, False)])
 def test_linear_decode_within_one_ulp(gpu, M, N, K, bias):
     """Small-M linear against the fp64 product rounded to bf16: every output
     within 1 bf16 ulp (fp32 sums in a different order may round the other
@@ -370,9 +372,14 @@ def test_model_fused_mlp_matches_two_launches(gpu):
                              block_tables=tables.to(gpu), seq_lens=lens.to(torch.int32).to(gpu))
     ids = torch.randint(0, 1024, (n,), generator=g).to(gpu)
     caches = [PagedSpikeCache(2, m.T, m.Hkv, m.D, 65, bs, device=gpu) for _ in range(2)]
+    # The cache words come from the test's own generator, so the result does not
+    # depend on what earlier tests drew from the global one (the fused/unfused
+    # gap is rounding amplified by spike flips, and varies with the data:
+    # 0.001-0.037 over ten seeds).
+    gc = torch.Generator(device=gpu).manual_seed(0)
     for (k0, v0), (k1, v1) in zip(caches[0].layers, caches[1].layers):
-        k0.random_(-2**31, 2**31 - 1)
-        v0.random_(-2**31, 2**31 - 1)
+        k0.random_(-2**31, 2**31 - 1, generator=gc)
+        v0.random_(-2**31, 2**31 - 1, generator=gc)
         k1.copy_(k0)
         v1.copy_(v0)
     outs = []
