@@ -509,6 +509,49 @@ def test_model_matches_reference_forward(gpu):
     _compare(got, want, cache, ref, m)
 
 
+def test_incremental_decode_matches_whole_prefill(gpu):
+    """Prefill of P + K tokens in one chunk against a prefill of P then K
+    single-token decode steps (reference: tests/test_kv_cache.py:87-126,
+    incremental decode vs full-prefix recompute).  The decode steps run the
+    decode kernels (fused attention, small-M GEMMs, fused MLP), the chunk the
+    prefill path (library GEMMs, SDPA on the dense spikes), so the two round
+    differently and a spike on its threshold may flip: the last token's hidden
+    state and the caches are held to the model tests' bounds, and the next
+    token must agree."""
+    m = _small_model(gpu, seed=4)
+    bs, P, K = 16, 13, 5
+    g = torch.Generator().manual_seed(6)
+    prompts = [torch.randint(0, 1024, (P + K,), generator=g).tolist() for _ in range(2)]
+    tables = [[3, 8, 1], [0, 6, 9]]
+    whole = PagedSpikeCache(2, m.T, m.Hkv, m.D, 12, bs, device=gpu)
+    steps = PagedSpikeCache(2, m.T, m.Hkv, m.D, 12, bs, device=gpu)
+
+    ids, pos, meta = _prefill_meta(prompts, tables, bs, gpu)
+    h_all = m.forward_paged(ids, pos, whole.layers, meta)
+    want = h_all[torch.tensor([P + K - 1, 2 * (P + K) - 1], device=gpu)]
+
+    ids, pos, meta = _prefill_meta([p[:P] for p in prompts], tables, bs, gpu)
+    m.forward_paged(ids, pos, steps.layers, meta)
+    for i in range(P, P + K):
+        meta_d = AttentionMetadata(
+            slot_mapping=torch.tensor(slot_mapping(tables[0], i, 1, bs) + slot_mapping(tables[1], i, 1, bs),
+                                      device=gpu),
+            block_size=bs, num_decode_tokens=2,
+            block_tables=torch.tensor(tables, dtype=torch.int32, device=gpu),
+            seq_lens=torch.tensor([i + 1, i + 1], dtype=torch.int32, device=gpu))
+        got = m.forward_paged(torch.tensor([prompts[0][i], prompts[1][i]], device=gpu),
+                              torch.tensor([i, i], device=gpu), steps.layers, meta_d)
+    torch.cuda.synchronize()
+    rel = float((got.float() - want.float()).abs().max() / want.float().abs().max())
+    assert rel < 0.05, f"hidden rel err {rel}"
+    assert torch.equal(m.compute_logits(got).argmax(-1), m.compute_logits(want).argmax(-1))
+    for (kc, vc), (kr, vr) in zip(steps.layers, whole.layers):
+        for a, b in ((kc, kr), (vc, vr)):
+            diff = (a ^ b).view(torch.uint8)
+            bits = sum(int(((diff >> i) & 1).sum()) for i in range(8))
+            assert bits <= 1e-3 * a.numel() * 32, f"{bits} cache bits differ"
+
+
 def _compare(got, want, cache, ref, m):
     assert got.shape == want.shape and got.dtype == want.dtype
     scale = want.float().abs().max()
