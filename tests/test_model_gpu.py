@@ -552,6 +552,44 @@ def test_incremental_decode_matches_whole_prefill(gpu):
             assert bits <= 1e-3 * a.numel() * 32, f"{bits} cache bits differ"
 
 
+def test_chunked_prefill_matches_whole_prefill(gpu):
+    """A 60-token prompt prefilled in one chunk against chunks of 16 tokens,
+    each attending to the cached prefix through the packed cache (reference:
+    tests/test_engine.py:117-130, "a prompt split across steps must land in the
+    same cache state").  Layer 0's cache depends only on the embedding, a norm
+    and a row-independent GEMM: it must be identical.  Deeper layers see
+    attention summed over other sequence lengths (SDPA over the chunk and its
+    gathered prefix), which rounds differently, and the MLP gate's LIF turns
+    such differences into a few flipped spikes (measured: 0.9-1.2 % of the
+    bits written at layer 1 over three seeds and chunkings, 0.03 % with one
+    59-token chunk).  So deeper layers are held to 2 % of the bits written, the
+    last hidden state to a loose relative bound, and the next token must agree."""
+    m = _small_model(gpu, seed=8)
+    bs, L, C = 16, 60, 16
+    prompt = torch.randint(0, 1024, (L,), generator=torch.Generator().manual_seed(9)).tolist()
+    table = [7, 2, 11, 4]
+    whole = PagedSpikeCache(2, m.T, m.Hkv, m.D, 12, bs, device=gpu)
+    chunked = PagedSpikeCache(2, m.T, m.Hkv, m.D, 12, bs, device=gpu)
+    ids, pos, meta = _prefill_meta([prompt], [table], bs, gpu)
+    want = m.forward_paged(ids, pos, whole.layers, meta)[-1:]
+    for c in range(0, L, C):
+        ids, pos, meta = _prefill_meta([prompt[c:c + C]], [table], bs, gpu, ctx=[c])
+        got = m.forward_paged(ids, pos, chunked.layers, meta)[-1:]
+    torch.cuda.synchronize()
+    rel = float((got.float() - want.float()).abs().max() / want.float().abs().max())
+    assert rel < 0.2, f"hidden rel err {rel}"
+    assert torch.equal(m.compute_logits(got).argmax(-1), m.compute_logits(want).argmax(-1))
+    written = L * m.T * m.Hkv * m.D  # bits of the prompt's tokens in one layer's k (or v) cache
+    for layer, ((kc, vc), (kr, vr)) in enumerate(zip(chunked.layers, whole.layers)):
+        for a, b in ((kc, kr), (vc, vr)):
+            if layer == 0:
+                assert torch.equal(a, b)
+                continue
+            diff = (a ^ b).view(torch.uint8)
+            bits = sum(int(((diff >> i) & 1).sum()) for i in range(8))
+            assert bits <= 0.02 * written, f"layer {layer}: {bits} of {written} cache bits differ"
+
+
 def _compare(got, want, cache, ref, m):
     assert got.shape == want.shape and got.dtype == want.dtype
     scale = want.float().abs().max()
