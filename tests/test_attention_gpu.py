@@ -181,6 +181,17 @@ def test_planned_short_contexts_pair_mode(T, q_heads, kv_heads, bs, gpu):
     _check(_run(case, gpu), oracle_attn(case), f"planned short T={T} H={q_heads}/{kv_heads} bs={bs}")
 
 
+@pytest.mark.parametrize("bs", [256, 512, 1024])
+def test_planned_large_blocks(bs, gpu):
+    """Planned launches (tables of >= 3072 tokens) with blocks as long as a
+    step's token stride (256: the per-step slot moves by whole blocks) and
+    longer (512, 1024: the general slot form), short and long items."""
+    lens = [5000, 0, 17, 4100, 9000, 300, 1, 2048]
+    case = attn_case(lens, block_size=bs, T=2, q_heads=14, kv_heads=2, density=0.2, q_density=0.2,
+                     seed=bs, compact=True)
+    _check(_run(case, gpu), oracle_attn(case), f"planned bs={bs}")
+
+
 @pytest.mark.parametrize("lens,T,q_heads,kv_heads", [
     ([0, 3500, 0, 17, 4096, 1], 4, 14, 2),     # planned, all items short: pairs, grid of ceil(ups/2)
     ([0, 3500, 0, 17, 4096, 1], 3, 7, 1),      # odd T * Hkv: the last pair half empty
